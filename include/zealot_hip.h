@@ -1,0 +1,290 @@
+/* zealot_hip.h — C ABI of libzealot_hip.so, the MI355X (gfx950) PPO learning
+ * hot path for zealot-rl.
+ *
+ * Plain C: opaque handles, raw device pointers, sizes and status codes; no
+ * exceptions cross this boundary. Every compute entry point is enqueued on
+ * the context's single HIP stream and is asynchronous unless it says
+ * otherwise; ordering between calls is stream (issue) order, as with the
+ * cuTile adapter it replaces (src/biped/cutile_gemm.rs:15-27).
+ *
+ * Device buffers passed in are BORROWED: the library never frees them
+ * (same contract as CutileGemm's zero-copy views, src/biped/cutile_gemm.rs:
+ * 23-27,404-411). Buffers from zl_alloc are freed with zl_free.
+ *
+ * Matrices are fp32, row-major. Unless stated otherwise a matrix argument
+ * has the dense row stride of its logical shape; `ld_*` arguments give an
+ * explicit row stride in elements.
+ *
+ * Threading: one context per host thread (the reference adapter is !Sync,
+ * src/biped/cutile_gemm.rs:353-361).
+ */
+#ifndef ZEALOT_HIP_H
+#define ZEALOT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int zl_status;
+#define ZL_OK 0
+#define ZL_ERR_INVALID 1        /* bad argument (shape, null pointer, range) */
+#define ZL_ERR_HIP 2            /* a HIP runtime call failed */
+#define ZL_ERR_CODE_OBJECT 3    /* zealot_kernels.hsaco missing or unloadable */
+#define ZL_ERR_SELF_TEST 4      /* zl_init's numeric self-test failed */
+
+typedef struct zl_ctx zl_ctx;
+typedef struct zl_mlp zl_mlp;
+typedef struct zl_ppo zl_ppo;
+
+/* ------------------------------------------------------------ context ---- */
+
+/* Create a context on `device`: one HIP stream, the gfx950 code object loaded
+ * with hipModuleLoad, then a numeric self-test against a host fp64 reference
+ * (the cases of CutileGemm::self_test, src/biped/cutile_gemm.rs:695-828, at
+ * an fp32 tolerance). A non-zero status means "use the fallback path"
+ * (CutileGemm::init returning None, src/biped/cutile_gemm.rs:368-424); *out
+ * is NULL then and zl_global_error() says why. Setting ZL_FORCE_SELF_TEST_FAIL=1
+ * forces the self-test failure branch. */
+zl_status zl_init(int device, zl_ctx** out);
+void zl_destroy(zl_ctx* ctx);
+/* Last error of a call on ctx ("" if none). */
+const char* zl_last_error(const zl_ctx* ctx);
+/* Error of the last failed zl_init in this process (ctx does not exist). */
+const char* zl_global_error(void);
+/* The context's hipStream_t, for interop with other HIP code. */
+void* zl_stream(zl_ctx* ctx);
+/* Worst relative error of the init self-test. */
+double zl_self_test_error(const zl_ctx* ctx);
+/* Block the host until all work enqueued on ctx has finished. */
+zl_status zl_synchronize(zl_ctx* ctx);
+/* Version string of the library. */
+const char* zl_version(void);
+/* Per-launch timing of one kernel of the code object (by its symbol name,
+ * e.g. "zk_gemm_am_bn_64x128"): every launch of it on ctx is bracketed by
+ * hipEvents on the context stream until zl_timing_end, which returns the summed
+ * kernel time and the launch count. While timing is on, composite entry
+ * points launch eagerly instead of replaying their captured graphs. The
+ * tracing counterpart of the reference's KHAL_CUDA_PROFILE per-kernel timer
+ * (src/bin/iter_e2e_bench.rs:731-735,833-835). */
+zl_status zl_timing_begin(zl_ctx* ctx, const char* kernel_name);
+zl_status zl_timing_end(zl_ctx* ctx, double* total_ms, long long* launches);
+/* sizeof(zl_ppo_config), sizeof(zl_batch), sizeof(zl_ppo_stats) as compiled
+ * into the library, for binding generators to check their struct layouts. */
+void zl_abi_struct_sizes(size_t out[3]);
+
+/* ------------------------------------------------------------ buffers ---- */
+
+zl_status zl_alloc(zl_ctx* ctx, size_t bytes, void** dev_out);
+zl_status zl_free(zl_ctx* ctx, void* dev);
+/* Synchronous host <-> device copies on the context stream. */
+zl_status zl_upload(zl_ctx* ctx, void* dev_dst, const void* host_src, size_t bytes);
+zl_status zl_download(zl_ctx* ctx, void* host_dst, const void* dev_src, size_t bytes);
+zl_status zl_copy_d2d(zl_ctx* ctx, void* dev_dst, const void* dev_src, size_t bytes);
+
+/* -------------------------------------- operators (cuTile adapter) ---- */
+
+/* out(m x n) = lhs(m x k) . rhs(k x n). lhs_t: the buffer holds the row-major
+ * (k x m) base of lhs; rhs_t: it holds the (n x k) base of rhs. Split-K with a
+ * deterministic fixed-order second pass for deep-K, small-output shapes.
+ * Replaces CutileGemm::gemm (src/biped/cutile_gemm.rs:477-570). */
+zl_status zl_gemm(zl_ctx* ctx, float* out, const float* lhs, int lhs_t, const float* rhs,
+                  int rhs_t, int m, int n, int k);
+
+/* out(m x n) = act(lhs(m x k) . rhs(k x n) + bias), bias a column vector read
+ * at bias[r * bias_row_stride], act = ELU when elu != 0.
+ * Replaces CutileGemm::gemm_bias_act (src/biped/cutile_gemm.rs:578-625). */
+zl_status zl_gemm_bias_act(zl_ctx* ctx, float* out, const float* lhs, const float* rhs, int m,
+                           int n, int k, const float* bias, int bias_row_stride, int elu);
+
+/* In place g(m x n) *= (y > 0 ? 1 : y + 1), y the post-activation.
+ * Replaces CutileGemm::elu_backward (src/biped/cutile_gemm.rs:629-656). */
+zl_status zl_elu_backward(zl_ctx* ctx, float* g, const float* y, int m, int n);
+
+/* out(m) = row sums of x(m x n). Replaces CutileGemm::row_sum
+ * (src/biped/cutile_gemm.rs:659-690). */
+zl_status zl_row_sum(zl_ctx* ctx, float* out, const float* x, int m, int n);
+
+/* ------------------------------------- operators (vortx kernels) ---- */
+
+/* Actor half of the PPO loss for `rows` samples, batch-major:
+ * d_mean(rows x A) = dL/dmean, d_log_std[A] = summed dL/dlog_std (with the
+ * entropy term), stats_dev[2] = {sum of scaled surrogate, sum of scaled
+ * mean-only KL} (mean_old may be NULL: KL = 0). Semantics of
+ * zealot-rl/src/ppo.rs:411-432,452; replaces vortx Ppo::actor_grad + the dls
+ * row_sum (src/bin/biped_train_gpu.rs:1257-1271,1350-1357). All pointers are
+ * device pointers. */
+zl_status zl_ppo_actor_grad(zl_ctx* ctx, const float* mean, int ld_mean, const float* action,
+                            int ld_action, const float* log_std, const float* adv,
+                            const float* logp_old, const float* mean_old, int ld_mean_old,
+                            int rows, int action_dim, float clip, float entropy_coef,
+                            float scale, float* d_mean, int ld_d_mean, float* d_log_std,
+                            float* stats_dev);
+
+/* Critic half: d_v[r] = value_coef * dv * scale with the clipped value loss
+ * (zealot-rl/src/ppo.rs:436-450); stats_dev[1] = sum of scaled value loss.
+ * Replaces vortx Ppo::value_grad (src/bin/biped_train_gpu.rs:1332-1343). */
+zl_status zl_ppo_value_grad(zl_ctx* ctx, const float* v, const float* value_old,
+                            const float* ret, int rows, float clip, float value_coef,
+                            float scale, float* d_v, float* stats_dev);
+
+/* One Adam step over n elements: the element update of
+ * zealot-rl/src/net.rs:240-245 with caller-supplied bias corrections
+ * (vortx Adam::step with AdamParams, src/bin/biped_train_gpu.rs:1168-1182). */
+zl_status zl_adam_step(zl_ctx* ctx, float* p, const float* g, float* m, float* v, size_t n,
+                       float lr, float beta1, float beta2, float eps, float bc1, float bc2);
+
+/* out_dev[0] = sum of squares of x[0..n) (deterministic two-pass).
+ * Replaces vortx Reduce::SqNorm (src/bin/biped_train_gpu.rs:1377-1397). */
+zl_status zl_grad_sqnorm(zl_ctx* ctx, const float* x, size_t n, float* out_dev);
+
+/* GAE(lambda) for N independent trajectories of length T, one lane per env
+ * (zealot-rl/src/ppo.rs:681-703, run per env by
+ * src/bin/biped_train_gpu.rs:974-981). Element (t, e) of rewards / values /
+ * dones is at t*in_ts + e*in_es, of adv / ret at t*out_ts + e*out_es;
+ * last_values[e] bootstraps the final step; dones are 0/1 bytes. */
+zl_status zl_gae(zl_ctx* ctx, const float* rewards, const float* values, const uint8_t* dones,
+                 const float* last_values, int T, int N, long long in_ts, long long in_es,
+                 long long out_ts, long long out_es, float gamma, float lam, float* adv,
+                 float* ret);
+
+/* In place (adv - mean) / max(sqrt(population var), 1e-6)
+ * (zealot-rl/src/ppo.rs:343-348, src/bin/biped_train_gpu.rs:1010-1016). */
+zl_status zl_adv_normalize(zl_ctx* ctx, float* adv, size_t n);
+
+/* action = mean + exp(log_std) * eps, logp = Gaussian log-prob of action
+ * (ActorCritic::sample / logp, zealot-rl/src/ppo.rs:297-323; the host loop of
+ * src/bin/biped_train_gpu.rs:910-930), eps supplied by the caller. */
+zl_status zl_sample_actions(zl_ctx* ctx, const float* mean, int ld_mean, const float* log_std,
+                            const float* eps, int rows, int action_dim, float* action,
+                            float* logp);
+
+/* ------------------------------------------------ GpuMlp equivalent ---- */
+
+/* A dense ELU MLP (hidden ELU, linear output) with device-resident weights,
+ * Adam moments and activation buffers for up to `batch` rows: the GpuMlp of
+ * src/bin/biped_train_gpu.rs:316-564, batch-major ([rows x dim]). */
+zl_status zl_mlp_create(zl_ctx* ctx, const int* dims, int ndims, int batch, zl_mlp** out);
+void zl_mlp_destroy(zl_mlp* mlp);
+/* Number of parameters in the packed layout w[0], b[0], w[1], b[1], ... with
+ * w[l] row-major [dims[l+1] x dims[l]] (zealot-rl/src/net.rs:30-34). */
+long long zl_mlp_num_params(const zl_mlp* mlp);
+/* Host packed params <-> device (GpuMlp::write_w / read_into, :541-563). */
+zl_status zl_mlp_write_weights(zl_mlp* mlp, const float* packed_host);
+zl_status zl_mlp_read_weights(zl_mlp* mlp, float* packed_host);
+/* Forward over `rows` input rows (device x, row stride ldx): all layer
+ * activations stay resident for zl_mlp_backward (GpuMlp::forward, :364-422). */
+zl_status zl_mlp_forward(zl_mlp* mlp, const float* x, int ldx, int rows);
+/* Device pointer to the output activations [rows x dims[L]] and its stride. */
+const float* zl_mlp_output(const zl_mlp* mlp, int* ld_out);
+/* Backward of dL/dout (device, row stride ld_g) through the last forward:
+ * weight/bias gradients summed over the rows (GpuMlp::backward, :423-500). */
+zl_status zl_mlp_backward(zl_mlp* mlp, const float* g_out, int ld_g);
+/* Download the gradients of the last backward, packed like the params. */
+zl_status zl_mlp_read_grads(zl_mlp* mlp, float* packed_host);
+/* Adam over all tensors with caller bias corrections (GpuMlp::adam, :501-538). */
+zl_status zl_mlp_adam(zl_mlp* mlp, float lr, float bc1, float bc2);
+/* Download / upload the Adam moments, packed like the params. */
+zl_status zl_mlp_read_moments(zl_mlp* mlp, float* m_host, float* v_host);
+zl_status zl_mlp_write_moments(zl_mlp* mlp, const float* m_host, const float* v_host);
+
+/* ----------------------------------------------- the PPO update ---- */
+
+#define ZL_SEMANTICS_ACTOR_CRITIC 0 /* ActorCritic::update, zealot-rl/src/ppo.rs:338-510 */
+#define ZL_SEMANTICS_GPU_TRAINER 1  /* src/bin/biped_train_gpu.rs:1164-1553 */
+
+typedef struct zl_ppo_config {
+  int semantics;       /* ZL_SEMANTICS_* */
+  float clip;          /* surrogate and value clip (PpoConfig::clip) */
+  float entropy_coef;
+  float value_coef;
+  int epochs;
+  int minibatches;
+  /* ACTOR_CRITIC: MlpGrad::clip per net (log_std unclipped).
+   * GPU_TRAINER: global norm over actor + critic + log_std, <= 0 disables. */
+  float max_grad_norm;
+  float desired_kl;
+  float lr_min, lr_max;
+  int adaptive_lr;     /* per minibatch (ACTOR_CRITIC) or per epoch (GPU_TRAINER) */
+  int early_stop;      /* GPU_TRAINER: stop epochs once KL > 5 * desired_kl */
+  int shuffle;         /* ACTOR_CRITIC: per-epoch Fisher-Yates (ppo.rs:357-363); else contiguous */
+  int normalize_adv;   /* normalise advantages in place first */
+  int clamp_log_std;   /* ACTOR_CRITIC: [-1.6, 1.0] each step; GPU_TRAINER: [-1.6, 0.0] after */
+} zl_ppo_config;
+
+/* One rollout batch, structure of arrays, all DEVICE pointers, n samples in
+ * batch order (sample i = row i). obs and critic_obs are the already
+ * normalised observations (the trainer stages normalised obs,
+ * src/bin/biped_train_gpu.rs:1021-1030). */
+typedef struct zl_batch {
+  long long n;
+  const float* obs;        int ld_obs;       /* [n x actor_dims[0]] */
+  const float* critic_obs; int ld_critic_obs;/* [n x critic_dims[0]] (may alias obs) */
+  const float* action;     int ld_action;    /* [n x A] */
+  const float* mean_old;   int ld_mean_old;  /* [n x A] rollout means (KL), may be NULL */
+  const float* logp_old;                     /* [n] */
+  const float* value_old;                    /* [n] */
+  float* adv;                                /* [n], normalised in place if requested */
+  const float* ret;                          /* [n] */
+} zl_batch;
+
+/* PpoStats (zealot-rl/src/ppo.rs:90-102) plus the trainer's epoch count. */
+typedef struct zl_ppo_stats {
+  float kl, surrogate, value_loss, entropy, lr;
+  int epochs_run;
+  float last_kl;       /* GPU_TRAINER: last per-epoch full-Gaussian KL */
+  float grad_norm[3];  /* last pre-clip norms: actor, critic, log_std (global in [0]) */
+} zl_ppo_stats;
+
+/* Actor + critic + log_std and their Adam state resident in one flat HBM
+ * buffer; activation / gradient buffers sized for `minibatch_rows` rows. The
+ * ActorCritic of zealot-rl/src/ppo.rs:208-229 with the trainer's GpuMlp pair. */
+zl_status zl_ppo_create(zl_ctx* ctx, const int* actor_dims, int n_actor, const int* critic_dims,
+                        int n_critic, int minibatch_rows, zl_ppo** out);
+void zl_ppo_destroy(zl_ppo* ppo);
+/* Host packed params (as zl_mlp_write_weights) <-> device; lr is the current
+ * adaptive learning rate. zl_ppo_set_params resets nothing else. */
+zl_status zl_ppo_set_params(zl_ppo* ppo, const float* actor, const float* critic,
+                            const float* log_std, float lr);
+zl_status zl_ppo_get_params(zl_ppo* ppo, float* actor, float* critic, float* log_std, float* lr);
+/* Adam moments, packed (any pointer may be NULL). */
+zl_status zl_ppo_get_moments(zl_ppo* ppo, float* m_actor, float* v_actor, float* m_critic,
+                             float* v_critic, float* m_log_std, float* v_log_std);
+/* Zero the Adam moments and step counters (a freshly constructed ActorCritic). */
+zl_status zl_ppo_reset_optimizer(zl_ppo* ppo);
+/* Adam step count (ACTOR_CRITIC t) and trainer gstep. */
+zl_status zl_ppo_get_counters(zl_ppo* ppo, int* t, unsigned long long* gstep);
+/* The whole update: epochs x minibatches of actor + critic forward, PPO losses,
+ * backward, grad clip, Adam, adaptive LR, all on the device with no host
+ * round trip inside (captured once into a hipGraph and replayed). Blocks until
+ * done and fills *stats (ActorCritic::update, zealot-rl/src/ppo.rs:338-384, or
+ * src/bin/biped_train_gpu.rs:1164-1553 per config->semantics). */
+zl_status zl_ppo_update(zl_ppo* ppo, const zl_batch* batch, const zl_ppo_config* config,
+                        zl_ppo_stats* stats);
+/* Gradients of one minibatch without stepping: forward, PPO losses and
+ * backward over batch rows [row0, row0 + rows) (or rows perm_dev[row0 + r] when
+ * perm_dev, a device int array, is non-NULL), leaving the summed gradients in
+ * the flat gradient buffer (read them with zl_ppo_get_grads) and
+ * stats[3] = {surrogate, value_loss, kl} (host). The accumulation of
+ * zealot-rl/src/ppo.rs:406-462 before clip / Adam. Blocks until done. */
+zl_status zl_ppo_minibatch_grads(zl_ppo* ppo, const zl_batch* batch, const zl_ppo_config* config,
+                                 long long row0, int rows, const int* perm_dev, float* stats);
+/* Download the gradient buffer, packed like the params (any pointer may be NULL). */
+zl_status zl_ppo_get_grads(zl_ppo* ppo, float* actor, float* critic, float* log_std);
+/* Critic values for n rows of (normalised) critic obs, in minibatch-sized
+ * chunks: values[i] (ActorCritic::value, zealot-rl/src/ppo.rs:290-294). */
+zl_status zl_ppo_values(zl_ppo* ppo, const float* critic_obs, int ld, long long n,
+                        float* values);
+/* Actor means for n rows of (normalised) obs: mean[i * ld_mean + k]
+ * (ActorCritic::mean, zealot-rl/src/ppo.rs:282-287; GpuPolicy::forward,
+ * src/biped/gpu_policy.rs:210-248). */
+zl_status zl_ppo_actor_mean(zl_ppo* ppo, const float* obs, int ld, long long n, float* mean,
+                            int ld_mean);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ZEALOT_HIP_H */

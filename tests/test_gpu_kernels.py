@@ -1,0 +1,313 @@
+"""GPU parity of the operator-level entry points against the CPU oracle and
+fp64 closed forms. Tolerances: forward/backward 1e-4 relative to the tensor's
+max |value| (fp32); Adam and GAE bit-exact / 2 ulp (same operation order, no
+FP contraction, correctly rounded div/sqrt on both sides)."""
+
+import numpy as np
+import pytest
+
+from conftest import rel_amax, ulp_diff
+from oracle import zl_oracle as zo
+from zealot_amd import ops, synth
+from zealot_amd.rl import GpuMlp, packed_count
+
+pytestmark = pytest.mark.gpu
+
+FWD_BWD_TOL = 1e-4
+
+
+def st_val(r, c, seed, a=31, b=17, cst=101, p=97):
+    i = np.arange(r)[:, None]
+    j = np.arange(c)[None, :]
+    h = (i * a + j * b + seed * cst) % p
+    return (h.astype(np.float32) / np.float32(p / 2.0) - np.float32(1.0)).astype(np.float32)
+
+
+# (m, n, k, lhs_t, rhs_t) of CutileGemm::self_test (src/biped/cutile_gemm.rs:699-708)
+CUTILE_CASES = [
+    (12, 300, 45, False, False),
+    (45, 300, 256, True, False),
+    (256, 45, 300, False, True),
+    (64, 96, 4096, False, True),
+    (64, 96, 3072, False, True),
+    (512, 12288, 51, False, False),
+]
+
+
+def test_self_test_error_recorded(ctx):
+    print(f"[gpu] self-test worst rel err {ctx.self_test_error:.3e}", flush=True)
+    assert 0.0 <= ctx.self_test_error <= FWD_BWD_TOL
+
+
+@pytest.mark.parametrize("ci,case", list(enumerate(CUTILE_CASES)))
+def test_gemm_cutile_cases(ctx, ci, case):
+    m, n, k, lt, rt = case
+    L = st_val(m, k, ci)
+    R = st_val(k, n, ci + 7)
+    ref = L.astype(np.float64) @ R.astype(np.float64)
+    dl = ctx.to_device(L.T.copy() if lt else L)
+    dr = ctx.to_device(R.T.copy() if rt else R)
+    out = ctx.alloc((m, n))
+    ops.gemm(ctx, out, dl, lt, dr, rt, m, n, k)
+    got = out.numpy()
+    err = rel_amax(got, ref)
+    print(f"[gpu] gemm case {ci} {case}: rel err {err:.2e}", flush=True)
+    assert err <= FWD_BWD_TOL
+
+
+@pytest.mark.parametrize("lt", [False, True])
+@pytest.mark.parametrize("rt", [False, True])
+@pytest.mark.parametrize("shape", [(1, 1, 1), (5, 7, 3), (33, 129, 17), (130, 70, 1000), (29, 123, 24576)])
+def test_gemm_layouts_ragged(ctx, lt, rt, shape):
+    m, n, k = shape
+    g = np.random.default_rng(m * 1000 + n * 10 + k)
+    L = g.standard_normal((m, k)).astype(np.float32)
+    R = g.standard_normal((k, n)).astype(np.float32)
+    ref = L.astype(np.float64) @ R.astype(np.float64)
+    dl = ctx.to_device(L.T.copy() if lt else L)
+    dr = ctx.to_device(R.T.copy() if rt else R)
+    out = ctx.alloc((m, n))
+    ops.gemm(ctx, out, dl, lt, dr, rt, m, n, k)
+    err = rel_amax(out.numpy(), ref)
+    assert err <= FWD_BWD_TOL, (shape, lt, rt, err)
+
+
+def test_gemm_bias_elu_backward_rowsum(ctx):
+    # src/biped/cutile_gemm.rs:749-826: strided bias column (stride 8), ELU, backward, row sums.
+    m, n, k = 100, 300, 45
+    f = lambda r, c, s: st_val(r, c, s, 29, 13, 89, 83)  # noqa: E731
+    L, R, Bb, G = f(m, k, 1), f(k, n, 2), f(m, 8, 3), f(m, n, 4)
+    z = L.astype(np.float64) @ R.astype(np.float64) + Bb[:, :1].astype(np.float64)
+    ref = np.where(z > 0, z, np.expm1(z))
+    dl, dr, db, dg = ctx.to_device(L), ctx.to_device(R), ctx.to_device(Bb), ctx.to_device(G)
+    out = ctx.alloc((m, n))
+    ops.gemm_bias_act(ctx, out, dl, dr, m, n, k, db, 8, True)
+    y = out.numpy()
+    assert rel_amax(y, ref) <= FWD_BWD_TOL
+    ops.elu_backward(ctx, dg, out, m, n)
+    g2 = dg.numpy()
+    gref = G * np.where(y > 0, np.float32(1.0), y + np.float32(1.0))
+    assert np.array_equal(g2, gref.astype(np.float32))  # one f32 multiply: exact
+    rs = ctx.alloc(m)
+    ops.row_sum(ctx, rs, dg, m, n)
+    assert rel_amax(rs.numpy(), g2.astype(np.float64).sum(1)) <= FWD_BWD_TOL
+
+
+def test_config1_single_layer(ctx):
+    """X [4096 x 123] . W [123 x 512] + b, ELU (config 1) vs the oracle's Mlp::forward."""
+    c1 = synth.config1()
+    x, w_kn, b = c1["x"], c1["w_kn"], c1["b"]
+    # Oracle: the layer as the hidden layer of an Mlp [123, 512, 1] (ELU applied).
+    params = np.concatenate([w_kn.T.ravel(), b, np.zeros(513, np.float32)]).astype(np.float32)
+    ref = zo.mlp_forward([123, 512, 1], params, x)[0]
+    truth = x.astype(np.float64) @ w_kn.astype(np.float64) + b
+    truth = np.where(truth > 0, truth, np.expm1(truth))
+    # The reference's fused layer is feature-major (bias per row of out,
+    # src/bin/biped_train_gpu.rs:382-394): out^T [512 x 4096] = W^T . X^T + b.
+    dwt = ctx.to_device(w_kn.T.copy())
+    dxt = ctx.to_device(x.T.copy())
+    db = ctx.to_device(b)
+    out_t = ctx.alloc((512, 4096))
+    ops.gemm_bias_act(ctx, out_t, dwt, dxt, 512, 4096, 123, db, 1, True)
+    got = out_t.numpy().T
+    e_gpu, e_cpu = rel_amax(got, truth), rel_amax(ref, truth)
+    print(f"[gpu] config1: gpu vs f64 {e_gpu:.2e}, oracle vs f64 {e_cpu:.2e}, "
+          f"gpu vs oracle {rel_amax(got, ref):.2e}", flush=True)
+    assert rel_amax(got, ref) <= FWD_BWD_TOL
+
+
+def _mlp_case(ctx, dims, rows, seed, bias_bound=0.1):
+    g = np.random.default_rng(seed)
+    params = synth.kaiming_uniform_net(g, dims, bias_bound=bias_bound)
+    x = np.clip(g.standard_normal((rows, dims[0])), -5, 5).astype(np.float32)
+    mlp = GpuMlp(ctx, dims, rows)
+    mlp.write_weights(params)
+    assert np.array_equal(mlp.read_weights(), params)
+    dx = ctx.to_device(x)
+    mlp.forward(dx, rows)
+    return g, params, x, dx, mlp
+
+
+@pytest.mark.parametrize("dims,rows", [([4, 6, 5, 3], 7), ([123, 512, 256, 128, 29], 4096),
+                                       ([123, 512, 256, 128, 1], 1000), ([17, 33, 2], 300)])
+def test_mlp_forward_vs_oracle(ctx, dims, rows):
+    g, params, x, dx, mlp = _mlp_case(ctx, dims, rows, seed=rows)
+    got = mlp.output(rows)
+    ref = zo.mlp_forward(dims, params, x)[-1]
+    err = rel_amax(got, ref)
+    print(f"[gpu] mlp fwd {dims} x {rows}: rel err {err:.2e}", flush=True)
+    assert err <= FWD_BWD_TOL
+
+
+@pytest.mark.parametrize("dims,rows", [([4, 6, 5, 3], 7), ([123, 512, 256, 128, 29], 4096),
+                                       ([123, 512, 256, 128, 1], 2048), ([17, 33, 2], 300)])
+def test_mlp_backward_vs_oracle(ctx, dims, rows):
+    g, params, x, dx, mlp = _mlp_case(ctx, dims, rows, seed=rows + 1)
+    gout = (g.standard_normal((rows, dims[-1])) / rows).astype(np.float32)
+    mlp.backward(ctx.to_device(gout))
+    got = mlp.read_grads()
+    ref, _ = zo.mlp_backward(dims, params, x, gout)
+    # per-tensor amax-normalised error
+    o = 0
+    worst = 0.0
+    for l in range(len(dims) - 1):
+        for sz in (dims[l + 1] * dims[l], dims[l + 1]):
+            e = rel_amax(got[o:o + sz], ref[o:o + sz])
+            worst = max(worst, e)
+            o += sz
+    print(f"[gpu] mlp bwd {dims} x {rows}: worst per-tensor rel err {worst:.2e}", flush=True)
+    assert worst <= FWD_BWD_TOL
+
+
+def test_config3_adam_bit_exact(ctx):
+    """Adam over actor + critic + log_std (config 3): 10 warm steps then one
+    more, on identical gradients, vs net.rs:240-245 on the CPU. <= 2 ulp."""
+    na = packed_count(synth.ACTOR_DIMS)
+    nc = packed_count(synth.CRITIC_DIMS)
+    c3 = synth.config3(na, nc)
+    p = np.concatenate([c3["actor"], c3["critic"], c3["log_std"]]).astype(np.float32)
+    n = p.size
+    dp, dm, dv = ctx.to_device(p), ctx.to_device(np.zeros(n, np.float32)), ctx.to_device(np.zeros(n, np.float32))
+    hp, hm, hv = p.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    for t, gr in enumerate(c3["grads"], start=1):
+        bc1 = np.float32(1.0) - np.float32(zo.powi(0.9, t))
+        bc2 = np.float32(1.0) - np.float32(zo.powi(0.999, t))
+        dg = ctx.to_device(gr)
+        ops.adam_step(ctx, dp, dg, dm, dv, n, 1e-3, float(bc1), float(bc2))
+        hp, hm, hv = zo.adam_flat(hp, gr, hm, hv, 1e-3, float(bc1), float(bc2))
+    up, um, uv = ulp_diff(dp.numpy(), hp), ulp_diff(dm.numpy(), hm), ulp_diff(dv.numpy(), hv)
+    print(f"[gpu] adam 11 steps over {n} params: max ulp p={up} m={um} v={uv}", flush=True)
+    assert up <= 2 and um <= 2 and uv <= 2
+
+
+def test_grad_sqnorm(ctx):
+    g = np.random.default_rng(3).standard_normal(459_323).astype(np.float32) * 1e-2
+    d = ctx.to_device(g)
+    out = ctx.alloc(1)
+    ops.grad_sqnorm(ctx, d, g.size, out)
+    ref = float(np.sum(g.astype(np.float64) ** 2))
+    assert abs(out.numpy()[0] - ref) / ref < 1e-5
+
+
+def _gae_f64(r, v, d, last_v, gamma, lam):
+    """Closed form: adv_t = sum_k (gamma*lam)^k delta_{t+k}, cut at dones."""
+    T = len(r)
+    adv = np.zeros(T)
+    for t in range(T):
+        acc, coef = 0.0, 1.0
+        for k in range(t, T):
+            nv = last_v if k == T - 1 else v[k + 1]
+            nt = 0.0 if d[k] else 1.0
+            acc += coef * (r[k] + gamma * nv * nt - v[k])
+            if d[k]:
+                break
+            coef *= gamma * lam
+        adv[t] = acc
+    return adv, adv + np.asarray(v, np.float64)
+
+
+@pytest.mark.parametrize("T,N", [(1, 1), (2, 3), (24, 4096), (37, 100)])
+def test_gae_bit_exact(ctx, T, N):
+    g = np.random.default_rng(T * 7 + N)
+    r = g.standard_normal((T, N)).astype(np.float32)
+    v = g.standard_normal((T, N)).astype(np.float32)
+    d = (g.random((T, N)) < 0.05).astype(np.uint8)
+    lv = g.standard_normal(N).astype(np.float32)
+    dr, dvv, dd, dl = ctx.to_device(r), ctx.to_device(v), ctx.to_device(d), ctx.to_device(lv)
+    adv, ret = ctx.alloc((T, N)), ctx.alloc((T, N))
+    ops.gae(ctx, dr, dvv, dd, dl, T, N, adv, ret, 0.99, 0.95)
+    ga, gr = adv.numpy(), ret.numpy()
+    for e in range(min(N, 64)):
+        ra, rr = zo.gae(r[:, e], v[:, e], d[:, e], float(lv[e]), 0.99, 0.95)
+        assert np.array_equal(ga[:, e], ra) and np.array_equal(gr[:, e], rr), e
+        fa, fr = _gae_f64(r[:, e], v[:, e], d[:, e], float(lv[e]), 0.99, 0.95)
+        assert np.allclose(ga[:, e], fa, rtol=1e-4, atol=1e-4)
+
+
+def test_gae_env_major_output(ctx):
+    """Output strides: write adv/ret in env-major sample order (e*T + t)."""
+    T, N = 24, 257
+    g = np.random.default_rng(11)
+    r = g.standard_normal((T, N)).astype(np.float32)
+    v = g.standard_normal((T, N)).astype(np.float32)
+    d = (g.random((T, N)) < 0.02).astype(np.uint8)
+    lv = g.standard_normal(N).astype(np.float32)
+    adv, ret = ctx.alloc(T * N), ctx.alloc(T * N)
+    ops.gae(ctx, ctx.to_device(r), ctx.to_device(v), ctx.to_device(d), ctx.to_device(lv), T, N, adv, ret,
+            0.99, 0.95, in_strides=(N, 1), out_strides=(1, T))
+    ga = adv.numpy().reshape(N, T)
+    for e in range(N):
+        ra, _ = zo.gae(r[:, e], v[:, e], d[:, e], float(lv[e]), 0.99, 0.95)
+        assert np.array_equal(ga[e], ra)
+
+
+def test_adv_normalize(ctx):
+    a = np.random.default_rng(5).standard_normal(98_304).astype(np.float32) * 3 + 1
+    d = ctx.to_device(a)
+    ops.adv_normalize(ctx, d, a.size)
+    got = d.numpy()
+    ref = zo.adv_normalize(a)
+    truth = (a - a.astype(np.float64).mean()) / a.astype(np.float64).std()
+    assert rel_amax(got, ref) < 1e-5 and rel_amax(got, truth) < 1e-5
+    assert abs(float(got.astype(np.float64).mean())) < 1e-5
+    # constant input: sd floored at 1e-6 -> all zeros, no NaN
+    d2 = ctx.to_device(np.full(1000, 2.5, np.float32))
+    ops.adv_normalize(ctx, d2, 1000)
+    assert np.all(d2.numpy() == 0.0)
+
+
+def test_actor_value_grad_ops(ctx):
+    """zl_ppo_actor_grad / zl_ppo_value_grad vs the oracle's per-sample fold
+    (through a 1-layer linear actor whose output is the mean itself)."""
+    rows, A = 777, 29
+    g = np.random.default_rng(21)
+    mean = g.standard_normal((rows, A)).astype(np.float32)
+    action = (mean + 0.6 * g.standard_normal((rows, A))).astype(np.float32)
+    log_std = np.full(A, -0.5, np.float32) + 0.1 * g.standard_normal(A).astype(np.float32)
+    adv = g.standard_normal(rows).astype(np.float32)
+    logp_old = (synth.gaussian_logp(action, mean, log_std) + 0.3 * g.standard_normal(rows)).astype(np.float32)
+    mean_old = (mean + 0.05 * g.standard_normal((rows, A))).astype(np.float32)
+    dm, ds_ = ctx.alloc((rows, A)), ctx.alloc(A)
+    stats = ctx.alloc(2)
+    ops.ppo_actor_grad(ctx, ctx.to_device(mean), ctx.to_device(action), ctx.to_device(log_std),
+                       ctx.to_device(adv), ctx.to_device(logp_old), ctx.to_device(mean_old), rows, A,
+                       0.2, 0.005, 1.0 / rows, dm, ds_, stats)
+    # oracle: identity actor (dims [A, A], W = I, b = 0) so dL/dmean = g_out.
+    ad = [A, A]
+    eye = np.concatenate([np.eye(A, dtype=np.float32).ravel(), np.zeros(A, np.float32)])
+    cd = [1, 1]
+    crit = np.array([1.0, 0.0], np.float32)  # v = obs
+    v = g.standard_normal(rows).astype(np.float32)
+    vold = (v + 0.3 * g.standard_normal(rows)).astype(np.float32)
+    ret = g.standard_normal(rows).astype(np.float32)
+    batch = dict(obs=mean, critic_obs=v[:, None].copy(), action=action, mean_old=mean_old,
+                 logp_old=logp_old, value_old=vold, adv=adv, ret=ret)
+    ga, gc, gl, st = zo.minibatch_grads(ad, cd, eye, crit, log_std, batch, np.arange(rows), 0.2, 0.005, 1.0)
+    # dW of the identity layer = sum_r dmean[r,k] * mean[r,i] -> compare via db = sum_r dmean
+    db_ref = ga[A * A:]
+    assert rel_amax(dm.numpy().astype(np.float64).sum(0), db_ref) <= FWD_BWD_TOL
+    assert rel_amax(ds_.numpy(), gl) <= FWD_BWD_TOL
+    s = stats.numpy()
+    assert abs(s[0] - st[0]) <= 1e-4 * max(1.0, abs(st[0]))
+    assert abs(s[1] - st[2]) <= 1e-4 * max(1.0, abs(st[2]))
+    # value grad
+    dvv, vst = ctx.alloc(rows), ctx.alloc(1)
+    ops.ppo_value_grad(ctx, ctx.to_device(v), ctx.to_device(vold), ctx.to_device(ret), rows, 0.2, 1.0,
+                       1.0 / rows, dvv, vst)
+    # critic [1,1] with w=1,b=0: db = sum dv
+    assert rel_amax(dvv.numpy().astype(np.float64).sum(), gc[1]) <= FWD_BWD_TOL
+    assert abs(vst.numpy()[0] - st[1]) <= 1e-4 * max(1.0, abs(st[1]))
+
+
+def test_sample_actions(ctx):
+    c2 = synth.config2()
+    rows, A = 4096, 29
+    means = zo.mlp_forward(synth.ACTOR_DIMS, c2["actor"], c2["obs"])[-1]
+    act, lp = ctx.alloc((rows, A)), ctx.alloc(rows)
+    ops.sample_actions(ctx, ctx.to_device(means), ctx.to_device(c2["log_std"]), ctx.to_device(c2["eps"]),
+                       rows, A, act, lp)
+    std = np.exp(c2["log_std"]).astype(np.float32)
+    ref_a = (means + std * c2["eps"]).astype(np.float32)
+    assert rel_amax(act.numpy(), ref_a) < 1e-6
+    ref_lp = synth.gaussian_logp(ref_a, means, c2["log_std"])
+    assert rel_amax(lp.numpy(), ref_lp) < 1e-5

@@ -1,0 +1,437 @@
+"""CPU tests that pin the oracle (the C++ restatement of zealot-rl) before it
+is trusted as the GPU path's checker: the reference's own unit tests as
+known-answer tests (zealot-rl/src/{rng,net,ppo}.rs #[cfg(test)]), independent
+integer / float64 closed forms, finite differences, and the golden fixtures
+under tests/golden/."""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+import np_ref
+from conftest import rel_amax, ulp_diff
+from oracle import zl_oracle as zo
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+MASK64 = (1 << 64) - 1
+
+
+def lcg_units_int(seed, n):
+    """Independent restatement of rng.rs:21-27 in exact integer arithmetic."""
+    s = (seed | 1) & MASK64
+    out = np.empty(n, np.float32)
+    for i in range(n):
+        s = (s * 6364136223846793005 + 1442695040888963407) & MASK64
+        out[i] = np.float32((s >> 40) / float(1 << 24))  # 24-bit integer / 2^24: exact
+    return out
+
+
+# ------------------------------------------------------------------- rng.rs
+
+@pytest.mark.parametrize("seed", [0, 1, 7, 9, 123, 2024, 2**63 + 5])
+def test_lcg_unit_exact(seed):
+    assert np.array_equal(zo.lcg_units(seed, 2000), lcg_units_int(seed, 2000))
+
+
+def test_deterministic_unit():
+    # rng.rs:39-46
+    assert np.array_equal(zo.lcg_units(9, 100), zo.lcg_units(9, 100))
+
+
+def test_gauss_box_muller_pairing():
+    """gauss = sqrt(-2 ln max(u1, 1e-7)) * cos(tau * u2), u1 drawn first
+    (rng.rs:30-31). numpy's float32 log/cos are independent of glibc's, so
+    allow a few ulp; swapping u1/u2 would fail by orders of magnitude."""
+    u = lcg_units_int(2024, 4000).astype(np.float32)
+    u1, u2 = np.maximum(u[0::2], np.float32(1e-7)), u[1::2]
+    tau = np.float32(6.28318530717958647692)
+    want = (np.sqrt(np.float32(-2.0) * np.log(u1)) * np.cos(tau * u2)).astype(np.float32)
+    got = zo.lcg_gauss(2024, 2000)
+    assert ulp_diff(got, want) <= 8
+    swapped = (np.sqrt(np.float32(-2.0) * np.log(np.maximum(u2, np.float32(1e-7)))) * np.cos(tau * u[0::2])).astype(np.float32)
+    assert rel_amax(got, swapped) > 0.1
+
+
+def test_golden_lcg_stream():
+    with open(os.path.join(GOLDEN, "lcg_streams.json")) as f:
+        gold = json.load(f)
+    for case in gold["units"]:
+        got = zo.lcg_units(case["seed"], len(case["bits"])).view(np.uint32)
+        assert [int(x) for x in got] == case["bits"]
+
+
+@pytest.mark.parametrize("x", [0.9, 0.999])
+def test_powi_is_a_power(x):
+    """Rust powi via square-and-multiply: close to the correctly rounded x^t
+    (repeated squaring doubles the relative error per squaring, so allow
+    ~t ulp; an off-by-one exponent would be off by millions of ulp), and
+    exactly the plain product for t = 1, 2."""
+    xf = float(np.float32(x))
+    for t in range(1, 200):
+        got = np.float32(zo.powi(x, t))
+        exact = np.float32(xf ** t)
+        assert ulp_diff(got, exact) <= max(8, t), t
+    assert np.float32(zo.powi(x, 1)) == np.float32(x)
+    assert np.float32(zo.powi(x, 2)) == np.float32(np.float32(x) * np.float32(x))
+
+
+# ------------------------------------------------------------------- net.rs
+
+def test_elu_and_grad():
+    # net.rs:258-265
+    assert zo.lib().zlo_elu(2.0) == 2.0
+    assert abs(zo.lib().zlo_elu(0.0)) < 1e-9
+    assert abs(zo.lib().zlo_elu(-1.0) - (np.exp(np.float32(-1.0)) - 1.0)) < 1e-6
+    assert zo.lib().zlo_elu_grad_from_act(2.0) == 1.0
+    assert abs(zo.lib().zlo_elu_grad_from_act(zo.lib().zlo_elu(-1.0)) - np.exp(-1.0)) < 1e-6
+
+
+def test_mlp_init_is_scaled_gaussian():
+    """Mlp::new (net.rs:61-79): w = gauss * sqrt(1/fan_in) (x out_scale on the
+    last layer) drawn layer by layer from one Lcg; biases zero."""
+    dims = [4, 6, 5, 3]
+    p = zo.mlp_init(dims, 0.5, 123)
+    gs = zo.lcg_gauss(123, 24 + 30 + 15)
+    ws, bs = np_ref.unpack(dims, p)
+    o = 0
+    for l, w in enumerate(ws):
+        s = np.float32(np.sqrt(np.float32(1.0) / np.float32(dims[l]))) * np.float32(0.5 if l == 2 else 1.0)
+        assert np.array_equal(w.ravel().astype(np.float32), (gs[o:o + w.size] * s).astype(np.float32))
+        o += w.size
+    assert all(np.all(b == 0) for b in bs)
+
+
+@pytest.mark.parametrize("dims", [[4, 6, 5, 3], [123, 64, 29], [10, 1]])
+def test_forward_closed_form(dims):
+    g = np.random.default_rng(len(dims))
+    p = (g.standard_normal(zo.packed_count(dims)) * 0.3).astype(np.float32)
+    x = g.standard_normal((50, dims[0])).astype(np.float32)
+    got = zo.mlp_forward(dims, p, x)
+    want = np_ref.forward(dims, p, x)[1:]
+    for a, b in zip(got, want):
+        assert rel_amax(a, b) < 1e-5
+
+
+def test_backward_matches_finite_difference():
+    """net.rs:267-307 verbatim: dims [4,6,5,3], Lcg(123), central differences
+    with eps 1e-3 on indices {0, len/2, len-1} of every layer, tol 1e-2."""
+    dims = [4, 6, 5, 3]
+    p = zo.mlp_init(dims, 1.0, 123)
+    x = np.array([[0.3, -0.7, 0.1, 0.9]], np.float32)
+    target = np.array([0.2, -0.4, 0.6], np.float32)
+
+    def loss(params):
+        o = zo.mlp_forward(dims, params, x)[-1][0]
+        return np.float32(0.5) * np.float32(sum(np.float32((o[k] - target[k]) ** 2) for k in range(3)))
+
+    o = zo.mlp_forward(dims, p, x)[-1][0]
+    g, _ = zo.mlp_backward(dims, p, x, (o - target)[None, :])
+    eps = 1e-3
+    off = 0
+    for l in range(3):
+        n_w = dims[l + 1] * dims[l]
+        for idx in (0, n_w // 2, n_w - 1):
+            q = p.copy()
+            q[off + idx] = p[off + idx] + eps
+            lp = loss(q)
+            q[off + idx] = p[off + idx] - eps
+            lm = loss(q)
+            fd = (lp - lm) / (2 * eps)
+            assert abs(fd - g[off + idx]) < 1e-2, (l, idx, fd, g[off + idx])
+        off += n_w + dims[l + 1]
+
+
+def test_backward_all_params_f64_fd():
+    """Every weight and bias of a small net against float64 central differences."""
+    dims = [5, 7, 4, 3]
+    g = np.random.default_rng(3)
+    p = (g.standard_normal(zo.packed_count(dims)) * 0.5).astype(np.float32)
+    x = g.standard_normal((9, 5)).astype(np.float32)
+    gout = g.standard_normal((9, 3)).astype(np.float32)
+    got, gin = zo.mlp_backward(dims, p, x, gout, want_gin=True)
+
+    def L(params):
+        return float(np.sum(np_ref.forward(dims, params, x)[-1] * gout))
+
+    eps = 1e-6
+    fd = np.empty(p.size)
+    pf = p.astype(np.float64)
+    for i in range(p.size):
+        q = pf.copy()
+        q[i] += eps
+        lp = L(q)
+        q[i] -= 2 * eps
+        fd[i] = (lp - L(q)) / (2 * eps)
+    assert rel_amax(got, fd) < 1e-4
+    # dL/dx (the returned input gradient)
+    fdx = np.empty_like(x, dtype=np.float64)
+    for r in range(x.shape[0]):
+        for c in range(x.shape[1]):
+            xp = x.astype(np.float64).copy()
+            xp[r, c] += eps
+            a = float(np.sum(np_ref.forward(dims, p, xp)[-1] * gout))
+            xp[r, c] -= 2 * eps
+            b = float(np.sum(np_ref.forward(dims, p, xp)[-1] * gout))
+            fdx[r, c] = (a - b) / (2 * eps)
+    assert rel_amax(gin, fdx) < 1e-4
+
+
+def test_adam_minimizes_quadratic():
+    """net.rs:309-328: [2,1] net, Lcg(7), lr 1e-2, 500 steps, loss < 1e-3 x initial."""
+    dims = [2, 1]
+    p = zo.mlp_init(dims, 1.0, 7)
+    x = np.array([[1.0, -2.0]], np.float32)
+    target = np.float32(0.5)
+
+    def loss(q):
+        return float((zo.mlp_forward(dims, q, x)[-1][0, 0] - target) ** 2)
+
+    l0 = loss(p)
+    m = np.zeros_like(p)
+    v = np.zeros_like(p)
+    d = zo.dims_arr(dims)
+    for t in range(1, 501):
+        out = zo.mlp_forward(dims, p, x)[-1]
+        gout = np.float32(2.0) * (out - target)
+        gr, _ = zo.mlp_backward(dims, p, x, gout)
+        zo.lib().zlo_adam_step(zo._p(d), 2, zo._p(p), zo._p(gr), zo._p(m), zo._p(v), t, 1e-2)
+    assert loss(p) < l0 * 1e-3
+
+
+def test_adam_closed_form_first_step():
+    """Step 1 from zero moments: m = 0.1 g, v = 0.001 g^2 -> p -= lr g / (|g| + eps)."""
+    g = np.array([1e-3, -2.0, 0.5, 0.0], np.float32)
+    p = np.array([0.1, 0.2, -0.3, 0.4], np.float32)
+    bc1 = np.float32(1.0) - np.float32(zo.powi(0.9, 1))
+    bc2 = np.float32(1.0) - np.float32(zo.powi(0.999, 1))
+    p1, m1, v1 = zo.adam_flat(p, g, np.zeros(4), np.zeros(4), 1e-2, float(bc1), float(bc2))
+    want = p.astype(np.float64) - 1e-2 * g / (np.abs(g.astype(np.float64)) + 1e-8)
+    assert np.allclose(p1, want, rtol=1e-5, atol=1e-7)
+    assert p1[3] == p[3]
+
+
+def test_grad_clip_caps_norm():
+    """net.rs:330-338: dims [3,4,2], b[0][0] = 100, clip(1.0) -> norm 1."""
+    dims = [3, 4, 2]
+    g = np.zeros(zo.packed_count(dims), np.float32)
+    g[12] = 100.0  # b[0][0] follows w[0] (4 x 3)
+    clipped, n = zo.mlpgrad_clip(dims, g, 1.0)
+    assert n == pytest.approx(100.0)
+    assert abs(float(np.sqrt(np.sum(clipped.astype(np.float64) ** 2))) - 1.0) < 1e-4
+    same, _ = zo.mlpgrad_clip(dims, g * 1e-4, 1.0)  # below the bound: untouched
+    assert np.array_equal(same, g * np.float32(1e-4))
+
+
+# ------------------------------------------------------------------- ppo.rs
+
+def test_gae_matches_hand_computation():
+    # ppo.rs:709-721
+    adv, ret = zo.gae([1.0, 2.0], [0.0, 0.0], [0, 0], 0.0, 1.0, 1.0)
+    assert abs(ret[1] - 2.0) < 1e-6 and abs(ret[0] - 3.0) < 1e-6
+    assert abs(adv[0] - 3.0) < 1e-6 and abs(adv[1] - 2.0) < 1e-6
+
+
+def test_gae_respects_done_boundary():
+    # ppo.rs:760-768
+    adv, _ = zo.gae([1.0, 1.0], [5.0, 5.0], [1, 0], 0.0, 0.99, 0.95)
+    assert abs(adv[0] - (-4.0)) < 1e-6
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 24])
+def test_gae_closed_form(T):
+    g = np.random.default_rng(T)
+    for _ in range(20):
+        r = g.standard_normal(T).astype(np.float32)
+        v = g.standard_normal(T).astype(np.float32)
+        d = (g.random(T) < 0.2).astype(np.uint8)
+        lv = float(g.standard_normal())
+        adv, ret = zo.gae(r, v, d, lv, 0.99, 0.95)
+        for t in range(T):
+            acc, coef = 0.0, 1.0
+            for k in range(t, T):
+                nv = lv if k == T - 1 else float(v[k + 1])
+                nt = 0.0 if d[k] else 1.0
+                acc += coef * (float(r[k]) + 0.99 * nv * nt - float(v[k]))
+                if d[k]:
+                    break
+                coef *= 0.99 * 0.95
+            assert abs(adv[t] - acc) <= 1e-5 * max(1.0, abs(acc))
+            assert abs(ret[t] - (acc + float(v[t]))) <= 1e-5 * max(1.0, abs(acc))
+
+
+def test_golden_gae_vectors():
+    with open(os.path.join(GOLDEN, "gae_cases.json")) as f:
+        gold = json.load(f)
+    for case in gold["cases"]:
+        adv, ret = zo.gae(case["rewards"], case["values"], case["dones"], case["last_value"],
+                          case["gamma"], case["lam"])
+        assert np.allclose(adv, case["adv"], atol=1e-6) and np.allclose(ret, case["ret"], atol=1e-6)
+
+
+def test_adv_normalize_population_variance():
+    a = np.random.default_rng(1).standard_normal(1000).astype(np.float32) * 2 + 3
+    got = zo.adv_normalize(a)
+    want = (a - a.astype(np.float64).mean()) / a.astype(np.float64).std(ddof=0)
+    assert rel_amax(got, want) < 1e-5
+    assert np.all(zo.adv_normalize(np.full(8, 3.0, np.float32)) == 0.0)  # sd floor 1e-6
+
+
+def _ppo_tiny(seed, v_shift):
+    g = np.random.default_rng(seed)
+    ad, cd = [3, 5, 2], [3, 5, 1]
+    actor = (g.standard_normal(zo.packed_count(ad)) * 0.5).astype(np.float32)
+    critic = (g.standard_normal(zo.packed_count(cd)) * 0.5).astype(np.float32)
+    log_std = np.array([-0.3, 0.2], np.float32)
+    n = 16
+    obs = g.standard_normal((n, 3)).astype(np.float32)
+    means = np_ref.forward(ad, actor, obs)[-1].astype(np.float32)
+    vals = np_ref.forward(cd, critic, obs)[-1][:, 0].astype(np.float32)
+    action = (means + 0.7 * g.standard_normal((n, 2))).astype(np.float32)
+    lp = np.sum(-0.5 * ((action - means) / np.exp(log_std)) ** 2 - log_std - 0.9189385, axis=1)
+    batch = dict(obs=obs, critic_obs=obs, action=action,
+                 mean_old=(means + 0.1 * g.standard_normal((n, 2))).astype(np.float32),
+                 logp_old=(lp + 0.02 * g.standard_normal(n)).astype(np.float32),
+                 value_old=(vals + v_shift).astype(np.float32),
+                 adv=g.standard_normal(n).astype(np.float32),
+                 ret=g.standard_normal(n).astype(np.float32))
+    return ad, cd, actor, critic, log_std, batch
+
+
+def test_ppo_minibatch_grads_finite_difference():
+    """The per-sample PPO gradients (ppo.rs:411-450) against float64 central
+    differences of the minibatch loss  s*sum[-surr + c_v*vloss] - c_ent*entropy
+    (value clamp inactive: |v - v_old| < clip; ratios inside or outside the
+    clip band are both covered by the random draw)."""
+    ad, cd, actor, critic, log_std, batch = _ppo_tiny(12, v_shift=0.05)
+    n = batch["obs"].shape[0]
+    idx = np.arange(n)
+    ga, gc, gl, st = zo.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
+
+    def L(a, c, ls):
+        aa = np_ref.forward(ad, a, batch["obs"])
+        mean = aa[-1]
+        d = batch["action"] - mean
+        lp = np.sum(-0.5 * (d / np.exp(ls)) ** 2 - ls - 0.9189385, axis=1)
+        ratio = np.exp(lp - batch["logp_old"])
+        A = batch["adv"].astype(np.float64)
+        surr = np.minimum(ratio * A, np.clip(ratio, 0.8, 1.2) * A)
+        v = np_ref.forward(cd, c, batch["critic_obs"])[-1][:, 0]
+        vo, R = batch["value_old"].astype(np.float64), batch["ret"].astype(np.float64)
+        vc = vo + np.clip(v - vo, -0.2, 0.2)
+        vl = np.maximum((v - R) ** 2, (vc - R) ** 2)
+        ent = np.sum(ls + 0.5 + 0.9189385)
+        return float(np.sum(-surr + vl) / n - 0.01 * ent)
+
+    a64, c64, l64 = actor.astype(np.float64), critic.astype(np.float64), log_std.astype(np.float64)
+    eps = 1e-6
+
+    def fd(vec, f):
+        out = np.empty(vec.size)
+        for i in range(vec.size):
+            q = vec.copy()
+            q[i] += eps
+            hi = f(q)
+            q[i] -= 2 * eps
+            out[i] = (hi - f(q)) / (2 * eps)
+        return out
+
+    fa = fd(a64, lambda q: L(q, c64, l64))
+    fc = fd(c64, lambda q: L(a64, q, l64))
+    fl = fd(l64, lambda q: L(a64, c64, q))
+    assert rel_amax(ga, fa) < 1e-3 and rel_amax(gc, fc) < 1e-3 and rel_amax(gl, fl) < 1e-3
+
+
+def test_value_clamp_straight_through():
+    """Q7 (ppo.rs:440-447): when the clipped loss wins, dv = 2(v_clipped - R);
+    the clamp's own zero derivative is ignored. Checked on the critic's
+    output bias gradient (= sum over samples of dL/dv)."""
+    ad, cd, actor, critic, log_std, batch = _ppo_tiny(3, v_shift=0.0)
+    n = batch["obs"].shape[0]
+    v = np_ref.forward(cd, critic, batch["critic_obs"])[-1][:, 0]
+    even = np.arange(n) % 2 == 0
+    batch["value_old"] = (v + np.where(even, 1.0, -1.0)).astype(np.float32)  # clamp active
+    # even rows: R next to v (the clipped loss wins); odd rows: R past v_old (unclipped wins)
+    batch["ret"] = np.where(even, v + 0.01, batch["value_old"] - 0.05).astype(np.float32)
+    _, gc, _, _ = zo.minibatch_grads(ad, cd, actor, critic, log_std, batch, np.arange(n), 0.2, 0.0, 1.0)
+    vo, R = batch["value_old"].astype(np.float64), batch["ret"].astype(np.float64)
+    vc = vo + np.clip(v - vo, -0.2, 0.2)
+    use_c = (vc - R) ** 2 > (v - R) ** 2
+    assert use_c.any() and (~use_c).any()
+    dv = np.where(use_c, 2 * (vc - R), 2 * (v - R)) / n
+    assert abs(gc[-1] - dv.sum()) < 1e-5 * max(1.0, abs(dv.sum()))
+
+
+def test_ppo_improves_on_bandit():
+    """ppo.rs:772-845 verbatim: a 1-step Gaussian bandit; PPO pulls the actor
+    mean to the target (rayon replaced by the single-threaded fold)."""
+    rng = np.array([2024 | 1], np.uint64)
+    ac = zo.ActorCritic([3, 32, 2], [3, 32, 1], 0.6, 3e-3, rng_state=rng)
+    cfg = zo.PpoCfg(0.99, 0.95, 0.2, 0.0, 1.0, 4, 4, 1.0, 0.01, 1e-5, 1e-2, 1)
+    obs = np.array([0.5, -0.2, 0.1], np.float32)
+    target = np.array([0.7, -0.4], np.float32)
+
+    def mean_reward():
+        m = ac.mean(obs)
+        return -float((m[0] - target[0]) ** 2 + (m[1] - target[1]) ** 2)
+
+    r0 = mean_reward()
+    n = 256
+    for _ in range(120):
+        acts = np.empty((n, 2), np.float32)
+        means = np.empty((n, 2), np.float32)
+        logps = np.empty(n, np.float32)
+        vals = np.empty(n, np.float32)
+        rews = np.empty(n, np.float32)
+        for i in range(n):
+            a, lp, m = ac.sample(obs, rng)
+            acts[i], logps[i], means[i] = a, lp, m
+            rews[i] = -((a[0] - target[0]) ** 2 + (a[1] - target[1]) ** 2)
+            vals[i] = ac.value(obs)
+        advs = np.empty(n, np.float32)
+        rets = np.empty(n, np.float32)
+        for i in range(n):
+            ad_, rt_ = zo.gae([rews[i]], [vals[i]], [1], 0.0, 0.99, 0.95)
+            advs[i], rets[i] = ad_[0], rt_[0]
+        obs_b = np.tile(obs, (n, 1))
+        ac.update(dict(obs=obs_b, critic_obs=obs_b, action=acts, mean_old=means, logp_old=logps,
+                       value_old=vals, adv=advs, ret=rets), cfg, nthreads=1, normalize_obs=True)
+    r1 = mean_reward()
+    assert r1 > r0 + 0.2, (r0, r1)
+    m = ac.mean(obs)
+    assert abs(m[0] - target[0]) < 0.25 and abs(m[1] - target[1]) < 0.25
+
+
+def test_trainer_and_actor_critic_agree_on_one_step():
+    """One epoch of one minibatch covering the whole batch, no clip: the two
+    restated update semantics take the same Adam step (t = gstep = 1)."""
+    ad, cd, actor, critic, log_std, batch = _ppo_tiny(5, v_shift=0.05)
+    batch["adv"] = zo.adv_normalize(batch["adv"])
+    ac = zo.ActorCritic(ad, cd, 1.0, 1e-3, 1)
+    ac.set(actor, critic, log_std, 1e-3)
+    cfg = zo.PpoCfg(0.99, 0.95, 0.2, 0.01, 1.0, 1, 1, 1e9, 0.01, 1e-5, 1e-2, 0)
+    ac.update(batch, cfg, nthreads=1, normalize_obs=False)
+    a1, c1, l1, _, _ = ac.get()
+    tr = zo.Trainer(ad, cd, actor, critic, log_std, 1e-3)
+    tcfg = zo.TrainerCfg(0.2, 0.01, 1.0, 1, 1, 0.0, 0.01, 1e-5, 1e-2, 0, 0, 0)
+    tr.update(batch, tcfg)
+    a2, c2, l2, _, gstep = tr.get()
+    assert gstep == 1
+    # Same gradient up to summation order (shuffled vs contiguous), Adam step 1.
+    assert np.max(np.abs(a1 - a2)) < 1e-6 + 2e-3 * 1e-3
+    assert np.max(np.abs(l1 - l2)) < 1e-6
+
+
+def test_trainer_early_stop_and_clamp():
+    """Trainer semantics: a tiny desired_kl trips the early stop after the first
+    epoch, and log_std is clamped to [-1.6, 0.0] after the update."""
+    ad, cd, actor, critic, log_std, batch = _ppo_tiny(9, v_shift=0.05)
+    batch["adv"] = zo.adv_normalize(batch["adv"])
+    log_std = np.array([0.5, -2.0], np.float32)
+    tr = zo.Trainer(ad, cd, actor, critic, log_std, 1e-2)
+    st = tr.update(batch, zo.TrainerCfg(0.2, 0.01, 1.0, 5, 2, 1.0, 1e-6, 1e-5, 1e-2, 1, 1, 1))
+    _, _, ls, lr, gstep = tr.get()
+    assert int(st[5]) == 1 and gstep == 2
+    assert np.all(ls <= 0.0) and np.all(ls >= -1.6)
+    assert lr == pytest.approx(max(1e-2 / 1.5, 1e-5), rel=1e-6)

@@ -1,0 +1,53 @@
+// common.hip — shared device helpers for the gfx950 code object.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "zk_args.h"
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+namespace zk {
+
+constexpr int kThreads = 256;
+constexpr float kLogSqrt2Pi = 0.9189385f;  // zealot-rl/src/ppo.rs:18
+
+// zealot-rl/src/net.rs:14-16: x > 0 ? x : exp(x) - 1 (not expm1).
+__device__ __forceinline__ float elu(float x) { return x > 0.0f ? x : expf(x) - 1.0f; }
+
+// zealot-rl/src/net.rs:21-23: derivative from the post-activation.
+__device__ __forceinline__ float elu_grad_from_act(float a) { return a > 0.0f ? 1.0f : a + 1.0f; }
+
+__device__ __forceinline__ float clampf(float x, float lo, float hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// Rust f32::powi lowering (__powisf2): square-and-multiply from the low bit,
+// plain f32 multiplies. Bit-identical to the host computation.
+__device__ __forceinline__ float powi_f32(float x, int n) {
+  unsigned int k = n < 0 ? -(unsigned int)n : (unsigned int)n;
+  float y = (k & 1u) ? x : 1.0f;
+  while (k >>= 1) {
+    x = x * x;
+    if (k & 1u) y = y * x;
+  }
+  return n < 0 ? 1.0f / y : y;
+}
+
+// Deterministic in-block tree sum over kThreads values held one per thread.
+// `sm` must hold kThreads floats. Returns the total in every thread.
+__device__ __forceinline__ float block_sum(float v, float* sm) {
+  const int t = threadIdx.x;
+  sm[t] = v;
+  __syncthreads();
+#pragma unroll
+  for (int s = kThreads / 2; s > 0; s >>= 1) {
+    if (t < s) sm[t] = sm[t] + sm[t + s];
+    __syncthreads();
+  }
+  float r = sm[0];
+  __syncthreads();
+  return r;
+}
+
+}  // namespace zk

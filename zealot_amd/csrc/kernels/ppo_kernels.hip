@@ -1,0 +1,474 @@
+// ppo_kernels.hip — the non-GEMM kernels of the PPO update on gfx950.
+//
+// All are bandwidth/latency-bound and written as single-pass, coalesced
+// kernels with deterministic (fixed-order, atomic-free) reductions. FP
+// contraction is off for the whole code object, so every expression rounds
+// like the reference's Rust source (zealot-rl/src/net.rs, ppo.rs).
+#pragma once
+#include "common.hip"
+
+namespace zk {
+
+// ------------------------------------------------------------------ losses
+
+// Per-sample body of zealot-rl/src/ppo.rs:411-432 and :452 (actor half of
+// minibatch_step), one thread per sample; the per-sample log_std gradient and
+// statistics are reduced per block in a fixed tree (the rayon fold of
+// :406-462 has no fixed order either).
+__device__ void actor_loss_body(const ActorLossArgs& p) {
+  extern __shared__ float sm[];  // [kThreads * A] + [kThreads]
+  if (p.guard && *p.guard == 0) return;
+  const int t = threadIdx.x;
+  const int r = blockIdx.x * kThreads + t;
+  const int A = p.A;
+  float* contrib = sm;                   // [kThreads][A]
+  float* red = sm + kThreads * A;        // [kThreads]
+  float surr_c = 0.f, kl_c = 0.f;
+  if (r < p.rows) {
+    const long long s = p.perm ? p.perm[p.row0 + r] : (long long)(p.row0 + r);
+    const float* mu = p.mean + (long long)r * p.ldm;
+    const float* act = p.action + s * p.ldact;
+    float lp = 0.f;
+    for (int k = 0; k < A; ++k) {  // ActorCritic::logp, ppo.rs:297-305
+      const float ls = p.log_std[k];
+      const float sd = expf(ls);
+      const float d = (act[k] - mu[k]) / sd;
+      lp += -0.5f * d * d - ls - kLogSqrt2Pi;
+    }
+    const float ratio = expf(lp - p.logp_old[s]);
+    const float a = p.adv[s];
+    const float lo = 1.0f - p.clip, hi = 1.0f + p.clip;
+    const float surr = fminf(ratio * a, clampf(ratio, lo, hi) * a);
+    surr_c = surr * p.scale;
+    const bool clipped = (a >= 0.0f && ratio > hi) || (a < 0.0f && ratio < lo);
+    float* dl = p.delta + (long long)r * p.ldd;
+    for (int k = 0; k < A; ++k) {
+      const float inv_var = expf(-2.0f * p.log_std[k]);
+      float gm = 0.f, c = 0.f;
+      if (!clipped) {
+        const float d = act[k] - mu[k];
+        gm = -(a * ratio * d * inv_var) * p.scale;
+        const float dls = a * ratio * ((d * d) * inv_var - 1.0f);
+        c = -dls * p.scale;
+      }
+      c += -p.entropy_coef * p.scale;
+      dl[k] = gm;
+      contrib[t * A + k] = c;
+    }
+    if (p.mean_old) {  // ActorCritic::kl, ppo.rs:327-334
+      const float* mo = p.mean_old + s * p.ldmo;
+      float klv = 0.f;
+      for (int k = 0; k < A; ++k) {
+        const float inv = expf(-p.log_std[k]);
+        const float y = (mu[k] - mo[k]) * inv;
+        klv += 0.5f * (y * y);
+      }
+      kl_c = klv * p.scale;
+    }
+  } else {
+    for (int k = 0; k < A; ++k) contrib[t * A + k] = 0.f;
+  }
+  __syncthreads();
+  // Fixed-tree reduction of the [kThreads][A] contributions over threads.
+  for (int st = kThreads / 2; st > 0; st >>= 1) {
+    for (int i = t; i < st * A; i += kThreads) contrib[i] = contrib[i] + contrib[i + st * A];
+    __syncthreads();
+  }
+  for (int k = t; k < A; k += kThreads) p.gls_part[(long long)blockIdx.x * A + k] = contrib[k];
+  const float s_tot = block_sum(surr_c, red);
+  const float k_tot = block_sum(kl_c, red);
+  if (t == 0) {
+    p.stat_part[blockIdx.x * 2 + 0] = s_tot;
+    p.stat_part[blockIdx.x * 2 + 1] = k_tot;
+  }
+}
+
+// zealot-rl/src/ppo.rs:436-450 (clipped value loss; the clamp's derivative is
+// ignored, so the gradient flows through v_clipped as if it were v).
+__device__ void value_loss_body(const ValueLossArgs& p) {
+  __shared__ float red[kThreads];
+  if (p.guard && *p.guard == 0) return;
+  const int t = threadIdx.x;
+  const int r = blockIdx.x * kThreads + t;
+  float vl_c = 0.f;
+  if (r < p.rows) {
+    const long long s = p.perm ? p.perm[p.row0 + r] : (long long)(p.row0 + r);
+    const float v = p.v[(long long)r * p.ldv];
+    const float vo = p.value_old[s], R = p.ret[s];
+    const float vc = vo + clampf(v - vo, -p.clip, p.clip);
+    const float lu = (v - R) * (v - R);
+    const float lc = (vc - R) * (vc - R);
+    float vloss, dv;
+    if (lc > lu) {
+      vloss = lc;
+      dv = 2.0f * (vc - R);
+    } else {
+      vloss = lu;
+      dv = 2.0f * (v - R);
+    }
+    vl_c = vloss * p.scale;
+    p.delta[(long long)r * p.ldd] = p.value_coef * dv * p.scale;
+  }
+  const float tot = block_sum(vl_c, red);
+  if (t == 0) p.stat_part[blockIdx.x] = tot;
+}
+
+// ------------------------------------------------- grad norm / finalize / Adam
+
+// Per-block sum of squares over fixed chunks of two contiguous ranges.
+__device__ void sumsq_body(const SumsqArgs& p) {
+  __shared__ float red[kThreads];
+  if (p.guard && *p.guard == 0) return;
+  const int b = blockIdx.x;
+  long long off, len;
+  int cb;
+  if (b < p.blocks0) {
+    off = p.off0;
+    len = p.len0;
+    cb = b;
+  } else {
+    off = p.off1;
+    len = p.len1;
+    cb = b - p.blocks0;
+  }
+  const long long lo = (long long)cb * p.chunk;
+  const long long hi = min(len, lo + p.chunk);
+  float s = 0.f;
+  for (long long i = lo + threadIdx.x; i < hi; i += kThreads) {
+    const float x = p.x[off + i];
+    s += x * x;
+  }
+  const float tot = block_sum(s, red);
+  if (threadIdx.x == 0) p.part[b] = tot;
+}
+
+// Scalar tail of one minibatch step: ppo.rs:464-489 (ActorCritic::update
+// semantics) or src/bin/biped_train_gpu.rs:1350-1452 (trainer semantics),
+// with every scalar kept on the device.
+__device__ void finalize_body(const FinalizeArgs& p) {
+  __shared__ float sg[256];
+  if (p.guard && *p.guard == 0) return;
+  const int t = threadIdx.x;
+  const int A = p.pp.A;
+  for (int k = t; k < A; k += kThreads) {
+    float g = 0.f;
+    for (int b = 0; b < p.nb_a; ++b) g += p.gls_part[(long long)b * A + k];
+    p.g_logstd[k] = g;
+    if (k < 256) sg[k] = g;
+  }
+  __syncthreads();
+  if (t != 0) return;
+  DevState* st = p.st;
+  const PpoParams& pp = p.pp;
+  float surr = 0.f, kl = 0.f, vloss = 0.f;
+  for (int b = 0; b < p.nb_a; ++b) {
+    surr += p.astat_part[b * 2 + 0];
+    kl += p.astat_part[b * 2 + 1];
+  }
+  for (int b = 0; b < p.nb_v; ++b) vloss += p.vstat_part[b];
+  float sq_a = 0.f, sq_c = 0.f, sq_l = 0.f;
+  for (int b = 0; b < p.nsq_a; ++b) sq_a += p.sq_part[b];
+  for (int b = p.nsq_a; b < p.nsq; ++b) sq_c += p.sq_part[b];
+  for (int k = 0; k < A; ++k) {
+    const float g = k < 256 ? sg[k] : p.g_logstd[k];
+    sq_l += g * g;
+  }
+  float ent = 0.f;  // ActorCritic::entropy, ppo.rs:308-311 (pre-step log_std)
+  const float c = 0.5f + kLogSqrt2Pi;
+  for (int k = 0; k < A; ++k) ent += p.log_std[k] + c;
+
+  if (pp.mode == 0) {
+    if (pp.adaptive_lr) {  // ppo.rs:476-482
+      if (kl > pp.desired_kl * 2.0f)
+        st->lr = fmaxf(st->lr / 1.5f, pp.lr_min);
+      else if (kl > 0.0f && kl < pp.desired_kl / 2.0f)
+        st->lr = fminf(st->lr * 1.5f, pp.lr_max);
+    }
+    // MlpGrad::clip per net (net.rs:197-202); log_std is not clipped.
+    const float na = sqrtf(sq_a), nc = sqrtf(sq_c);
+    st->scale[0] = (na > pp.max_grad_norm && na > 0.0f) ? pp.max_grad_norm / na : 1.0f;
+    st->scale[1] = (nc > pp.max_grad_norm && nc > 0.0f) ? pp.max_grad_norm / nc : 1.0f;
+    st->scale[2] = 1.0f;
+    st->norm[0] = na;
+    st->norm[1] = nc;
+    st->norm[2] = sqrtf(sq_l);
+    st->t += 1;  // Adam::step / step_log_std advance together (net.rs:235, ppo.rs:497)
+    st->bc1 = 1.0f - powi_f32(pp.beta1, st->t);
+    st->bc2 = 1.0f - powi_f32(pp.beta2, st->t);
+  } else {
+    // Global clip over actor + critic + log_std (biped_train_gpu.rs:1368-1452).
+    float s = 1.0f;
+    if (pp.max_grad_norm > 0.0f) {
+      const float norm = sqrtf(sq_a + sq_c + sq_l);
+      if (norm > pp.max_grad_norm) s = pp.max_grad_norm / norm;
+      st->norm[0] = norm;
+    }
+    st->scale[0] = s;
+    st->scale[1] = s;
+    st->scale[2] = s;
+  }
+  st->ep_kl += kl;
+  st->ep_surr += surr;
+  st->ep_vloss += vloss;
+  st->ep_ent += ent;
+  st->mb_in_epoch += 1;
+}
+
+// Adam element update of zealot-rl/src/net.rs:240-245 over one flat buffer
+// holding every tensor of the update, float4-vectorised.
+__device__ void adam_body(const AdamArgs& p) {
+  if (p.guard && *p.guard == 0) return;
+  float lr = p.lr, bc1 = p.bc1, bc2 = p.bc2;
+  float s0 = 1.f, s1 = 1.f, s2 = 1.f;
+  if (p.st) {
+    lr = p.st->lr;
+    bc1 = p.st->bc1;
+    bc2 = p.st->bc2;
+    s0 = p.st->scale[0];
+    s1 = p.st->scale[1];
+    s2 = p.st->scale[2];
+  }
+  const float b1 = p.beta1, b2 = p.beta2, eps = p.eps;
+  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+  const long long i0 = ((long long)blockIdx.x * kThreads + threadIdx.x) * 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const long long i = i0 + j;
+    if (i < p.n) {
+      const int grp = i < p.end_a ? 0 : (i < p.end_c ? 1 : 2);
+      const float sc = grp == 0 ? s0 : (grp == 1 ? s1 : s2);
+      const float gr = p.g[i] * sc;
+      const float m = b1 * p.m[i] + omb1 * gr;
+      const float v = b2 * p.v[i] + omb2 * gr * gr;
+      float x = p.p[i] - lr * (m / bc1) / (sqrtf(v / bc2) + eps);
+      if (grp == 2 && p.clamp_ls) x = clampf(x, -1.6f, 1.0f);
+      p.m[i] = m;
+      p.v[i] = v;
+      p.p[i] = x;
+    }
+  }
+}
+
+// --------------------------------------------------------------- epoch logic
+
+__device__ void epoch_begin_body(const EpochBeginArgs& p) {
+  if (p.guard && *p.guard == 0) return;
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  DevState* st = p.st;
+  if (p.pp.mode == 1) {  // biped_train_gpu.rs:1165-1167
+    st->gstep += (unsigned long long)p.pp.n_mb;
+    const unsigned long long cap = 1ull << 30;
+    const int tt = (int)(st->gstep < cap ? st->gstep : cap);
+    st->bc1 = 1.0f - powi_f32(p.pp.beta1, tt);
+    st->bc2 = 1.0f - powi_f32(p.pp.beta2, tt);
+  }
+  st->ep_kl = 0.f;
+  st->ep_surr = 0.f;
+  st->ep_vloss = 0.f;
+  st->ep_ent = 0.f;
+  st->mb_in_epoch = 0;
+}
+
+// Full-Gaussian KL(old || new) of src/bin/biped_train_gpu.rs:1478-1491, one
+// thread per row of the last minibatch, block partials.
+__device__ void kl_body(const KlArgs& p) {
+  __shared__ float red[kThreads];
+  if (p.guard && *p.guard == 0) return;
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  float acc = 0.f;
+  if (r < p.rows) {
+    const long long s = p.perm ? p.perm[p.row0 + r] : (long long)(p.row0 + r);
+    for (int k = 0; k < p.A; ++k) {
+      const float ls_new = p.log_std[k], ls_old = p.log_std_old[k];
+      const float sig_old2 = expf(2.0f * ls_old);
+      const float inv_sig_new2 = expf(-2.0f * ls_new);
+      const float dmu = p.mean[(long long)r * p.ldm + k] - p.mean_old[s * p.ldmo + k];
+      acc += (ls_new - ls_old) + 0.5f * (sig_old2 + dmu * dmu) * inv_sig_new2 - 0.5f;
+    }
+  }
+  const float tot = block_sum(acc, red);
+  if (threadIdx.x == 0) p.part[blockIdx.x] = tot;
+}
+
+__device__ void epoch_end_body(const EpochEndArgs& p) {
+  if (*p.active == 0) return;
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  DevState* st = p.st;
+  const PpoParams& pp = p.pp;
+  const float inv = 1.0f / (float)pp.n_mb;  // ppo.rs:374-381
+  st->stats[0] = st->ep_kl * inv;
+  st->stats[1] = st->ep_surr * inv;
+  st->stats[2] = st->ep_vloss * inv;
+  st->stats[3] = st->ep_ent * inv;
+  st->epochs_run += 1;
+  if (pp.mode == 1 && p.kl_part) {
+    float kl = 0.f;
+    for (int b = 0; b < p.nkl; ++b) kl += p.kl_part[b];
+    kl /= (float)pp.mb;
+    st->last_kl = kl;
+    if (pp.adaptive_lr) {  // biped_train_gpu.rs:1497-1501
+      if (kl > pp.desired_kl * 2.0f)
+        st->lr = fmaxf(st->lr / 1.5f, pp.lr_min);
+      else if (kl > 0.0f && kl < pp.desired_kl / 2.0f)
+        st->lr = fminf(st->lr * 1.5f, pp.lr_max);
+    }
+    if (pp.early_stop && kl > pp.desired_kl * 5.0f) *p.active = 0;  // :1513-1515
+  }
+  st->stats[4] = st->lr;
+}
+
+// --------------------------------------------------------- GAE / advantages
+
+// zealot-rl/src/ppo.rs:681-703: one thread per env, serial backward scan.
+__device__ void gae_body(const GaeArgs& p) {
+  if (p.guard && *p.guard == 0) return;
+  const int e = blockIdx.x * kThreads + threadIdx.x;
+  if (e >= p.N) return;
+  float acc = 0.f;
+  float next_v = p.last_v[e];
+  for (int i = p.T - 1; i >= 0; --i) {
+    const long long ii = (long long)i * p.in_ts + (long long)e * p.in_es;
+    const long long oi = (long long)i * p.out_ts + (long long)e * p.out_es;
+    const float nt = p.done[ii] ? 0.0f : 1.0f;
+    const float vi = p.v[ii];
+    const float delta = p.r[ii] + p.gamma * next_v * nt - vi;
+    acc = delta + p.gamma * p.lam * nt * acc;
+    p.adv[oi] = acc;
+    p.ret[oi] = acc + vi;
+    next_v = vi;
+  }
+}
+
+// Advantage normalisation (ppo.rs:343-348 / biped_train_gpu.rs:1010-1016):
+// population variance, sd floored at 1e-6. Three launches; every block
+// re-derives mean / var from the same partials in the same order.
+__device__ void adv_norm_body(const AdvNormArgs& p) {
+  __shared__ float red[kThreads];
+  __shared__ float bc[2];
+  if (p.guard && *p.guard == 0) return;
+  const long long lo = (long long)blockIdx.x * p.chunk;
+  const long long hi = min(p.n, lo + p.chunk);
+  if (p.phase > 0) {
+    if (threadIdx.x == 0) {
+      float s = 0.f;
+      for (int b = 0; b < p.nparts; ++b) s += p.part[b];
+      const float mean = s / (float)p.n;
+      bc[0] = mean;
+      if (p.phase == 2) {
+        float q = 0.f;
+        for (int b = 0; b < p.nparts; ++b) q += p.part2[b];
+        const float var = q / (float)p.n;
+        bc[1] = fmaxf(sqrtf(var), 1e-6f);
+      }
+    }
+    __syncthreads();
+  }
+  if (p.phase == 0) {
+    float s = 0.f;
+    for (long long i = lo + threadIdx.x; i < hi; i += kThreads) s += p.x[i];
+    const float tot = block_sum(s, red);
+    if (threadIdx.x == 0) p.part[blockIdx.x] = tot;
+  } else if (p.phase == 1) {
+    const float mean = bc[0];
+    float s = 0.f;
+    for (long long i = lo + threadIdx.x; i < hi; i += kThreads) {
+      const float d = p.x[i] - mean;
+      s += d * d;
+    }
+    const float tot = block_sum(s, red);
+    if (threadIdx.x == 0) p.part2[blockIdx.x] = tot;
+  } else {
+    const float mean = bc[0], sd = bc[1];
+    for (long long i = lo + threadIdx.x; i < hi; i += kThreads) p.x[i] = (p.x[i] - mean) / sd;
+  }
+}
+
+// ------------------------------------------------------ elementwise utilities
+
+// cuTile elu_backward_ct (src/biped/cutile_gemm.rs:272-286): g *= elu'(y).
+__device__ void elu_backward_body(const EluBwdArgs& p) {
+  if (p.guard && *p.guard == 0) return;
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= p.rows * p.cols) return;
+  const long long r = i / p.cols;
+  const int c = (int)(i % p.cols);
+  float* gp = p.g + r * p.ldg + c;
+  *gp = *gp * elu_grad_from_act(p.y[r * p.ldy + c]);
+}
+
+// cuTile row_sum_ct (src/biped/cutile_gemm.rs:290-311): one block per row.
+__device__ void row_sum_body(const RowSumArgs& p) {
+  __shared__ float red[kThreads];
+  if (p.guard && *p.guard == 0) return;
+  const int r = blockIdx.x;
+  float s = 0.f;
+  for (int c = threadIdx.x; c < p.cols; c += kThreads) s += p.x[(long long)r * p.ldx + c];
+  const float tot = block_sum(s, red);
+  if (threadIdx.x == 0) p.out[r] = tot;
+}
+
+// Row gather / pad: dst[r, c] = src[srow, c] for c < cols, 0 for cols <= c < ldd
+// when zero_pad (otherwise those columns are left untouched).
+__device__ void copy_rows_body(const CopyRowsArgs& p) {
+  if (p.guard && *p.guard == 0) return;
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= p.rows * p.ldd) return;
+  const long long r = i / p.ldd;
+  const int c = (int)(i % p.ldd);
+  if (c >= p.cols && !p.zero_pad) return;
+  float v = 0.f;
+  if (c < p.cols) {
+    const long long sr = p.perm ? p.perm[p.row0 + r] : p.row0 + r;
+    v = p.src[sr * p.lds + c];
+  }
+  p.dst[r * p.ldd + c] = v;
+}
+
+// ActorCritic::sample + logp (zealot-rl/src/ppo.rs:314-323, :297-305) with
+// the Gaussian noise supplied by the caller.
+__device__ void sample_body(const SampleArgs& p) {
+  if (p.guard && *p.guard == 0) return;
+  const int r = blockIdx.x * kThreads + threadIdx.x;
+  if (r >= p.rows) return;
+  const float* mu = p.mean + (long long)r * p.ldm;
+  const float* ep = p.eps + (long long)r * p.lde;
+  float* act = p.action + (long long)r * p.lda;
+  for (int k = 0; k < p.A; ++k) {
+    const float sd = expf(p.log_std[k]);
+    act[k] = mu[k] + sd * ep[k];
+  }
+  float lp = 0.f;
+  for (int k = 0; k < p.A; ++k) {
+    const float ls = p.log_std[k];
+    const float sd = expf(ls);
+    const float d = (act[k] - mu[k]) / sd;
+    lp += -0.5f * d * d - ls - kLogSqrt2Pi;
+  }
+  p.logp[r] = lp;
+}
+
+__device__ void clamp_body(const ClampArgs& p) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i < p.n) p.x[i] = clampf(p.x[i], p.lo, p.hi);
+}
+
+}  // namespace zk
+
+#define ZK_KERNEL(NAME, ARGS, BODY) \
+  extern "C" __global__ __launch_bounds__(256) void NAME(zk::ARGS p) { zk::BODY(p); }
+
+ZK_KERNEL(zk_actor_loss, ActorLossArgs, actor_loss_body)
+ZK_KERNEL(zk_value_loss, ValueLossArgs, value_loss_body)
+ZK_KERNEL(zk_sumsq, SumsqArgs, sumsq_body)
+ZK_KERNEL(zk_finalize, FinalizeArgs, finalize_body)
+ZK_KERNEL(zk_adam, AdamArgs, adam_body)
+ZK_KERNEL(zk_epoch_begin, EpochBeginArgs, epoch_begin_body)
+ZK_KERNEL(zk_kl, KlArgs, kl_body)
+ZK_KERNEL(zk_epoch_end, EpochEndArgs, epoch_end_body)
+ZK_KERNEL(zk_gae, GaeArgs, gae_body)
+ZK_KERNEL(zk_adv_norm, AdvNormArgs, adv_norm_body)
+ZK_KERNEL(zk_elu_backward, EluBwdArgs, elu_backward_body)
+ZK_KERNEL(zk_row_sum, RowSumArgs, row_sum_body)
+ZK_KERNEL(zk_copy_rows, CopyRowsArgs, copy_rows_body)
+ZK_KERNEL(zk_sample, SampleArgs, sample_body)
+ZK_KERNEL(zk_clamp, ClampArgs, clamp_body)

@@ -1,0 +1,237 @@
+// zk_args.h — kernel argument blocks shared by the gfx950 code object and the
+// host runtime. Plain structs (pointers, 32/64-bit scalars): the layout is
+// identical on x86-64 and amdgcn, so the host passes them by value through
+// hipModuleLaunchKernel.
+#pragma once
+#include <stdint.h>
+
+namespace zk {
+
+enum EpiMode : int {
+  kEpiStore = 0,    // C = acc
+  kEpiBiasN = 1,    // C = act(acc + bias[n])           (batch-major forward)
+  kEpiBiasM = 2,    // C = act(acc + bias[m*stride])    (feature-major forward)
+  kEpiEluGrad = 3,  // C = acc * elu'(Y[m*ldy + n])     (dgrad of a hidden layer)
+};
+
+struct GemmArgs {
+  const float* A;
+  const float* B;
+  float* C;
+  const float* bias;
+  const float* Y;
+  float* rowsumA;          // [splits x M] row sums of A (n-tile-0 blocks), nullable
+  const int* permA;        // storage-row gather for A, nullable
+  const int* permB;        // storage-row gather for B, nullable
+  const int* guard;        // no-op when *guard == 0, nullable
+  long long split_stride;  // elements between split-K partial outputs
+  int M, N, K;
+  int lda, ldb, ldc, ldy;
+  int bias_stride;
+  int epi;
+  int act;                 // ELU in the bias epilogues
+  int vecA, vecB;          // float4 global loads are aligned and in bounds
+  int kt_per_split;        // k-tiles per grid.z slice
+};
+
+struct SplitReduceArgs {
+  const float* part;     // [splits x rows_mn x cols] dense partials
+  float* out;            // element (r, c) at out[r * ldo + c]
+  const float* rowpart;  // [splits x rows], nullable
+  float* rowout;         // [rows]
+  const int* guard;
+  long long mn;          // rows_mn * cols
+  int cols, ldo;
+  int rows;
+  int splits;
+};
+
+// Scalars that live on the device for a whole update so that no kernel needs
+// a host round trip (learning rate, Adam step, clip scales, statistics).
+struct DevState {
+  float lr;
+  int t;                     // Adam steps taken (ActorCritic::update semantics)
+  float bc1, bc2;            // bias corrections for the next Adam launch
+  float scale[3];            // clip scale per group: actor, critic, log_std
+  int active;                // 0 once the trainer's KL early stop fired
+  int epochs_run;
+  int mb_in_epoch;
+  float ep_kl, ep_surr, ep_vloss, ep_ent;
+  float stats[5];            // kl, surrogate, value_loss, entropy, lr
+  float last_kl;
+  float norm[3];             // last pre-clip norms (actor, critic, log_std) / global
+  int pad0;
+  unsigned long long gstep;  // trainer gstep (src/bin/biped_train_gpu.rs:1165)
+};
+
+struct PpoParams {
+  int mode;  // 0 = ActorCritic::update (zealot-rl/src/ppo.rs:338), 1 = GPU trainer
+  int A;     // action dim
+  int mb;    // rows per minibatch
+  int n_mb;  // minibatches per epoch
+  float clip, entropy_coef, value_coef, scale;  // scale = 1/mb
+  float max_grad_norm;
+  float desired_kl, lr_min, lr_max;
+  int adaptive_lr, early_stop;
+  int clamp_ls;  // clamp log_std to [-1.6, 1.0] in every Adam step
+  float beta1, beta2, eps;
+};
+
+struct ActorLossArgs {
+  const float* mean;      // [rows x ldm] actor output of this minibatch
+  const float* action;    // [n x ldact] full batch
+  const float* adv;       // [n]
+  const float* logp_old;  // [n]
+  const float* mean_old;  // [n x ldmo], nullable (no KL statistic)
+  const float* log_std;   // [A]
+  const int* perm;        // sample = perm ? perm[row0 + r] : row0 + r
+  float* delta;           // [rows x ldd] dL/dmean
+  float* gls_part;        // [blocks x A] log_std gradient partials
+  float* stat_part;       // [blocks x 2] surrogate, kl partials
+  const int* guard;
+  int ldm, ldact, ldmo, ldd;
+  int row0, rows, A;
+  float clip, entropy_coef, scale;
+};
+
+struct ValueLossArgs {
+  const float* v;          // [rows x ldv] critic output
+  const float* value_old;  // [n]
+  const float* ret;        // [n]
+  const int* perm;
+  float* delta;            // [rows x ldd]
+  float* stat_part;        // [blocks] value-loss partials
+  const int* guard;
+  int ldv, ldd, row0, rows;
+  float clip, value_coef, scale;
+};
+
+struct SumsqArgs {
+  const float* x;
+  float* part;           // one partial per block
+  const int* guard;
+  long long off0, len0;  // group 0 range
+  long long off1, len1;  // group 1 range
+  int blocks0;           // blocks assigned to group 0; the rest cover group 1
+  int chunk;             // elements per block
+};
+
+struct FinalizeArgs {
+  DevState* st;
+  const float* gls_part;    // [nb_a x A]
+  const float* astat_part;  // [nb_a x 2]
+  const float* vstat_part;  // [nb_v]
+  const float* sq_part;     // [nsq]
+  const float* log_std;     // [A] (pre-step values)
+  float* g_logstd;          // [A] log_std gradient slot in the flat gradient
+  const int* guard;
+  PpoParams pp;
+  int nb_a, nb_v, nsq, nsq_a;
+};
+
+struct AdamArgs {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  const DevState* st;         // lr / bc1 / bc2 / scale from the device, or
+  const int* guard;
+  long long n, end_a, end_c;  // groups: [0,end_a) actor, [end_a,end_c) critic, rest log_std
+  float lr, bc1, bc2;         // ... these when st == nullptr (scale = 1)
+  float beta1, beta2, eps;
+  int clamp_ls;               // clamp group 2 to [-1.6, 1.0] (ppo.rs:508)
+};
+
+struct EpochBeginArgs {
+  DevState* st;
+  const int* guard;
+  PpoParams pp;
+};
+
+struct KlArgs {
+  const float* mean;         // [rows x ldm] last minibatch's actor output
+  const float* mean_old;     // [n x ldmo]
+  const float* log_std;      // [A] current
+  const float* log_std_old;  // [A] rollout snapshot
+  const int* perm;
+  float* part;               // [blocks]
+  const int* guard;
+  int ldm, ldmo, row0, rows, A;
+};
+
+struct EpochEndArgs {
+  DevState* st;
+  const float* kl_part;  // [nkl] (trainer mode), nullable
+  int* active;           // early-stop flag (the guard of every later kernel)
+  PpoParams pp;
+  int nkl;
+};
+
+struct GaeArgs {
+  const float* r;
+  const float* v;
+  const uint8_t* done;
+  const float* last_v;       // [N]
+  float* adv;
+  float* ret;
+  long long in_ts, in_es;    // element (t, e) of r / v / done at t*in_ts + e*in_es
+  long long out_ts, out_es;  // element (t, e) of adv / ret
+  int T, N;
+  float gamma, lam;
+  const int* guard;
+};
+
+struct AdvNormArgs {
+  float* x;
+  float* part;   // [nparts] sums
+  float* part2;  // [nparts] sums of squared deviations
+  const int* guard;
+  long long n;
+  int nparts;
+  int chunk;     // elements per block
+  int phase;     // 0: sums, 1: squared deviations, 2: apply
+};
+
+struct EluBwdArgs {
+  float* g;
+  const float* y;
+  long long rows;
+  int cols, ldg, ldy;
+  const int* guard;
+};
+
+struct RowSumArgs {
+  float* out;
+  const float* x;
+  int rows, cols, ldx;
+  const int* guard;
+};
+
+struct CopyRowsArgs {
+  float* dst;
+  const float* src;
+  const int* perm;  // source row = perm ? perm[row0 + r] : row0 + r
+  long long rows;
+  int cols, ldd, lds, row0;
+  int zero_pad;     // write 0 to columns [cols, ldd); otherwise leave them
+  const int* guard;
+};
+
+struct SampleArgs {
+  const float* mean;  // [rows x ldm]
+  const float* log_std;
+  const float* eps;   // [rows x lde]
+  float* action;      // [rows x lda]
+  float* logp;        // [rows]
+  int rows, A, ldm, lde, lda;
+  const int* guard;
+};
+
+struct ClampArgs {
+  float* x;
+  int n;
+  float lo, hi;
+  const int* guard;
+};
+
+}  // namespace zk

@@ -1,0 +1,1074 @@
+// mlp_ppo.cpp — the GpuMlp equivalent (zl_mlp) and the whole PPO update
+// (zl_ppo) on one device-resident flat parameter buffer.
+//
+// HBM layout. All parameters of an update live in ONE flat fp32 buffer:
+//   actor  w[0] b[0] w[1] b[1] ... | critic w[0] b[0] ... | log_std
+// with every tensor start aligned to 64 floats (256 B) and w[l] stored
+// [dims[l+1] x ldw] with ldw = dims[l] rounded up to 4, so every GEMM operand
+// row is 16-byte aligned for float4 loads. Gradients and the two Adam moments
+// use the same layout, so the optimiser is one flat, vectorised pass (one
+// launch for all 2L + 2L + 1 tensors) and the grad-norm clip is a reduction
+// over two contiguous ranges. Padding stays zero forever (zero grads give a
+// zero Adam update). Activations are batch-major [rows x ld] with ld the
+// feature count rounded up to 4.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace zl {
+
+zl_status adv_normalize_into(zl_ctx* c, float* adv, long long n, float* scratch, int nparts,
+                             int chunk, const int* guard);
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Offsets of one MLP's tensors inside the flat buffer.
+struct NetLayout {
+  std::vector<int> dims;
+  int L = 0;
+  std::vector<long long> w_off, b_off;
+  std::vector<int> ldw;
+  long long begin = 0, end = 0;
+  long long packed = 0;  // parameter count in the packed (reference) layout
+
+  void build(const int* d, int nd, long long start) {
+    dims.assign(d, d + nd);
+    L = nd - 1;
+    w_off.resize(L);
+    b_off.resize(L);
+    ldw.resize(L);
+    begin = start;
+    long long cur = start;
+    packed = 0;
+    for (int l = 0; l < L; ++l) {
+      ldw[l] = (int)round_up(dims[l], 4);
+      w_off[l] = cur;
+      cur += round_up((long long)dims[l + 1] * ldw[l], 64);
+      b_off[l] = cur;
+      cur += round_up(dims[l + 1], 64);
+      packed += (long long)dims[l + 1] * dims[l] + dims[l + 1];
+    }
+    end = cur;
+  }
+  // Packed (w[0], b[0], w[1], ...; w[l] row-major [out x in]) <-> flat.
+  void scatter(const float* packed_src, float* flat) const {
+    for (int l = 0; l < L; ++l) {
+      const int out = dims[l + 1], in = dims[l];
+      for (int o = 0; o < out; ++o)
+        std::memcpy(flat + w_off[l] + (long long)o * ldw[l], packed_src + (long long)o * in,
+                    (size_t)in * 4);
+      packed_src += (long long)out * in;
+      std::memcpy(flat + b_off[l], packed_src, (size_t)out * 4);
+      packed_src += out;
+    }
+  }
+  void gather(const float* flat, float* packed_dst) const {
+    for (int l = 0; l < L; ++l) {
+      const int out = dims[l + 1], in = dims[l];
+      for (int o = 0; o < out; ++o)
+        std::memcpy(packed_dst + (long long)o * in, flat + w_off[l] + (long long)o * ldw[l],
+                    (size_t)in * 4);
+      packed_dst += (long long)out * in;
+      std::memcpy(packed_dst, flat + b_off[l], (size_t)out * 4);
+      packed_dst += out;
+    }
+  }
+};
+
+// Per-row activation and delta buffers of one MLP for up to `rows` rows.
+struct NetBuffers {
+  int rows = 0;
+  std::vector<float*> act;    // act[l], l = 1..L: [rows x ld[l]]
+  std::vector<int> ld;        // ld[l] = dims[l] rounded up to 4
+  std::vector<float*> delta;  // delta[l], l = 0..L-1: [rows x ld[l+1]] (dL/dz_l)
+
+  zl_status alloc(zl_ctx* c, const NetLayout& nl, int r) {
+    rows = r;
+    act.assign(nl.L + 1, nullptr);
+    delta.assign(nl.L, nullptr);
+    ld.assign(nl.L + 1, 0);
+    for (int l = 0; l <= nl.L; ++l) ld[l] = (int)round_up(nl.dims[l], 4);
+    for (int l = 1; l <= nl.L; ++l)
+      ZL_HIP(c, hipMalloc((void**)&act[l], (size_t)r * ld[l] * 4));
+    for (int l = 0; l < nl.L; ++l)
+      ZL_HIP(c, hipMalloc((void**)&delta[l], (size_t)r * ld[l + 1] * 4));
+    return ZL_OK;
+  }
+  void release() {
+    for (float* p : act)
+      if (p) hipFree(p);
+    for (float* p : delta)
+      if (p) hipFree(p);
+    act.clear();
+    delta.clear();
+  }
+};
+
+static size_t net_ws_floats(const NetLayout& nl, int rows) {
+  size_t w = 0;
+  for (int l = 0; l < nl.L; ++l)
+    w = std::max(w, gemm_ws_floats(nl.dims[l + 1], nl.dims[l], rows, false, false, zk::kEpiStore));
+  return w;
+}
+
+// Forward of GpuMlp::forward (src/bin/biped_train_gpu.rs:364-422): one fused
+// GEMM + bias + ELU launch per layer, linear last layer (zealot-rl/src/net.rs:88-108).
+static zl_status net_forward(zl_ctx* c, const NetLayout& nl, const NetBuffers& nb,
+                             const float* params, const float* x, int ldx, const int* permx,
+                             int rows, const int* guard) {
+  for (int l = 0; l < nl.L; ++l) {
+    GemmDesc d;
+    d.A = l == 0 ? x : nb.act[l];
+    d.lda = l == 0 ? ldx : nb.ld[l];
+    d.a_kc = true;
+    d.permA = l == 0 ? permx : nullptr;
+    d.B = params + nl.w_off[l];
+    d.ldb = nl.ldw[l];
+    d.b_kc = true;
+    d.C = nb.act[l + 1];
+    d.ldc = nb.ld[l + 1];
+    d.M = rows;
+    d.N = nl.dims[l + 1];
+    d.K = nl.dims[l];
+    d.epi = zk::kEpiBiasN;
+    d.bias = params + nl.b_off[l];
+    d.act = l < nl.L - 1 ? 1 : 0;
+    d.guard = guard;
+    zl_status s = run_gemm(c, d);
+    if (s) return s;
+  }
+  return ZL_OK;
+}
+
+// Backward of GpuMlp::backward (src/bin/biped_train_gpu.rs:423-500) with the
+// math of zealot-rl/src/net.rs:113-140: per layer the weight gradient
+// dW = delta^T . a (split-K over the rows, fixed-order reduction) with the
+// bias gradient as the row sums of delta^T fused in, then (l > 0) the data
+// gradient delta_{l-1} = (delta_l . W_l) * elu'(a_l) with ELU' fused into the
+// GEMM epilogue. `top` is dL/dz of the output layer.
+static zl_status net_backward(zl_ctx* c, const NetLayout& nl, const NetBuffers& nb,
+                              const float* params, float* grads, const float* x, int ldx,
+                              const int* permx, int rows, const float* top, int ld_top,
+                              const int* guard, float* ws, size_t ws_floats) {
+  for (int l = nl.L - 1; l >= 0; --l) {
+    const float* dl = l == nl.L - 1 ? top : nb.delta[l];
+    const int ldd = l == nl.L - 1 ? ld_top : nb.ld[l + 1];
+    GemmDesc w;
+    w.A = dl;
+    w.lda = ldd;
+    w.a_kc = false;
+    w.B = l == 0 ? x : nb.act[l];
+    w.ldb = l == 0 ? ldx : nb.ld[l];
+    w.b_kc = false;
+    w.permB = l == 0 ? permx : nullptr;
+    w.C = grads + nl.w_off[l];
+    w.ldc = nl.ldw[l];
+    w.M = nl.dims[l + 1];
+    w.N = nl.dims[l];
+    w.K = rows;
+    w.rowsum_out = grads + nl.b_off[l];
+    w.guard = guard;
+    w.ws = ws;
+    w.ws_floats = ws_floats;
+    zl_status s = run_gemm(c, w);
+    if (s) return s;
+    if (l > 0) {
+      GemmDesc d;
+      d.A = dl;
+      d.lda = ldd;
+      d.a_kc = true;
+      d.B = params + nl.w_off[l];
+      d.ldb = nl.ldw[l];
+      d.b_kc = false;
+      d.C = nb.delta[l - 1];
+      d.ldc = nb.ld[l];
+      d.M = rows;
+      d.N = nl.dims[l];
+      d.K = nl.dims[l + 1];
+      d.epi = zk::kEpiEluGrad;
+      d.Y = nb.act[l];
+      d.ldy = nb.ld[l];
+      d.guard = guard;
+      s = run_gemm(c, d);
+      if (s) return s;
+    }
+  }
+  return ZL_OK;
+}
+
+static zl_status copy_rows(zl_ctx* c, float* dst, int ldd, const float* src, int lds, int cols,
+                           long long rows, const int* perm, int row0, const int* guard,
+                           bool zero_pad) {
+  zk::CopyRowsArgs a{};
+  a.dst = dst;
+  a.src = src;
+  a.perm = perm;
+  a.rows = rows;
+  a.cols = cols;
+  a.ldd = ldd;
+  a.lds = lds;
+  a.row0 = row0;
+  a.zero_pad = zero_pad ? 1 : 0;
+  a.guard = guard;
+  return launch(c, K_COPY_ROWS, (unsigned)cdiv(rows * ldd, kThreads), 1, 1, a);
+}
+
+// zealot-rl/src/rng.rs:13-31 (only unit() is needed for the shuffle).
+struct Lcg {
+  uint64_t s;
+  explicit Lcg(uint64_t seed) : s(seed | 1ULL) {}
+  float unit() {
+    s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+    return (float)(s >> 40) / (float)(1ULL << 24);
+  }
+};
+
+}  // namespace zl
+
+using namespace zl;
+
+// ================================================================== zl_mlp
+
+struct zl_mlp {
+  zl_ctx* c = nullptr;
+  NetLayout nl;
+  NetBuffers nb;
+  long long nflat = 0;
+  float *params = nullptr, *grads = nullptr, *m = nullptr, *v = nullptr;
+  float* ws = nullptr;
+  size_t ws_floats = 0;
+  const float* x = nullptr;
+  int ldx = 0, rows = 0;
+};
+
+extern "C" {
+
+zl_status zl_mlp_create(zl_ctx* c, const int* dims, int nd, int batch, zl_mlp** out) {
+  if (!c || !dims || !out || nd < 2 || batch < 1) return ZL_ERR_INVALID;
+  *out = nullptr;
+  for (int i = 0; i < nd; ++i)
+    if (dims[i] < 1) return fail(c, ZL_ERR_INVALID, "zl_mlp_create: dims[%d] = %d", i, dims[i]);
+  zl_mlp* p = new zl_mlp();
+  p->c = c;
+  p->nl.build(dims, nd, 0);
+  p->nflat = p->nl.end;
+  const size_t bytes = (size_t)p->nflat * 4;
+  hipError_t e = hipSuccess;
+  for (float** b : {&p->params, &p->grads, &p->m, &p->v}) {
+    if (e == hipSuccess) e = hipMalloc((void**)b, bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(*b, 0, bytes, c->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  zl_status s = e == hipSuccess ? ZL_OK : fail(c, ZL_ERR_HIP, "zl_mlp_create: %s", hipGetErrorString(e));
+  if (!s) s = p->nb.alloc(c, p->nl, batch);
+  if (!s) {
+    p->ws_floats = std::max<size_t>(net_ws_floats(p->nl, batch), 1);
+    if (hipMalloc((void**)&p->ws, p->ws_floats * 4) != hipSuccess)
+      s = fail(c, ZL_ERR_HIP, "zl_mlp_create: scratch alloc failed");
+  }
+  if (s) {
+    zl_mlp_destroy(p);
+    return s;
+  }
+  *out = p;
+  return ZL_OK;
+}
+
+void zl_mlp_destroy(zl_mlp* p) {
+  if (!p) return;
+  if (p->c && p->c->stream) hipStreamSynchronize(p->c->stream);
+  p->nb.release();
+  for (float* b : {p->params, p->grads, p->m, p->v, p->ws})
+    if (b) hipFree(b);
+  delete p;
+}
+
+long long zl_mlp_num_params(const zl_mlp* p) { return p ? p->nl.packed : -1; }
+
+static zl_status flat_upload(zl_ctx* c, const NetLayout& nl, long long nflat, float* dev,
+                             const float* packed) {
+  std::vector<float> host((size_t)nflat, 0.0f);
+  nl.scatter(packed, host.data());
+  ZL_HIP(c, hipMemcpyAsync(dev, host.data(), host.size() * 4, hipMemcpyHostToDevice, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  return ZL_OK;
+}
+
+static zl_status flat_download(zl_ctx* c, const NetLayout& nl, long long nflat, const float* dev,
+                               float* packed) {
+  std::vector<float> host((size_t)nflat);
+  ZL_HIP(c, hipMemcpyAsync(host.data(), dev, host.size() * 4, hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  nl.gather(host.data(), packed);
+  return ZL_OK;
+}
+
+zl_status zl_mlp_write_weights(zl_mlp* p, const float* packed) {
+  if (!p || !packed) return ZL_ERR_INVALID;
+  return flat_upload(p->c, p->nl, p->nflat, p->params, packed);
+}
+
+zl_status zl_mlp_read_weights(zl_mlp* p, float* packed) {
+  if (!p || !packed) return ZL_ERR_INVALID;
+  return flat_download(p->c, p->nl, p->nflat, p->params, packed);
+}
+
+zl_status zl_mlp_read_grads(zl_mlp* p, float* packed) {
+  if (!p || !packed) return ZL_ERR_INVALID;
+  return flat_download(p->c, p->nl, p->nflat, p->grads, packed);
+}
+
+zl_status zl_mlp_read_moments(zl_mlp* p, float* mh, float* vh) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_status s = ZL_OK;
+  if (mh) s = flat_download(p->c, p->nl, p->nflat, p->m, mh);
+  if (!s && vh) s = flat_download(p->c, p->nl, p->nflat, p->v, vh);
+  return s;
+}
+
+zl_status zl_mlp_write_moments(zl_mlp* p, const float* mh, const float* vh) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_status s = ZL_OK;
+  if (mh) s = flat_upload(p->c, p->nl, p->nflat, p->m, mh);
+  if (!s && vh) s = flat_upload(p->c, p->nl, p->nflat, p->v, vh);
+  return s;
+}
+
+zl_status zl_mlp_forward(zl_mlp* p, const float* x, int ldx, int rows) {
+  if (!p) return ZL_ERR_INVALID;
+  if (!x || rows < 1 || rows > p->nb.rows || ldx < p->nl.dims[0])
+    return fail(p->c, ZL_ERR_INVALID, "zl_mlp_forward: rows %d (batch %d), ldx %d", rows,
+                p->nb.rows, ldx);
+  p->x = x;
+  p->ldx = ldx;
+  p->rows = rows;
+  return net_forward(p->c, p->nl, p->nb, p->params, x, ldx, nullptr, rows, nullptr);
+}
+
+const float* zl_mlp_output(const zl_mlp* p, int* ld_out) {
+  if (!p) return nullptr;
+  if (ld_out) *ld_out = p->nb.ld[p->nl.L];
+  return p->nb.act[p->nl.L];
+}
+
+zl_status zl_mlp_backward(zl_mlp* p, const float* g_out, int ld_g) {
+  if (!p) return ZL_ERR_INVALID;
+  if (!g_out || !p->x || ld_g < p->nl.dims[p->nl.L])
+    return fail(p->c, ZL_ERR_INVALID, "zl_mlp_backward: no forward or bad gradient");
+  return net_backward(p->c, p->nl, p->nb, p->params, p->grads, p->x, p->ldx, nullptr, p->rows,
+                      g_out, ld_g, nullptr, p->ws, p->ws_floats);
+}
+
+zl_status zl_mlp_adam(zl_mlp* p, float lr, float bc1, float bc2) {
+  if (!p) return ZL_ERR_INVALID;
+  return zl_adam_step(p->c, p->params, p->grads, p->m, p->v, (size_t)p->nflat, lr, 0.9f, 0.999f,
+                      1e-8f, bc1, bc2);
+}
+
+}  // extern "C"
+
+// ================================================================== zl_ppo
+
+struct zl_ppo {
+  zl_ctx* c = nullptr;
+  NetLayout actor, critic;
+  long long ls_off = 0;
+  int A = 0;
+  long long nflat = 0;
+  float *params = nullptr, *grads = nullptr, *m = nullptr, *v = nullptr;
+  NetBuffers ab, cb;
+  int mb_cap = 0;
+  float* ws = nullptr;
+  size_t ws_floats = 0;
+  // Reduction partials.
+  float* gls_part = nullptr;  // [nb x A]
+  float* astat_part = nullptr;
+  float* vstat_part = nullptr;
+  float* sq_part = nullptr;
+  float* kl_part = nullptr;
+  float* adv_part = nullptr;
+  int nb_cap = 0, nsq_a = 0, nsq = 0;
+  static constexpr int kSqChunk = 4096;
+  static constexpr int kAdvChunk = 4096;
+  size_t adv_part_cap = 0;
+  zk::DevState* dstate = nullptr;
+  float* ls_old = nullptr;
+  float* stat_out = nullptr;  // [8] scratch for zl_ppo_minibatch_grads
+  // Observation staging (padded, 16-byte aligned rows) and shuffle orders.
+  float* obs_pad = nullptr;
+  size_t obs_pad_floats = 0;
+  float* cobs_pad = nullptr;
+  size_t cobs_pad_floats = 0;
+  int* perm = nullptr;
+  size_t perm_cap = 0;
+  std::vector<int> perm_host;
+  zk::DevState hstate{};
+  // Captured update graph and the signature it was captured for.
+  hipGraphExec_t gexec = nullptr;
+  std::string gkey;
+};
+
+namespace {
+
+zl_status grow(zl_ctx* c, void** p, size_t* cap, size_t bytes) {
+  if (bytes <= *cap) return ZL_OK;
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  if (*p) ZL_HIP(c, hipFree(*p));
+  *p = nullptr;
+  *cap = 0;
+  ZL_HIP(c, hipMalloc(p, bytes));
+  *cap = bytes;
+  return ZL_OK;
+}
+
+struct Plan {
+  int mode, mb, n_mb, epochs;
+  long long n;
+  bool stage_obs, stage_cobs, share_cobs, shuffle;
+  const float* X;
+  int ldx;
+  const float* XC;
+  int ldxc;
+  zk::PpoParams pp;
+};
+
+zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg, const Plan& pl) {
+  zl_ctx* c = p->c;
+  const int* guard = &p->dstate->active;
+  const int A = p->A;
+  zl_status s = ZL_OK;
+  if (cfg->normalize_adv) {
+    const int nparts = (int)cdiv(pl.n, zl_ppo::kAdvChunk);
+    s = adv_normalize_into(c, b->adv, pl.n, p->adv_part, nparts, zl_ppo::kAdvChunk, guard);
+    if (s) return s;
+  }
+  if (pl.stage_obs) {
+    s = copy_rows(c, p->obs_pad, pl.ldx, b->obs, b->ld_obs, p->actor.dims[0], pl.n, nullptr, 0,
+                  guard, true);
+    if (s) return s;
+  }
+  if (pl.stage_cobs && !pl.share_cobs) {
+    s = copy_rows(c, p->cobs_pad, pl.ldxc, b->critic_obs, b->ld_critic_obs, p->critic.dims[0],
+                  pl.n, nullptr, 0, guard, true);
+    if (s) return s;
+  }
+  const int La = p->actor.L, Lc = p->critic.L;
+  const int nb = (int)cdiv(pl.mb, kThreads);
+  const unsigned shm = (unsigned)((kThreads * A + kThreads) * 4);
+  const float* log_std = p->params + p->ls_off;
+  for (int e = 0; e < pl.epochs; ++e) {
+    zk::EpochBeginArgs eb{};
+    eb.st = p->dstate;
+    eb.guard = guard;
+    eb.pp = pl.pp;
+    if ((s = launch(c, K_EPOCH_BEGIN, 1, 1, 1, eb))) return s;
+    const int* perm_e = pl.shuffle ? p->perm + (size_t)e * pl.n : nullptr;
+    for (int k = 0; k < pl.n_mb; ++k) {
+      const int row0 = k * pl.mb;
+      const int* px = perm_e ? perm_e + row0 : nullptr;
+      const float* xa = perm_e ? pl.X : pl.X + (size_t)row0 * pl.ldx;
+      const float* xc = perm_e ? pl.XC : pl.XC + (size_t)row0 * pl.ldxc;
+      if ((s = net_forward(c, p->actor, p->ab, p->params, xa, pl.ldx, px, pl.mb, guard))) return s;
+      if ((s = net_forward(c, p->critic, p->cb, p->params, xc, pl.ldxc, px, pl.mb, guard)))
+        return s;
+      zk::ActorLossArgs al{};
+      al.mean = p->ab.act[La];
+      al.ldm = p->ab.ld[La];
+      al.action = b->action;
+      al.ldact = b->ld_action;
+      al.adv = b->adv;
+      al.logp_old = b->logp_old;
+      al.mean_old = b->mean_old;
+      al.ldmo = b->ld_mean_old;
+      al.log_std = log_std;
+      al.perm = perm_e;
+      al.row0 = row0;
+      al.rows = pl.mb;
+      al.A = A;
+      al.delta = p->ab.delta[La - 1];
+      al.ldd = p->ab.ld[La];
+      al.gls_part = p->gls_part;
+      al.stat_part = p->astat_part;
+      al.guard = guard;
+      al.clip = cfg->clip;
+      al.entropy_coef = cfg->entropy_coef;
+      al.scale = pl.pp.scale;
+      if ((s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, al, shm))) return s;
+      zk::ValueLossArgs vl{};
+      vl.v = p->cb.act[Lc];
+      vl.ldv = p->cb.ld[Lc];
+      vl.value_old = b->value_old;
+      vl.ret = b->ret;
+      vl.perm = perm_e;
+      vl.row0 = row0;
+      vl.rows = pl.mb;
+      vl.delta = p->cb.delta[Lc - 1];
+      vl.ldd = p->cb.ld[Lc];
+      vl.stat_part = p->vstat_part;
+      vl.guard = guard;
+      vl.clip = cfg->clip;
+      vl.value_coef = cfg->value_coef;
+      vl.scale = pl.pp.scale;
+      if ((s = launch(c, K_VALUE_LOSS, (unsigned)nb, 1, 1, vl))) return s;
+      if ((s = net_backward(c, p->actor, p->ab, p->params, p->grads, xa, pl.ldx, px, pl.mb,
+                            p->ab.delta[La - 1], p->ab.ld[La], guard, p->ws, p->ws_floats)))
+        return s;
+      if ((s = net_backward(c, p->critic, p->cb, p->params, p->grads, xc, pl.ldxc, px, pl.mb,
+                            p->cb.delta[Lc - 1], p->cb.ld[Lc], guard, p->ws, p->ws_floats)))
+        return s;
+      zk::SumsqArgs sq{};
+      sq.x = p->grads;
+      sq.part = p->sq_part;
+      sq.guard = guard;
+      sq.off0 = p->actor.begin;
+      sq.len0 = p->actor.end - p->actor.begin;
+      sq.off1 = p->critic.begin;
+      sq.len1 = p->critic.end - p->critic.begin;
+      sq.blocks0 = p->nsq_a;
+      sq.chunk = zl_ppo::kSqChunk;
+      if ((s = launch(c, K_SUMSQ, (unsigned)p->nsq, 1, 1, sq))) return s;
+      zk::FinalizeArgs fz{};
+      fz.st = p->dstate;
+      fz.gls_part = p->gls_part;
+      fz.astat_part = p->astat_part;
+      fz.vstat_part = p->vstat_part;
+      fz.sq_part = p->sq_part;
+      fz.log_std = log_std;
+      fz.g_logstd = p->grads + p->ls_off;
+      fz.guard = guard;
+      fz.pp = pl.pp;
+      fz.nb_a = nb;
+      fz.nb_v = nb;
+      fz.nsq = p->nsq;
+      fz.nsq_a = p->nsq_a;
+      if ((s = launch(c, K_FINALIZE, 1, 1, 1, fz))) return s;
+      zk::AdamArgs ad{};
+      ad.p = p->params;
+      ad.g = p->grads;
+      ad.m = p->m;
+      ad.v = p->v;
+      ad.st = p->dstate;
+      ad.guard = guard;
+      ad.n = p->nflat;
+      ad.end_a = p->critic.begin;
+      ad.end_c = p->ls_off;
+      ad.beta1 = pl.pp.beta1;
+      ad.beta2 = pl.pp.beta2;
+      ad.eps = pl.pp.eps;
+      ad.clamp_ls = pl.pp.clamp_ls;
+      if ((s = launch(c, K_ADAM, (unsigned)cdiv(p->nflat, 4 * kThreads), 1, 1, ad))) return s;
+    }
+    const bool trainer_kl = pl.mode == ZL_SEMANTICS_GPU_TRAINER && b->mean_old != nullptr;
+    if (trainer_kl) {  // src/bin/biped_train_gpu.rs:1469-1492 (last minibatch)
+      zk::KlArgs kl{};
+      kl.mean = p->ab.act[La];
+      kl.ldm = p->ab.ld[La];
+      kl.mean_old = b->mean_old;
+      kl.ldmo = b->ld_mean_old;
+      kl.log_std = log_std;
+      kl.log_std_old = p->ls_old;
+      kl.perm = nullptr;
+      kl.row0 = (pl.n_mb - 1) * pl.mb;
+      kl.rows = pl.mb;
+      kl.A = A;
+      kl.part = p->kl_part;
+      kl.guard = guard;
+      if ((s = launch(c, K_KL, (unsigned)nb, 1, 1, kl))) return s;
+    }
+    zk::EpochEndArgs ee{};
+    ee.st = p->dstate;
+    ee.kl_part = trainer_kl ? p->kl_part : nullptr;
+    ee.active = &p->dstate->active;
+    ee.pp = pl.pp;
+    ee.nkl = nb;
+    if ((s = launch(c, K_EPOCH_END, 1, 1, 1, ee))) return s;
+  }
+  if (pl.mode == ZL_SEMANTICS_GPU_TRAINER && cfg->clamp_log_std) {
+    // src/bin/biped_train_gpu.rs:1529-1541, after the epoch loop (even after an early stop).
+    zk::ClampArgs cl{};
+    cl.x = p->params + p->ls_off;
+    cl.n = A;
+    cl.lo = -1.6f;
+    cl.hi = 0.0f;
+    if ((s = launch(c, K_CLAMP, 1, 1, 1, cl))) return s;
+  }
+  return ZL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, int nc, int mb,
+                        zl_ppo** out) {
+  if (!c || !adims || !cdims || !out || na < 2 || nc < 2 || mb < 1) return ZL_ERR_INVALID;
+  *out = nullptr;
+  for (int i = 0; i < na; ++i)
+    if (adims[i] < 1) return fail(c, ZL_ERR_INVALID, "zl_ppo_create: actor dims[%d] = %d", i, adims[i]);
+  for (int i = 0; i < nc; ++i)
+    if (cdims[i] < 1) return fail(c, ZL_ERR_INVALID, "zl_ppo_create: critic dims[%d] = %d", i, cdims[i]);
+  if (cdims[nc - 1] != 1)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_create: critic must output a scalar");  // ppo.rs:242-246
+  if (adims[na - 1] > 48)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_create: action dim %d > 48", adims[na - 1]);
+  zl_ppo* p = new zl_ppo();
+  p->c = c;
+  p->actor.build(adims, na, 0);
+  p->critic.build(cdims, nc, p->actor.end);
+  p->A = adims[na - 1];
+  p->ls_off = p->critic.end;
+  p->nflat = p->ls_off + round_up(p->A, 64);
+  p->mb_cap = mb;
+  const size_t bytes = (size_t)p->nflat * 4;
+  zl_status s = ZL_OK;
+  auto dalloc = [&](void** ptr, size_t nbytes) {
+    if (s) return;
+    hipError_t e = hipMalloc(ptr, std::max<size_t>(nbytes, 4));
+    if (e == hipSuccess) e = hipMemsetAsync(*ptr, 0, std::max<size_t>(nbytes, 4), c->stream);
+    if (e != hipSuccess) s = fail(c, ZL_ERR_HIP, "zl_ppo_create: %s", hipGetErrorString(e));
+  };
+  dalloc((void**)&p->params, bytes);
+  dalloc((void**)&p->grads, bytes);
+  dalloc((void**)&p->m, bytes);
+  dalloc((void**)&p->v, bytes);
+  if (!s) s = p->ab.alloc(c, p->actor, mb);
+  if (!s) s = p->cb.alloc(c, p->critic, mb);
+  p->ws_floats = std::max<size_t>(std::max(net_ws_floats(p->actor, mb), net_ws_floats(p->critic, mb)), 1);
+  dalloc((void**)&p->ws, p->ws_floats * 4);
+  p->nb_cap = (int)cdiv(mb, kThreads);
+  dalloc((void**)&p->gls_part, (size_t)p->nb_cap * p->A * 4);
+  dalloc((void**)&p->astat_part, (size_t)p->nb_cap * 2 * 4);
+  dalloc((void**)&p->vstat_part, (size_t)p->nb_cap * 4);
+  dalloc((void**)&p->kl_part, (size_t)p->nb_cap * 4);
+  p->nsq_a = (int)cdiv(p->actor.end - p->actor.begin, zl_ppo::kSqChunk);
+  p->nsq = p->nsq_a + (int)cdiv(p->critic.end - p->critic.begin, zl_ppo::kSqChunk);
+  dalloc((void**)&p->sq_part, (size_t)p->nsq * 4);
+  dalloc((void**)&p->dstate, sizeof(zk::DevState));
+  dalloc((void**)&p->ls_old, (size_t)p->A * 4);
+  dalloc((void**)&p->stat_out, 8 * 4);
+  if (!s && hipStreamSynchronize(c->stream) != hipSuccess)
+    s = fail(c, ZL_ERR_HIP, "zl_ppo_create: stream sync failed");
+  if (s) {
+    zl_ppo_destroy(p);
+    return s;
+  }
+  p->hstate = zk::DevState{};
+  p->hstate.lr = 1e-3f;
+  *out = p;
+  return ZL_OK;
+}
+
+void zl_ppo_destroy(zl_ppo* p) {
+  if (!p) return;
+  if (p->c && p->c->stream) hipStreamSynchronize(p->c->stream);
+  if (p->gexec) hipGraphExecDestroy(p->gexec);
+  p->ab.release();
+  p->cb.release();
+  for (void* b : {(void*)p->params, (void*)p->grads, (void*)p->m, (void*)p->v, (void*)p->ws,
+                  (void*)p->gls_part, (void*)p->astat_part, (void*)p->vstat_part,
+                  (void*)p->kl_part, (void*)p->sq_part, (void*)p->adv_part, (void*)p->dstate,
+                  (void*)p->ls_old, (void*)p->obs_pad, (void*)p->cobs_pad, (void*)p->perm,
+                  (void*)p->stat_out})
+    if (b) hipFree(b);
+  delete p;
+}
+
+zl_status zl_ppo_set_params(zl_ppo* p, const float* actor, const float* critic,
+                            const float* log_std, float lr) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  std::vector<float> host((size_t)p->nflat, 0.0f);
+  ZL_HIP(c, hipMemcpyAsync(host.data(), p->params, host.size() * 4, hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  if (actor) p->actor.scatter(actor, host.data());
+  if (critic) p->critic.scatter(critic, host.data());
+  if (log_std) std::memcpy(host.data() + p->ls_off, log_std, (size_t)p->A * 4);
+  ZL_HIP(c, hipMemcpyAsync(p->params, host.data(), host.size() * 4, hipMemcpyHostToDevice, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  p->hstate.lr = lr;
+  return ZL_OK;
+}
+
+zl_status zl_ppo_get_params(zl_ppo* p, float* actor, float* critic, float* log_std, float* lr) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  std::vector<float> host((size_t)p->nflat);
+  ZL_HIP(c, hipMemcpyAsync(host.data(), p->params, host.size() * 4, hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  if (actor) p->actor.gather(host.data(), actor);
+  if (critic) p->critic.gather(host.data(), critic);
+  if (log_std) std::memcpy(log_std, host.data() + p->ls_off, (size_t)p->A * 4);
+  if (lr) *lr = p->hstate.lr;
+  return ZL_OK;
+}
+
+zl_status zl_ppo_get_moments(zl_ppo* p, float* ma, float* va, float* mc, float* vc, float* mls,
+                             float* vls) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  std::vector<float> hm((size_t)p->nflat), hv((size_t)p->nflat);
+  ZL_HIP(c, hipMemcpyAsync(hm.data(), p->m, hm.size() * 4, hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipMemcpyAsync(hv.data(), p->v, hv.size() * 4, hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  if (ma) p->actor.gather(hm.data(), ma);
+  if (va) p->actor.gather(hv.data(), va);
+  if (mc) p->critic.gather(hm.data(), mc);
+  if (vc) p->critic.gather(hv.data(), vc);
+  if (mls) std::memcpy(mls, hm.data() + p->ls_off, (size_t)p->A * 4);
+  if (vls) std::memcpy(vls, hv.data() + p->ls_off, (size_t)p->A * 4);
+  return ZL_OK;
+}
+
+zl_status zl_ppo_reset_optimizer(zl_ppo* p) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  ZL_HIP(c, hipMemsetAsync(p->m, 0, (size_t)p->nflat * 4, c->stream));
+  ZL_HIP(c, hipMemsetAsync(p->v, 0, (size_t)p->nflat * 4, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  p->hstate.t = 0;
+  p->hstate.gstep = 0;
+  return ZL_OK;
+}
+
+zl_status zl_ppo_get_counters(zl_ppo* p, int* t, unsigned long long* gstep) {
+  if (!p) return ZL_ERR_INVALID;
+  if (t) *t = p->hstate.t;
+  if (gstep) *gstep = p->hstate.gstep;
+  return ZL_OK;
+}
+
+zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
+                        zl_ppo_stats* stats) {
+  if (!p || !b || !cfg) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  const int mode = cfg->semantics;
+  if (mode != ZL_SEMANTICS_ACTOR_CRITIC && mode != ZL_SEMANTICS_GPU_TRAINER)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_update: unknown semantics %d", mode);
+  if (!b->obs || !b->critic_obs || !b->action || !b->logp_old || !b->value_old || !b->adv ||
+      !b->ret)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_update: null batch pointer");
+  if (cfg->epochs < 0 || cfg->minibatches < 1 || b->n < cfg->minibatches)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_update: n %lld < minibatches %d", b->n, cfg->minibatches);
+  if (b->ld_obs < p->actor.dims[0] || b->ld_critic_obs < p->critic.dims[0] ||
+      b->ld_action < p->A || (b->mean_old && b->ld_mean_old < p->A))
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_update: row stride smaller than the row");
+  if (b->n > (1LL << 31) - 1) return fail(c, ZL_ERR_INVALID, "zl_ppo_update: n too large");
+  Plan pl{};
+  pl.mode = mode;
+  pl.n = b->n;
+  pl.epochs = cfg->epochs;
+  pl.mb = (int)(b->n / cfg->minibatches);  // ppo.rs:350; biped_train_gpu.rs:645
+  pl.n_mb = mode == ZL_SEMANTICS_ACTOR_CRITIC ? cfg->minibatches : (int)(b->n / pl.mb);  // :1005
+  if (pl.mb > p->mb_cap)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_update: minibatch of %d rows > capacity %d", pl.mb,
+                p->mb_cap);
+  pl.shuffle = mode == ZL_SEMANTICS_ACTOR_CRITIC && cfg->shuffle;
+  // Observation staging: layer-0 operands need 16-byte aligned rows.
+  const int od = p->actor.dims[0], cd = p->critic.dims[0];
+  const int odp = (int)round_up(od, 4), cdp = (int)round_up(cd, 4);
+  pl.stage_obs = !(aligned16(b->obs) && b->ld_obs % 4 == 0);
+  pl.stage_cobs = !(aligned16(b->critic_obs) && b->ld_critic_obs % 4 == 0);
+  pl.share_cobs = pl.stage_obs && pl.stage_cobs && b->critic_obs == b->obs &&
+                  b->ld_critic_obs == b->ld_obs && od == cd;
+  zl_status s = ZL_OK;
+  if (pl.stage_obs) {
+    size_t cap = p->obs_pad_floats * 4;
+    if ((s = grow(c, (void**)&p->obs_pad, &cap, (size_t)pl.n * odp * 4))) return s;
+    p->obs_pad_floats = cap / 4;
+    pl.X = p->obs_pad;
+    pl.ldx = odp;
+  } else {
+    pl.X = b->obs;
+    pl.ldx = b->ld_obs;
+  }
+  if (pl.stage_cobs) {
+    if (pl.share_cobs) {
+      pl.XC = p->obs_pad;
+      pl.ldxc = odp;
+    } else {
+      size_t cap = p->cobs_pad_floats * 4;
+      if ((s = grow(c, (void**)&p->cobs_pad, &cap, (size_t)pl.n * cdp * 4))) return s;
+      p->cobs_pad_floats = cap / 4;
+      pl.XC = p->cobs_pad;
+      pl.ldxc = cdp;
+    }
+  } else {
+    pl.XC = b->critic_obs;
+    pl.ldxc = b->ld_critic_obs;
+  }
+  if (cfg->normalize_adv) {
+    size_t need = (size_t)2 * cdiv(pl.n, zl_ppo::kAdvChunk) * 4;
+    if ((s = grow(c, (void**)&p->adv_part, &p->adv_part_cap, need))) return s;
+  }
+  if (pl.shuffle) {
+    size_t cap = p->perm_cap * 4;
+    if ((s = grow(c, (void**)&p->perm, &cap, (size_t)pl.epochs * pl.n * 4 + 4))) return s;
+    p->perm_cap = cap / 4;
+    // Per-epoch Fisher-Yates with Lcg::new(t_logstd + 1) (zealot-rl/src/ppo.rs:357-363);
+    // t_logstd advances once per minibatch, so epoch e starts at t + e*minibatches.
+    p->perm_host.assign((size_t)pl.epochs * pl.n, 0);
+    for (int e = 0; e < pl.epochs; ++e) {
+      int* order = p->perm_host.data() + (size_t)e * pl.n;
+      for (long long i = 0; i < pl.n; ++i) order[i] = (int)i;
+      Lcg sh((uint64_t)(p->hstate.t + e * cfg->minibatches) + 1);
+      for (long long i = pl.n - 1; i >= 1; --i) {
+        size_t j = (size_t)(sh.unit() * (float)(i + 1));
+        std::swap(order[i], order[std::min<long long>((long long)j, i)]);
+      }
+    }
+  }
+  zk::PpoParams& pp = pl.pp;
+  pp.mode = mode;
+  pp.A = p->A;
+  pp.mb = pl.mb;
+  pp.n_mb = pl.n_mb;
+  pp.clip = cfg->clip;
+  pp.entropy_coef = cfg->entropy_coef;
+  pp.value_coef = cfg->value_coef;
+  pp.scale = 1.0f / (float)pl.mb;
+  pp.max_grad_norm = cfg->max_grad_norm;
+  pp.desired_kl = cfg->desired_kl;
+  pp.lr_min = cfg->lr_min;
+  pp.lr_max = cfg->lr_max;
+  pp.adaptive_lr = cfg->adaptive_lr;
+  pp.early_stop = mode == ZL_SEMANTICS_GPU_TRAINER ? cfg->early_stop : 0;
+  pp.clamp_ls = mode == ZL_SEMANTICS_ACTOR_CRITIC && cfg->clamp_log_std ? 1 : 0;
+  pp.beta1 = 0.9f;
+  pp.beta2 = 0.999f;
+  pp.eps = 1e-8f;
+
+  // The launch sequence depends only on these; everything that changes per
+  // update (scalars, orders, batch contents) lives in device memory.
+  char key[1024];
+  snprintf(key, sizeof(key),
+           "%d|%lld|%d|%d|%d|%p|%d|%p|%d|%p|%d|%p|%d|%p|%p|%p|%p|%d%d%d|%a|%a|%a|%a|%a|%a|%a|%d|%d|"
+           "%d|%d|%d|%p|%p",
+           mode, pl.n, pl.mb, pl.n_mb, pl.epochs, (const void*)b->obs, b->ld_obs,
+           (const void*)b->critic_obs, b->ld_critic_obs, (const void*)b->action, b->ld_action,
+           (const void*)b->mean_old, b->ld_mean_old, (const void*)b->logp_old,
+           (const void*)b->value_old, (const void*)b->adv, (const void*)b->ret, (int)pl.stage_obs,
+           (int)pl.stage_cobs, (int)pl.shuffle, (double)cfg->clip, (double)cfg->entropy_coef,
+           (double)cfg->value_coef, (double)cfg->max_grad_norm, (double)cfg->desired_kl,
+           (double)cfg->lr_min, (double)cfg->lr_max, cfg->adaptive_lr, cfg->early_stop,
+           cfg->normalize_adv, cfg->clamp_log_std, cfg->shuffle, (void*)p->obs_pad,
+           (void*)p->perm);
+  const bool eager = c->timing_kernel >= 0;
+  if (!eager && (!p->gexec || p->gkey != key)) {
+    if (p->gexec) {
+      hipGraphExecDestroy(p->gexec);
+      p->gexec = nullptr;
+    }
+    p->gkey.clear();
+    ZL_HIP(c, hipStreamSynchronize(c->stream));
+    ZL_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    s = enqueue_update(p, b, cfg, pl);
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &graph);
+    if (s) {
+      if (graph) hipGraphDestroy(graph);
+      return s;
+    }
+    if (e != hipSuccess)
+      return fail(c, ZL_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+    e = hipGraphInstantiate(&p->gexec, graph, nullptr, nullptr, 0);
+    hipGraphDestroy(graph);
+    if (e != hipSuccess) {
+      p->gexec = nullptr;
+      return fail(c, ZL_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+    }
+    p->gkey = key;
+  }
+  // Per-update device scalars: persistent lr / t / gstep, everything else reset.
+  zk::DevState st = p->hstate;
+  st.active = 1;
+  st.epochs_run = 0;
+  st.mb_in_epoch = 0;
+  st.ep_kl = st.ep_surr = st.ep_vloss = st.ep_ent = 0.f;
+  for (float& x : st.stats) x = 0.f;
+  st.stats[4] = st.lr;
+  st.scale[0] = st.scale[1] = st.scale[2] = 1.f;
+  st.norm[0] = st.norm[1] = st.norm[2] = 0.f;
+  st.last_kl = 0.f;
+  if (mode == ZL_SEMANTICS_ACTOR_CRITIC) {
+    st.bc1 = 1.f;
+    st.bc2 = 1.f;
+  }
+  ZL_HIP(c, hipMemcpyAsync(p->dstate, &st, sizeof(st), hipMemcpyHostToDevice, c->stream));
+  ZL_HIP(c, hipMemcpyAsync(p->ls_old, p->params + p->ls_off, (size_t)p->A * 4,
+                           hipMemcpyDeviceToDevice, c->stream));
+  if (pl.shuffle)
+    ZL_HIP(c, hipMemcpyAsync(p->perm, p->perm_host.data(), p->perm_host.size() * 4,
+                             hipMemcpyHostToDevice, c->stream));
+  if (eager) {
+    if ((s = enqueue_update(p, b, cfg, pl))) return s;
+  } else {
+    ZL_HIP(c, hipGraphLaunch(p->gexec, c->stream));
+  }
+  ZL_HIP(c, hipMemcpyAsync(&st, p->dstate, sizeof(st), hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  p->hstate.lr = st.lr;
+  p->hstate.t = st.t;
+  p->hstate.gstep = st.gstep;
+  if (stats) {
+    stats->kl = st.stats[0];
+    stats->surrogate = st.stats[1];
+    stats->value_loss = st.stats[2];
+    stats->entropy = st.stats[3];
+    stats->lr = st.stats[4];
+    stats->epochs_run = st.epochs_run;
+    stats->last_kl = st.last_kl;
+    stats->grad_norm[0] = st.norm[0];
+    stats->grad_norm[1] = st.norm[1];
+    stats->grad_norm[2] = st.norm[2];
+  }
+  return ZL_OK;
+}
+
+zl_status zl_ppo_get_grads(zl_ppo* p, float* actor, float* critic, float* log_std) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  std::vector<float> host((size_t)p->nflat);
+  ZL_HIP(c, hipMemcpyAsync(host.data(), p->grads, host.size() * 4, hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  if (actor) p->actor.gather(host.data(), actor);
+  if (critic) p->critic.gather(host.data(), critic);
+  if (log_std) std::memcpy(log_std, host.data() + p->ls_off, (size_t)p->A * 4);
+  return ZL_OK;
+}
+
+zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
+                                 long long row0, int rows, const int* perm_dev, float* stats) {
+  if (!p || !b || !cfg) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  if (!b->obs || !b->critic_obs || !b->action || !b->logp_old || !b->value_old || !b->adv ||
+      !b->ret || rows < 1 || rows > p->mb_cap || row0 < 0 || (!perm_dev && row0 + rows > b->n) ||
+      b->ld_obs < p->actor.dims[0] || b->ld_critic_obs < p->critic.dims[0] ||
+      b->ld_action < p->A || (b->mean_old && b->ld_mean_old < p->A))
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_minibatch_grads: bad argument");
+  // Layer-0 operands need 16-byte aligned rows: stage the rows of this call.
+  const int od = p->actor.dims[0], cd = p->critic.dims[0];
+  const int odp = (int)round_up(od, 4), cdp = (int)round_up(cd, 4);
+  zl_status s = ZL_OK;
+  size_t cap = p->obs_pad_floats * 4;
+  if ((s = grow(c, (void**)&p->obs_pad, &cap, (size_t)rows * odp * 4))) return s;
+  p->obs_pad_floats = cap / 4;
+  cap = p->cobs_pad_floats * 4;
+  if ((s = grow(c, (void**)&p->cobs_pad, &cap, (size_t)rows * cdp * 4))) return s;
+  p->cobs_pad_floats = cap / 4;
+  if ((s = copy_rows(c, p->obs_pad, odp, b->obs, b->ld_obs, od, rows, perm_dev, (int)row0, nullptr,
+                     true)))
+    return s;
+  if ((s = copy_rows(c, p->cobs_pad, cdp, b->critic_obs, b->ld_critic_obs, cd, rows, perm_dev,
+                     (int)row0, nullptr, true)))
+    return s;
+  const int La = p->actor.L, Lc = p->critic.L, A = p->A;
+  const int nb = (int)cdiv(rows, kThreads);
+  if ((s = net_forward(c, p->actor, p->ab, p->params, p->obs_pad, odp, nullptr, rows, nullptr)))
+    return s;
+  if ((s = net_forward(c, p->critic, p->cb, p->params, p->cobs_pad, cdp, nullptr, rows, nullptr)))
+    return s;
+  const float scale = 1.0f / (float)rows;
+  zk::ActorLossArgs al{};
+  al.mean = p->ab.act[La];
+  al.ldm = p->ab.ld[La];
+  al.action = b->action;
+  al.ldact = b->ld_action;
+  al.adv = b->adv;
+  al.logp_old = b->logp_old;
+  al.mean_old = b->mean_old;
+  al.ldmo = b->ld_mean_old;
+  al.log_std = p->params + p->ls_off;
+  al.perm = perm_dev;
+  al.row0 = (int)row0;
+  al.rows = rows;
+  al.A = A;
+  al.delta = p->ab.delta[La - 1];
+  al.ldd = p->ab.ld[La];
+  al.gls_part = p->gls_part;
+  al.stat_part = p->astat_part;
+  al.clip = cfg->clip;
+  al.entropy_coef = cfg->entropy_coef;
+  al.scale = scale;
+  if ((s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, al, (unsigned)((kThreads * A + kThreads) * 4))))
+    return s;
+  zk::ValueLossArgs vl{};
+  vl.v = p->cb.act[Lc];
+  vl.ldv = p->cb.ld[Lc];
+  vl.value_old = b->value_old;
+  vl.ret = b->ret;
+  vl.perm = perm_dev;
+  vl.row0 = (int)row0;
+  vl.rows = rows;
+  vl.delta = p->cb.delta[Lc - 1];
+  vl.ldd = p->cb.ld[Lc];
+  vl.stat_part = p->vstat_part;
+  vl.clip = cfg->clip;
+  vl.value_coef = cfg->value_coef;
+  vl.scale = scale;
+  if ((s = launch(c, K_VALUE_LOSS, (unsigned)nb, 1, 1, vl))) return s;
+  if ((s = net_backward(c, p->actor, p->ab, p->params, p->grads, p->obs_pad, odp, nullptr, rows,
+                        p->ab.delta[La - 1], p->ab.ld[La], nullptr, p->ws, p->ws_floats)))
+    return s;
+  if ((s = net_backward(c, p->critic, p->cb, p->params, p->grads, p->cobs_pad, cdp, nullptr, rows,
+                        p->cb.delta[Lc - 1], p->cb.ld[Lc], nullptr, p->ws, p->ws_floats)))
+    return s;
+  // Fixed-order sums of the per-block partials.
+  auto reduce = [&](const float* part, int width, float* out) {
+    zk::SplitReduceArgs r{};
+    r.part = part;
+    r.out = out;
+    r.mn = width;
+    r.cols = width;
+    r.ldo = width;
+    r.splits = nb;
+    return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(width, kThreads), 1, 1, r);
+  };
+  if ((s = reduce(p->gls_part, A, p->grads + p->ls_off))) return s;
+  if ((s = reduce(p->astat_part, 2, p->stat_out))) return s;
+  if ((s = reduce(p->vstat_part, 1, p->stat_out + 2))) return s;
+  float h[3];
+  ZL_HIP(c, hipMemcpyAsync(h, p->stat_out, sizeof(h), hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  if (stats) {
+    stats[0] = h[0];  // surrogate
+    stats[1] = h[2];  // value loss
+    stats[2] = h[1];  // kl
+  }
+  return ZL_OK;
+}
+
+static zl_status chunked_forward(zl_ppo* p, bool critic, const float* x, int ld, long long n,
+                                 float* out, int ld_out, int cols) {
+  zl_ctx* c = p->c;
+  const NetLayout& nl = critic ? p->critic : p->actor;
+  const NetBuffers& nb = critic ? p->cb : p->ab;
+  if (!x || !out || n < 0 || ld < nl.dims[0] || ld_out < cols)
+    return fail(c, ZL_ERR_INVALID, "forward: bad argument");
+  for (long long r0 = 0; r0 < n; r0 += p->mb_cap) {
+    const int rows = (int)std::min<long long>(p->mb_cap, n - r0);
+    zl_status s = net_forward(c, nl, nb, p->params, x + (size_t)r0 * ld, ld, nullptr, rows, nullptr);
+    if (s) return s;
+    s = copy_rows(c, out + (size_t)r0 * ld_out, ld_out, nb.act[nl.L], nb.ld[nl.L], cols, rows,
+                  nullptr, 0, nullptr, false);
+    if (s) return s;
+  }
+  return ZL_OK;
+}
+
+zl_status zl_ppo_values(zl_ppo* p, const float* cobs, int ld, long long n, float* values) {
+  if (!p) return ZL_ERR_INVALID;
+  return chunked_forward(p, true, cobs, ld, n, values, 1, 1);
+}
+
+zl_status zl_ppo_actor_mean(zl_ppo* p, const float* obs, int ld, long long n, float* mean,
+                            int ld_mean) {
+  if (!p) return ZL_ERR_INVALID;
+  return chunked_forward(p, false, obs, ld, n, mean, ld_mean, p->A);
+}
+
+}  // extern "C"

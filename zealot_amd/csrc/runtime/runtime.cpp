@@ -1,0 +1,776 @@
+// runtime.cpp — context, code-object loading, buffers and the stand-alone
+// operators of the C ABI (include/zealot_hip.h).
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace zl {
+
+const char* const kKernelNames[K_COUNT] = {
+    "zk_gemm_ak_bk_64x128", "zk_gemm_ak_bk_128x32", "zk_gemm_ak_bk_256x16",
+    "zk_gemm_ak_bn_64x128", "zk_gemm_am_bn_64x128", "zk_gemm_am_bk_64x128",
+    "zk_splitk_reduce",     "zk_actor_loss",        "zk_value_loss",
+    "zk_sumsq",             "zk_finalize",          "zk_adam",
+    "zk_epoch_begin",       "zk_kl",                "zk_epoch_end",
+    "zk_gae",               "zk_adv_norm",          "zk_elu_backward",
+    "zk_row_sum",           "zk_copy_rows",         "zk_sample",
+    "zk_clamp",
+};
+
+static thread_local std::string g_init_error;
+
+zl_status fail(zl_ctx* c, zl_status s, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  if (c)
+    c->err = buf;
+  else
+    g_init_error = buf;
+  return s;
+}
+
+zl_status timing_mark(zl_ctx* c, bool stop) {
+  // A start mark takes a fresh pair from the pool; a stop mark closes it.
+  if (!stop) {
+    if (c->ev_used * 2 + 2 > c->ev_pool.size()) {
+      for (int i = 0; i < 2; ++i) {
+        hipEvent_t e;
+        ZL_HIP(c, hipEventCreate(&e));
+        c->ev_pool.push_back(e);
+      }
+    }
+    ZL_HIP(c, hipEventRecord(c->ev_pool[c->ev_used * 2], c->stream));
+  } else {
+    ZL_HIP(c, hipEventRecord(c->ev_pool[c->ev_used * 2 + 1], c->stream));
+    c->ev_used += 1;
+  }
+  return ZL_OK;
+}
+
+zl_status ensure_ws(zl_ctx* c, size_t floats) {
+  if (floats <= c->ws_floats) return ZL_OK;
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  if (c->ws) ZL_HIP(c, hipFree(c->ws));
+  c->ws = nullptr;
+  c->ws_floats = 0;
+  size_t want = std::max<size_t>(floats, 1 << 20);
+  ZL_HIP(c, hipMalloc((void**)&c->ws, want * sizeof(float)));
+  c->ws_floats = want;
+  return ZL_OK;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+struct TileCfg {
+  KernelId k;
+  int bm, bn;
+};
+
+static TileCfg pick_tile(bool a_kc, bool b_kc, int N) {
+  if (a_kc && b_kc) {
+    if (N <= 16) return {K_GEMM_AK_BK_256x16, 256, 16};
+    if (N <= 32) return {K_GEMM_AK_BK_128x32, 128, 32};
+    return {K_GEMM_AK_BK_64x128, 64, 128};
+  }
+  if (a_kc) return {K_GEMM_AK_BN_64x128, 64, 128};
+  if (b_kc) return {K_GEMM_AM_BK_64x128, 64, 128};
+  return {K_GEMM_AM_BN_64x128, 64, 128};
+}
+
+int gemm_splits(int M, int N, int K, bool a_kc, bool b_kc, int epi) {
+  if (epi != zk::kEpiStore) return 1;
+  TileCfg t = pick_tile(a_kc, b_kc, N);
+  long long tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
+  long long kt = cdiv(K, 16);
+  // Deep-K, few-tile shapes (the weight gradients, K = batch rows) would
+  // leave most of the 256 CUs idle: slice K so the grid has ~2 waves of
+  // workgroups, keeping at least 8 k-tiles (128 rows) per slice.
+  if (K < 256 || tiles >= 512) return 1;
+  long long s = cdiv(512, tiles);
+  s = std::min<long long>(s, std::max<long long>(1, kt / 8));
+  if (s <= 1) return 1;
+  long long per = cdiv(kt, s);
+  return (int)cdiv(kt, per);
+}
+
+size_t gemm_ws_floats(int M, int N, int K, bool a_kc, bool b_kc, int epi) {
+  int s = gemm_splits(M, N, K, a_kc, b_kc, epi);
+  if (s <= 1) return 0;
+  return (size_t)s * M * N + (size_t)s * M;
+}
+
+zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
+  if (d.M <= 0 || d.N <= 0) return ZL_OK;
+  TileCfg t = pick_tile(d.a_kc, d.b_kc, d.N);
+  int splits = d.splits > 0 ? d.splits : gemm_splits(d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi);
+  if (d.epi != zk::kEpiStore) splits = 1;
+  const long long kt = cdiv(std::max(d.K, 0), 16);
+  int per = (int)std::max<long long>(1, cdiv(kt, splits));
+  splits = (int)std::max<long long>(1, cdiv(kt, per));
+
+  zk::GemmArgs a{};
+  a.A = d.A;
+  a.B = d.B;
+  a.bias = d.bias;
+  a.Y = d.Y;
+  a.permA = d.permA;
+  a.permB = d.permB;
+  a.guard = d.guard;
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldy = d.ldy;
+  a.bias_stride = d.bias_stride;
+  a.epi = d.epi;
+  a.act = d.act;
+  a.kt_per_split = per;
+  const int a_ext = d.a_kc ? d.K : d.M;
+  const int b_ext = d.b_kc ? d.K : d.N;
+  a.vecA = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4);
+  a.vecB = aligned16(d.B) && d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
+
+  const unsigned gx = (unsigned)cdiv(d.M, t.bm), gy = (unsigned)cdiv(d.N, t.bn);
+  if (splits == 1) {
+    a.C = d.C;
+    a.ldc = d.ldc;
+    a.split_stride = 0;
+    a.rowsumA = d.rowsum_out;
+    return launch(c, t.k, gx, gy, 1, a);
+  }
+  const size_t mn = (size_t)d.M * d.N;
+  const size_t need = (size_t)splits * mn + (d.rowsum_out ? (size_t)splits * d.M : 0);
+  float* ws = d.ws;
+  if (!ws) {
+    zl_status s = ensure_ws(c, need);
+    if (s) return s;
+    ws = c->ws;
+  } else if (need > d.ws_floats) {
+    return fail(c, ZL_ERR_INVALID, "split-K scratch too small (%zu < %zu floats)", d.ws_floats,
+                need);
+  }
+  a.C = ws;
+  a.ldc = d.N;
+  a.split_stride = (long long)mn;
+  a.rowsumA = d.rowsum_out ? ws + (size_t)splits * mn : nullptr;
+  zl_status s = launch(c, t.k, gx, gy, (unsigned)splits, a);
+  if (s) return s;
+  zk::SplitReduceArgs r{};
+  r.part = ws;
+  r.out = d.C;
+  r.rowpart = a.rowsumA;
+  r.rowout = d.rowsum_out;
+  r.guard = d.guard;
+  r.mn = (long long)mn;
+  r.cols = d.N;
+  r.ldo = d.ldc;
+  r.rows = d.rowsum_out ? d.M : 0;
+  r.splits = splits;
+  return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv((long long)mn + r.rows, kThreads), 1, 1, r);
+}
+
+static std::string code_object_path() {
+  if (const char* e = getenv("ZL_CODE_OBJECT")) return e;
+  Dl_info info;
+  if (dladdr((void*)&zl_init, &info) && info.dli_fname) {
+    std::string p = info.dli_fname;
+    size_t slash = p.rfind('/');
+    std::string dir = slash == std::string::npos ? "." : p.substr(0, slash);
+    return dir + "/zealot_kernels.hsaco";
+  }
+  return "zealot_kernels.hsaco";
+}
+
+// ----------------------------------------------------------------- self-test
+
+// Closed-form inputs of CutileGemm::self_test (src/biped/cutile_gemm.rs:711-716).
+static float st_val(int i, int j, int seed, int a, int b, int cst, int p) {
+  int h = (i * a + j * b + seed * cst) % p;
+  return (float)h / ((float)p / 2.0f) - 1.0f;
+}
+
+static zl_status self_test(zl_ctx* c, double* worst_out) {
+  struct Case {
+    int m, n, k;
+    bool lt, rt;
+  };
+  // (m, n, k, lhs_t, rhs_t) of src/biped/cutile_gemm.rs:699-708.
+  const Case cases[] = {{12, 300, 45, false, false}, {45, 300, 256, true, false},
+                        {256, 45, 300, false, true}, {64, 96, 4096, false, true},
+                        {64, 96, 3072, false, true}, {512, 12288, 51, false, false}};
+  double worst = 0.0;
+  const double tol = 1e-4;  // fp32 MFMA (the cuTile tf32 bound is 5e-2)
+  bool force_fail = getenv("ZL_FORCE_SELF_TEST_FAIL") && strcmp(getenv("ZL_FORCE_SELF_TEST_FAIL"), "1") == 0;
+  int ci = 0;
+  for (const Case& cs : cases) {
+    const int m = cs.m, n = cs.n, k = cs.k;
+    std::vector<float> L((size_t)m * k), R((size_t)k * n);
+    for (int i = 0; i < m; ++i)
+      for (int j = 0; j < k; ++j) L[(size_t)i * k + j] = st_val(i, j, ci, 31, 17, 101, 97);
+    for (int i = 0; i < k; ++i)
+      for (int j = 0; j < n; ++j) R[(size_t)i * n + j] = st_val(i, j, ci + 7, 31, 17, 101, 97);
+    std::vector<double> ref((size_t)m * n, 0.0);
+    for (int i = 0; i < m; ++i)
+      for (int p = 0; p < k; ++p) {
+        double l = L[(size_t)i * k + p];
+        const float* rr = &R[(size_t)p * n];
+        double* o = &ref[(size_t)i * n];
+        for (int j = 0; j < n; ++j) o[j] += l * rr[j];
+      }
+    std::vector<float> Lb = L, Rb = R;
+    if (cs.lt)
+      for (int i = 0; i < m; ++i)
+        for (int j = 0; j < k; ++j) Lb[(size_t)j * m + i] = L[(size_t)i * k + j];
+    if (cs.rt)
+      for (int i = 0; i < k; ++i)
+        for (int j = 0; j < n; ++j) Rb[(size_t)j * k + i] = R[(size_t)i * n + j];
+    float *dl = nullptr, *dr = nullptr, *dout = nullptr;
+    ZL_HIP(c, hipMalloc((void**)&dl, Lb.size() * 4));
+    ZL_HIP(c, hipMalloc((void**)&dr, Rb.size() * 4));
+    ZL_HIP(c, hipMalloc((void**)&dout, (size_t)m * n * 4));
+    ZL_HIP(c, hipMemcpy(dl, Lb.data(), Lb.size() * 4, hipMemcpyHostToDevice));
+    ZL_HIP(c, hipMemcpy(dr, Rb.data(), Rb.size() * 4, hipMemcpyHostToDevice));
+    zl_status s = zl_gemm(c, dout, dl, cs.lt, dr, cs.rt, m, n, k);
+    std::vector<float> got((size_t)m * n);
+    if (!s) {
+      ZL_HIP(c, hipStreamSynchronize(c->stream));
+      ZL_HIP(c, hipMemcpy(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost));
+    }
+    hipFree(dl);
+    hipFree(dr);
+    hipFree(dout);
+    if (s) return s;
+    double amax = 1e-6, err = 0.0;
+    for (double v : ref) amax = std::max(amax, std::fabs(v));
+    for (size_t i = 0; i < ref.size(); ++i) err = std::max(err, std::fabs(got[i] - ref[i]) / amax);
+    if (force_fail) err = 1.0;
+    if (!(err <= tol))
+      return fail(c, ZL_ERR_SELF_TEST, "self-test case %d (m=%d n=%d k=%d lt=%d rt=%d): rel err %.3e",
+                  ci, m, n, k, (int)cs.lt, (int)cs.rt, err);
+    worst = std::max(worst, err);
+    ++ci;
+  }
+  // Fused bias + ELU with a strided bias column, then the ELU backward and
+  // the row sums (src/biped/cutile_gemm.rs:749-826).
+  {
+    const int m = 100, n = 300, k = 45;
+    auto f = [](int i, int j, int seed) { return st_val(i, j, seed, 29, 13, 89, 83); };
+    std::vector<float> L((size_t)m * k), R((size_t)k * n), Bb((size_t)m * 8), G((size_t)m * n);
+    for (int i = 0; i < m; ++i)
+      for (int j = 0; j < k; ++j) L[(size_t)i * k + j] = f(i, j, 1);
+    for (int i = 0; i < k; ++i)
+      for (int j = 0; j < n; ++j) R[(size_t)i * n + j] = f(i, j, 2);
+    for (int i = 0; i < m; ++i)
+      for (int j = 0; j < 8; ++j) Bb[(size_t)i * 8 + j] = f(i, j, 3);
+    for (int i = 0; i < m; ++i)
+      for (int j = 0; j < n; ++j) G[(size_t)i * n + j] = f(i, j, 4);
+    std::vector<double> ref((size_t)m * n);
+    for (int i = 0; i < m; ++i)
+      for (int j = 0; j < n; ++j) {
+        double z = 0.0;
+        for (int p = 0; p < k; ++p) z += (double)L[(size_t)i * k + p] * R[(size_t)p * n + j];
+        z += Bb[(size_t)i * 8];
+        ref[(size_t)i * n + j] = z > 0.0 ? z : std::exp(z) - 1.0;
+      }
+    float *dl, *dr, *db, *dout, *dg, *ds;
+    ZL_HIP(c, hipMalloc((void**)&dl, L.size() * 4));
+    ZL_HIP(c, hipMalloc((void**)&dr, R.size() * 4));
+    ZL_HIP(c, hipMalloc((void**)&db, Bb.size() * 4));
+    ZL_HIP(c, hipMalloc((void**)&dout, (size_t)m * n * 4));
+    ZL_HIP(c, hipMalloc((void**)&dg, G.size() * 4));
+    ZL_HIP(c, hipMalloc((void**)&ds, (size_t)m * 4));
+    ZL_HIP(c, hipMemcpy(dl, L.data(), L.size() * 4, hipMemcpyHostToDevice));
+    ZL_HIP(c, hipMemcpy(dr, R.data(), R.size() * 4, hipMemcpyHostToDevice));
+    ZL_HIP(c, hipMemcpy(db, Bb.data(), Bb.size() * 4, hipMemcpyHostToDevice));
+    ZL_HIP(c, hipMemcpy(dg, G.data(), G.size() * 4, hipMemcpyHostToDevice));
+    zl_status s = zl_gemm_bias_act(c, dout, dl, dr, m, n, k, db, 8, 1);
+    if (!s) s = zl_elu_backward(c, dg, dout, m, n);
+    if (!s) s = zl_row_sum(c, ds, dg, m, n);
+    std::vector<float> got((size_t)m * n), got_g((size_t)m * n), got_s(m);
+    if (!s) {
+      ZL_HIP(c, hipStreamSynchronize(c->stream));
+      ZL_HIP(c, hipMemcpy(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost));
+      ZL_HIP(c, hipMemcpy(got_g.data(), dg, got_g.size() * 4, hipMemcpyDeviceToHost));
+      ZL_HIP(c, hipMemcpy(got_s.data(), ds, got_s.size() * 4, hipMemcpyDeviceToHost));
+    }
+    hipFree(dl);
+    hipFree(dr);
+    hipFree(db);
+    hipFree(dout);
+    hipFree(dg);
+    hipFree(ds);
+    if (s) return s;
+    double amax = 1e-6, err = 0.0, err_g = 0.0, err_s = 0.0;
+    for (double v : ref) amax = std::max(amax, std::fabs(v));
+    for (int i = 0; i < m; ++i) {
+      double rs = 0.0;
+      for (int j = 0; j < n; ++j) {
+        const size_t ix = (size_t)i * n + j;
+        const double y = ref[ix];
+        err = std::max(err, std::fabs(got[ix] - y) / amax);
+        const double gref = G[ix] * (y > 0.0 ? 1.0 : y + 1.0);
+        err_g = std::max(err_g, std::fabs(got_g[ix] - gref));
+        rs += got_g[ix];
+      }
+      err_s = std::max(err_s, std::fabs(got_s[i] - rs) / std::max(std::fabs(rs), 1.0));
+    }
+    if (!(err <= tol && err_g <= tol && err_s <= tol))
+      return fail(c, ZL_ERR_SELF_TEST,
+                  "self-test fused bias+elu: err %.3e, backward err %.3e, row_sum err %.3e", err,
+                  err_g, err_s);
+    worst = std::max(worst, std::max(err, std::max(err_g, err_s)));
+  }
+  *worst_out = worst;
+  return ZL_OK;
+}
+
+}  // namespace zl
+
+using namespace zl;
+
+extern "C" {
+
+const char* zl_version(void) { return "zealot_hip 0.1.0 (gfx950, fp32 MFMA)"; }
+
+void zl_abi_struct_sizes(size_t out[3]) {
+  out[0] = sizeof(zl_ppo_config);
+  out[1] = sizeof(zl_batch);
+  out[2] = sizeof(zl_ppo_stats);
+}
+
+const char* zl_global_error(void) { return g_init_error.c_str(); }
+
+zl_status zl_init(int device, zl_ctx** out) {
+  if (!out) return fail(nullptr, ZL_ERR_INVALID, "zl_init: out is NULL");
+  *out = nullptr;
+  g_init_error.clear();
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count <= 0)
+    return fail(nullptr, ZL_ERR_HIP, "zl_init: no HIP device (%s)",
+                e != hipSuccess ? hipGetErrorString(e) : "count 0");
+  if (device < 0 || device >= count)
+    return fail(nullptr, ZL_ERR_INVALID, "zl_init: device %d out of range [0, %d)", device, count);
+  e = hipSetDevice(device);
+  if (e != hipSuccess)
+    return fail(nullptr, ZL_ERR_HIP, "hipSetDevice: %s", hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess)
+    return fail(nullptr, ZL_ERR_HIP, "hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(nullptr, ZL_ERR_CODE_OBJECT, "zl_init: device is %s, the code object is gfx950",
+                prop.gcnArchName);
+  zl_ctx* c = new zl_ctx();
+  c->device = device;
+  std::string path = code_object_path();
+  e = hipModuleLoad(&c->module, path.c_str());
+  if (e != hipSuccess) {
+    fail(nullptr, ZL_ERR_CODE_OBJECT, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    delete c;
+    return ZL_ERR_CODE_OBJECT;
+  }
+  for (int k = 0; k < K_COUNT; ++k) {
+    e = hipModuleGetFunction(&c->fn[k], c->module, kKernelNames[k]);
+    if (e != hipSuccess) {
+      fail(nullptr, ZL_ERR_CODE_OBJECT, "kernel %s not in %s: %s", kKernelNames[k], path.c_str(),
+           hipGetErrorString(e));
+      hipModuleUnload(c->module);
+      delete c;
+      return ZL_ERR_CODE_OBJECT;
+    }
+  }
+  // Default-priority stream (no priority variants are used anywhere).
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    fail(nullptr, ZL_ERR_HIP, "hipStreamCreate: %s", hipGetErrorString(e));
+    hipModuleUnload(c->module);
+    delete c;
+    return ZL_ERR_HIP;
+  }
+  double worst = 0.0;
+  zl_status s = self_test(c, &worst);
+  if (s) {
+    g_init_error = c->err;
+    zl_destroy(c);
+    return s;
+  }
+  c->self_test_err = worst;
+  c->err.clear();
+  *out = c;
+  return ZL_OK;
+}
+
+zl_status zl_timing_begin(zl_ctx* c, const char* kernel_name) {
+  if (!c || !kernel_name) return ZL_ERR_INVALID;
+  for (int k = 0; k < K_COUNT; ++k) {
+    if (strcmp(kernel_name, kKernelNames[k]) == 0) {
+      ZL_HIP(c, hipStreamSynchronize(c->stream));
+      c->timing_kernel = k;
+      c->ev_used = 0;
+      return ZL_OK;
+    }
+  }
+  return fail(c, ZL_ERR_INVALID, "zl_timing_begin: unknown kernel %s", kernel_name);
+}
+
+zl_status zl_timing_end(zl_ctx* c, double* total_ms, long long* launches) {
+  if (!c) return ZL_ERR_INVALID;
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  double tot = 0.0;
+  for (size_t i = 0; i < c->ev_used; ++i) {
+    float ms = 0.f;
+    ZL_HIP(c, hipEventElapsedTime(&ms, c->ev_pool[2 * i], c->ev_pool[2 * i + 1]));
+    tot += ms;
+  }
+  if (total_ms) *total_ms = tot;
+  if (launches) *launches = (long long)c->ev_used;
+  c->timing_kernel = -1;
+  c->ev_used = 0;
+  return ZL_OK;
+}
+
+void zl_destroy(zl_ctx* c) {
+  if (!c) return;
+  if (c->stream) hipStreamSynchronize(c->stream);
+  for (hipEvent_t e : c->ev_pool) hipEventDestroy(e);
+  if (c->ws) hipFree(c->ws);
+  if (c->stream) hipStreamDestroy(c->stream);
+  if (c->module) hipModuleUnload(c->module);
+  delete c;
+}
+
+const char* zl_last_error(const zl_ctx* c) { return c ? c->err.c_str() : g_init_error.c_str(); }
+
+void* zl_stream(zl_ctx* c) { return c ? (void*)c->stream : nullptr; }
+
+double zl_self_test_error(const zl_ctx* c) { return c ? c->self_test_err : -1.0; }
+
+zl_status zl_synchronize(zl_ctx* c) {
+  if (!c) return ZL_ERR_INVALID;
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  return ZL_OK;
+}
+
+zl_status zl_alloc(zl_ctx* c, size_t bytes, void** out) {
+  if (!c || !out) return ZL_ERR_INVALID;
+  *out = nullptr;
+  ZL_HIP(c, hipMalloc(out, std::max<size_t>(bytes, 4)));
+  return ZL_OK;
+}
+
+zl_status zl_free(zl_ctx* c, void* p) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!p) return ZL_OK;
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  ZL_HIP(c, hipFree(p));
+  return ZL_OK;
+}
+
+zl_status zl_upload(zl_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return ZL_ERR_INVALID;
+  if (!bytes) return ZL_OK;
+  ZL_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  return ZL_OK;
+}
+
+zl_status zl_download(zl_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return ZL_ERR_INVALID;
+  if (!bytes) return ZL_OK;
+  ZL_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  return ZL_OK;
+}
+
+zl_status zl_copy_d2d(zl_ctx* c, void* dst, const void* src, size_t bytes) {
+  if (!c || (!dst && bytes) || (!src && bytes)) return ZL_ERR_INVALID;
+  if (!bytes) return ZL_OK;
+  ZL_HIP(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, c->stream));
+  return ZL_OK;
+}
+
+// ------------------------------------------------------------- operators
+
+zl_status zl_gemm(zl_ctx* c, float* out, const float* lhs, int lhs_t, const float* rhs, int rhs_t,
+                  int m, int n, int k) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!out || !lhs || !rhs || m < 0 || n < 0 || k < 0)
+    return fail(c, ZL_ERR_INVALID, "zl_gemm: bad argument (m=%d n=%d k=%d)", m, n, k);
+  GemmDesc d;
+  d.A = lhs;
+  d.a_kc = !lhs_t;
+  d.lda = lhs_t ? m : k;
+  d.B = rhs;
+  d.b_kc = rhs_t != 0;
+  d.ldb = rhs_t ? k : n;
+  d.C = out;
+  d.ldc = n;
+  d.M = m;
+  d.N = n;
+  d.K = k;
+  return run_gemm(c, d);
+}
+
+zl_status zl_gemm_bias_act(zl_ctx* c, float* out, const float* lhs, const float* rhs, int m, int n,
+                           int k, const float* bias, int bias_row_stride, int elu) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!out || !lhs || !rhs || !bias || m < 0 || n < 0 || k < 0 || bias_row_stride < 1)
+    return fail(c, ZL_ERR_INVALID, "zl_gemm_bias_act: bad argument");
+  GemmDesc d;
+  d.A = lhs;
+  d.a_kc = true;
+  d.lda = k;
+  d.B = rhs;
+  d.b_kc = false;
+  d.ldb = n;
+  d.C = out;
+  d.ldc = n;
+  d.M = m;
+  d.N = n;
+  d.K = k;
+  d.epi = zk::kEpiBiasM;
+  d.bias = bias;
+  d.bias_stride = bias_row_stride;
+  d.act = elu ? 1 : 0;
+  return run_gemm(c, d);
+}
+
+zl_status zl_elu_backward(zl_ctx* c, float* g, const float* y, int m, int n) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!g || !y || m < 0 || n < 0) return fail(c, ZL_ERR_INVALID, "zl_elu_backward: bad argument");
+  zk::EluBwdArgs a{};
+  a.g = g;
+  a.y = y;
+  a.rows = m;
+  a.cols = n;
+  a.ldg = n;
+  a.ldy = n;
+  return launch(c, K_ELU_BACKWARD, (unsigned)cdiv((long long)m * n, kThreads), 1, 1, a);
+}
+
+zl_status zl_row_sum(zl_ctx* c, float* out, const float* x, int m, int n) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!out || !x || m < 0 || n < 0) return fail(c, ZL_ERR_INVALID, "zl_row_sum: bad argument");
+  zk::RowSumArgs a{};
+  a.out = out;
+  a.x = x;
+  a.rows = m;
+  a.cols = n;
+  a.ldx = n;
+  return launch(c, K_ROW_SUM, (unsigned)m, 1, 1, a);
+}
+
+// Sum the [blocks x width] partials over blocks into out[width] (fixed order).
+static zl_status reduce_partials(zl_ctx* c, const float* part, int blocks, int width, float* out) {
+  zk::SplitReduceArgs r{};
+  r.part = part;
+  r.out = out;
+  r.mn = width;
+  r.cols = width;
+  r.ldo = width;
+  r.splits = blocks;
+  return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(width, kThreads), 1, 1, r);
+}
+
+zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const float* action,
+                            int ld_action, const float* log_std, const float* adv,
+                            const float* logp_old, const float* mean_old, int ld_mean_old,
+                            int rows, int A, float clip, float entropy_coef, float scale,
+                            float* d_mean, int ld_d_mean, float* d_log_std, float* stats_dev) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!mean || !action || !log_std || !adv || !logp_old || !d_mean || !d_log_std || !stats_dev ||
+      rows < 0 || A < 1 || A > 48 || ld_mean < A || ld_action < A || ld_d_mean < A ||
+      (mean_old && ld_mean_old < A))
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_actor_grad: bad argument (rows=%d A=%d)", rows, A);
+  const int nb = (int)cdiv(rows, kThreads);
+  const size_t need = (size_t)nb * A + (size_t)nb * 2;
+  zl_status s = ensure_ws(c, need);
+  if (s) return s;
+  zk::ActorLossArgs a{};
+  a.mean = mean;
+  a.action = action;
+  a.adv = adv;
+  a.logp_old = logp_old;
+  a.mean_old = mean_old;
+  a.log_std = log_std;
+  a.delta = d_mean;
+  a.gls_part = c->ws;
+  a.stat_part = c->ws + (size_t)nb * A;
+  a.ldm = ld_mean;
+  a.ldact = ld_action;
+  a.ldmo = ld_mean_old;
+  a.ldd = ld_d_mean;
+  a.row0 = 0;
+  a.rows = rows;
+  a.A = A;
+  a.clip = clip;
+  a.entropy_coef = entropy_coef;
+  a.scale = scale;
+  if (nb == 0) return ZL_OK;
+  s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, a, (unsigned)((kThreads * A + kThreads) * 4));
+  if (s) return s;
+  s = reduce_partials(c, a.gls_part, nb, A, d_log_std);
+  if (s) return s;
+  return reduce_partials(c, a.stat_part, nb, 2, stats_dev);
+}
+
+zl_status zl_ppo_value_grad(zl_ctx* c, const float* v, const float* value_old, const float* ret,
+                            int rows, float clip, float value_coef, float scale, float* d_v,
+                            float* stats_dev) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!v || !value_old || !ret || !d_v || !stats_dev || rows < 0)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_value_grad: bad argument");
+  const int nb = (int)cdiv(rows, kThreads);
+  if (nb == 0) return ZL_OK;
+  zl_status s = ensure_ws(c, (size_t)nb);
+  if (s) return s;
+  zk::ValueLossArgs a{};
+  a.v = v;
+  a.value_old = value_old;
+  a.ret = ret;
+  a.delta = d_v;
+  a.stat_part = c->ws;
+  a.ldv = 1;
+  a.ldd = 1;
+  a.rows = rows;
+  a.clip = clip;
+  a.value_coef = value_coef;
+  a.scale = scale;
+  s = launch(c, K_VALUE_LOSS, (unsigned)nb, 1, 1, a);
+  if (s) return s;
+  return reduce_partials(c, c->ws, nb, 1, stats_dev);
+}
+
+zl_status zl_adam_step(zl_ctx* c, float* p, const float* g, float* m, float* v, size_t n, float lr,
+                       float beta1, float beta2, float eps, float bc1, float bc2) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!p || !g || !m || !v) return fail(c, ZL_ERR_INVALID, "zl_adam_step: null pointer");
+  zk::AdamArgs a{};
+  a.p = p;
+  a.g = g;
+  a.m = m;
+  a.v = v;
+  a.n = (long long)n;
+  a.end_a = (long long)n;
+  a.end_c = (long long)n;
+  a.lr = lr;
+  a.bc1 = bc1;
+  a.bc2 = bc2;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.eps = eps;
+  return launch(c, K_ADAM, (unsigned)cdiv((long long)n, 4 * kThreads), 1, 1, a);
+}
+
+zl_status zl_grad_sqnorm(zl_ctx* c, const float* x, size_t n, float* out_dev) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!x || !out_dev) return fail(c, ZL_ERR_INVALID, "zl_grad_sqnorm: null pointer");
+  const int chunk = 8192;
+  const int nb = std::max(1, (int)cdiv((long long)n, chunk));
+  zl_status s = ensure_ws(c, (size_t)nb);
+  if (s) return s;
+  zk::SumsqArgs a{};
+  a.x = x;
+  a.part = c->ws;
+  a.off0 = 0;
+  a.len0 = (long long)n;
+  a.blocks0 = nb;
+  a.chunk = chunk;
+  s = launch(c, K_SUMSQ, (unsigned)nb, 1, 1, a);
+  if (s) return s;
+  return reduce_partials(c, c->ws, nb, 1, out_dev);
+}
+
+zl_status zl_gae(zl_ctx* c, const float* rewards, const float* values, const uint8_t* dones,
+                 const float* last_values, int T, int N, long long in_ts, long long in_es,
+                 long long out_ts, long long out_es, float gamma, float lam, float* adv,
+                 float* ret) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!rewards || !values || !dones || !last_values || !adv || !ret || T < 0 || N < 0)
+    return fail(c, ZL_ERR_INVALID, "zl_gae: bad argument");
+  zk::GaeArgs a{};
+  a.r = rewards;
+  a.v = values;
+  a.done = dones;
+  a.last_v = last_values;
+  a.adv = adv;
+  a.ret = ret;
+  a.in_ts = in_ts;
+  a.in_es = in_es;
+  a.out_ts = out_ts;
+  a.out_es = out_es;
+  a.T = T;
+  a.N = N;
+  a.gamma = gamma;
+  a.lam = lam;
+  return launch(c, K_GAE, (unsigned)cdiv(N, kThreads), 1, 1, a);
+}
+
+}  // extern "C"
+
+namespace zl {
+// Three-launch deterministic normalisation with caller scratch (2*nparts floats).
+zl_status adv_normalize_into(zl_ctx* c, float* adv, long long n, float* scratch, int nparts,
+                             int chunk, const int* guard) {
+  zk::AdvNormArgs a{};
+  a.x = adv;
+  a.part = scratch;
+  a.part2 = scratch + nparts;
+  a.guard = guard;
+  a.n = n;
+  a.nparts = nparts;
+  a.chunk = chunk;
+  for (int ph = 0; ph < 3; ++ph) {
+    a.phase = ph;
+    zl_status s = launch(c, K_ADV_NORM, (unsigned)nparts, 1, 1, a);
+    if (s) return s;
+  }
+  return ZL_OK;
+}
+}  // namespace zl
+
+extern "C" {
+
+zl_status zl_adv_normalize(zl_ctx* c, float* adv, size_t n) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!adv || n == 0) return fail(c, ZL_ERR_INVALID, "zl_adv_normalize: bad argument");
+  const int chunk = 4096;
+  const int nparts = (int)cdiv((long long)n, chunk);
+  zl_status s = ensure_ws(c, (size_t)2 * nparts);
+  if (s) return s;
+  return adv_normalize_into(c, adv, (long long)n, c->ws, nparts, chunk, nullptr);
+}
+
+zl_status zl_sample_actions(zl_ctx* c, const float* mean, int ld_mean, const float* log_std,
+                            const float* eps, int rows, int A, float* action, float* logp) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!mean || !log_std || !eps || !action || !logp || rows < 0 || A < 1 || ld_mean < A)
+    return fail(c, ZL_ERR_INVALID, "zl_sample_actions: bad argument");
+  zk::SampleArgs a{};
+  a.mean = mean;
+  a.log_std = log_std;
+  a.eps = eps;
+  a.action = action;
+  a.logp = logp;
+  a.rows = rows;
+  a.A = A;
+  a.ldm = ld_mean;
+  a.lde = A;
+  a.lda = A;
+  return launch(c, K_SAMPLE, (unsigned)cdiv(rows, kThreads), 1, 1, a);
+}
+
+}  // extern "C"

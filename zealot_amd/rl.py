@@ -1,0 +1,302 @@
+"""zealot-rl's learning-tier API on the MI355X path.
+
+Names and argument meanings follow the reference (zealot-rl/src/net.rs,
+ppo.rs; the GPU trainer's GpuMlp in src/bin/biped_train_gpu.rs); every call
+goes through libzealot_hip.so's C ABI. Parameters cross as the packed
+layout w[0], b[0], w[1], b[1], ... with w[l] row-major [dims[l+1] x dims[l]]
+(zealot-rl/src/net.rs:30-34).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _ffi
+from .device import Context, DeviceBuffer
+
+
+def _fptr(a: np.ndarray) -> C.c_void_p:
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def packed_count(dims) -> int:
+    return int(sum(dims[l + 1] * dims[l] + dims[l + 1] for l in range(len(dims) - 1)))
+
+
+def unpack(dims, packed):
+    """Packed params -> ([w[l] (out x in)], [b[l]])."""
+    ws, bs, o = [], [], 0
+    for l in range(len(dims) - 1):
+        out, inp = dims[l + 1], dims[l]
+        ws.append(np.asarray(packed[o : o + out * inp]).reshape(out, inp))
+        o += out * inp
+        bs.append(np.asarray(packed[o : o + out]))
+        o += out
+    return ws, bs
+
+
+def pack(ws, bs) -> np.ndarray:
+    parts = []
+    for w, b in zip(ws, bs):
+        parts.append(np.asarray(w, np.float32).ravel())
+        parts.append(np.asarray(b, np.float32).ravel())
+    return np.concatenate(parts).astype(np.float32)
+
+
+@dataclass
+class PpoConfig:
+    """zealot-rl/src/ppo.rs:22-65 plus the switches between the reference's
+    two update semantics (ActorCritic::update vs the GPU trainer)."""
+
+    semantics: int = _ffi.ZL_SEMANTICS_ACTOR_CRITIC
+    gamma: float = 0.99
+    lam: float = 0.95
+    clip: float = 0.2
+    entropy_coef: float = 0.01
+    value_coef: float = 1.0
+    epochs: int = 5
+    minibatches: int = 4
+    max_grad_norm: float = 1.0
+    desired_kl: float = 0.01
+    lr_min: float = 1e-5
+    lr_max: float = 1e-2
+    adaptive_lr: bool = True
+    early_stop: bool = False
+    shuffle: bool = True
+    normalize_adv: bool = True
+    clamp_log_std: bool = True
+
+    def to_c(self) -> _ffi.zl_ppo_config:
+        return _ffi.zl_ppo_config(
+            int(self.semantics), self.clip, self.entropy_coef, self.value_coef, int(self.epochs),
+            int(self.minibatches), self.max_grad_norm, self.desired_kl, self.lr_min, self.lr_max,
+            int(self.adaptive_lr), int(self.early_stop), int(self.shuffle),
+            int(self.normalize_adv), int(self.clamp_log_std),
+        )
+
+    @staticmethod
+    def gpu_trainer(**kw) -> "PpoConfig":
+        """The GPU trainer's update (src/bin/biped_train_gpu.rs:53-75, :1164-1553)."""
+        base = dict(
+            semantics=_ffi.ZL_SEMANTICS_GPU_TRAINER, entropy_coef=0.01, value_coef=1.0,
+            adaptive_lr=True, early_stop=True, shuffle=False, normalize_adv=True,
+            clamp_log_std=True,
+        )
+        base.update(kw)
+        return PpoConfig(**base)
+
+
+@dataclass
+class PpoStats:
+    """zealot-rl/src/ppo.rs:90-102 (+ trainer epoch count / KL, pre-clip norms)."""
+
+    kl: float
+    surrogate: float
+    value_loss: float
+    entropy: float
+    lr: float
+    epochs_run: int
+    last_kl: float
+    grad_norm: tuple
+
+
+class GpuMlp:
+    """Device-resident MLP (the GpuMlp of src/bin/biped_train_gpu.rs:316-564)."""
+
+    def __init__(self, ctx: Context, dims, batch: int):
+        self.ctx = ctx
+        self.dims = [int(d) for d in dims]
+        self.batch = int(batch)
+        d = (C.c_int * len(self.dims))(*self.dims)
+        h = C.c_void_p()
+        ctx.check(ctx.lib.zl_mlp_create(ctx.h, d, len(self.dims), self.batch, C.byref(h)), "zl_mlp_create")
+        self.h = h
+        self.n_params = int(ctx.lib.zl_mlp_num_params(h))
+
+    def write_weights(self, packed):
+        a = np.ascontiguousarray(packed, np.float32)
+        assert a.size == self.n_params
+        self.ctx.check(self.ctx.lib.zl_mlp_write_weights(self.h, _fptr(a)), "zl_mlp_write_weights")
+
+    def read_weights(self) -> np.ndarray:
+        out = np.empty(self.n_params, np.float32)
+        self.ctx.check(self.ctx.lib.zl_mlp_read_weights(self.h, _fptr(out)), "zl_mlp_read_weights")
+        return out
+
+    def forward(self, x: DeviceBuffer, rows: int, ldx: int | None = None):
+        ldx = self.dims[0] if ldx is None else ldx
+        self.ctx.check(self.ctx.lib.zl_mlp_forward(self.h, x.p, ldx, rows), "zl_mlp_forward")
+
+    def output(self, rows: int) -> np.ndarray:
+        ld = C.c_int()
+        p = self.ctx.lib.zl_mlp_output(self.h, C.byref(ld))
+        buf = np.empty((rows, ld.value), np.float32)
+        self.ctx.check(
+            self.ctx.lib.zl_download(self.ctx.h, _fptr(buf), C.c_void_p(p), buf.nbytes), "download"
+        )
+        return buf[:, : self.dims[-1]].copy()
+
+    def backward(self, g_out: DeviceBuffer, ld_g: int | None = None):
+        ld_g = self.dims[-1] if ld_g is None else ld_g
+        self.ctx.check(self.ctx.lib.zl_mlp_backward(self.h, g_out.p, ld_g), "zl_mlp_backward")
+
+    def read_grads(self) -> np.ndarray:
+        out = np.empty(self.n_params, np.float32)
+        self.ctx.check(self.ctx.lib.zl_mlp_read_grads(self.h, _fptr(out)), "zl_mlp_read_grads")
+        return out
+
+    def adam(self, lr: float, bc1: float, bc2: float):
+        self.ctx.check(self.ctx.lib.zl_mlp_adam(self.h, lr, bc1, bc2), "zl_mlp_adam")
+
+    def read_moments(self):
+        m = np.empty(self.n_params, np.float32)
+        v = np.empty(self.n_params, np.float32)
+        self.ctx.check(self.ctx.lib.zl_mlp_read_moments(self.h, _fptr(m), _fptr(v)), "read_moments")
+        return m, v
+
+    def write_moments(self, m, v):
+        m = np.ascontiguousarray(m, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        self.ctx.check(self.ctx.lib.zl_mlp_write_moments(self.h, _fptr(m), _fptr(v)), "write_moments")
+
+    def close(self):
+        if self.h:
+            self.ctx.lib.zl_mlp_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.ctx.h:
+                self.close()
+        except Exception:
+            pass
+
+
+class GpuActorCritic:
+    """The ActorCritic of zealot-rl/src/ppo.rs:208-229 resident on one MI355X:
+    actor, critic, log_std and all Adam state in one flat HBM buffer, updated
+    by zl_ppo_update with no host round trip inside the update."""
+
+    def __init__(self, ctx: Context, actor_dims, critic_dims, minibatch_rows: int):
+        self.ctx = ctx
+        self.actor_dims = [int(d) for d in actor_dims]
+        self.critic_dims = [int(d) for d in critic_dims]
+        self.action_dim = self.actor_dims[-1]
+        ad = (C.c_int * len(self.actor_dims))(*self.actor_dims)
+        cd = (C.c_int * len(self.critic_dims))(*self.critic_dims)
+        h = C.c_void_p()
+        ctx.check(
+            ctx.lib.zl_ppo_create(ctx.h, ad, len(ad), cd, len(cd), int(minibatch_rows), C.byref(h)),
+            "zl_ppo_create",
+        )
+        self.h = h
+        self.na = packed_count(self.actor_dims)
+        self.nc = packed_count(self.critic_dims)
+
+    def set_params(self, actor, critic, log_std, lr: float):
+        a = np.ascontiguousarray(actor, np.float32)
+        c = np.ascontiguousarray(critic, np.float32)
+        l = np.ascontiguousarray(log_std, np.float32)
+        assert a.size == self.na and c.size == self.nc and l.size == self.action_dim
+        self.ctx.check(self.ctx.lib.zl_ppo_set_params(self.h, _fptr(a), _fptr(c), _fptr(l), lr), "set_params")
+
+    def get_params(self):
+        a = np.empty(self.na, np.float32)
+        c = np.empty(self.nc, np.float32)
+        l = np.empty(self.action_dim, np.float32)
+        lr = C.c_float()
+        self.ctx.check(
+            self.ctx.lib.zl_ppo_get_params(self.h, _fptr(a), _fptr(c), _fptr(l), C.byref(lr)), "get_params"
+        )
+        return a, c, l, float(lr.value)
+
+    def get_moments(self):
+        out = [np.empty(n, np.float32) for n in (self.na, self.na, self.nc, self.nc, self.action_dim, self.action_dim)]
+        self.ctx.check(self.ctx.lib.zl_ppo_get_moments(self.h, *[_fptr(x) for x in out]), "get_moments")
+        return out
+
+    def reset_optimizer(self):
+        self.ctx.check(self.ctx.lib.zl_ppo_reset_optimizer(self.h), "reset_optimizer")
+
+    def counters(self):
+        t = C.c_int()
+        g = C.c_ulonglong()
+        self.ctx.check(self.ctx.lib.zl_ppo_get_counters(self.h, C.byref(t), C.byref(g)), "counters")
+        return int(t.value), int(g.value)
+
+    def update(self, batch: "DeviceBatch", cfg: PpoConfig) -> PpoStats:
+        st = _ffi.zl_ppo_stats()
+        b = batch.to_c()
+        c = cfg.to_c()
+        self.ctx.check(self.ctx.lib.zl_ppo_update(self.h, C.byref(b), C.byref(c), C.byref(st)), "zl_ppo_update")
+        return PpoStats(st.kl, st.surrogate, st.value_loss, st.entropy, st.lr, st.epochs_run,
+                        st.last_kl, tuple(st.grad_norm))
+
+    def minibatch_grads(self, batch: "DeviceBatch", cfg: PpoConfig, row0: int, rows: int,
+                        perm: DeviceBuffer | None = None):
+        """Gradients of one minibatch (no clip / Adam): returns
+        (actor, critic, log_std packed grads, {surrogate, value_loss, kl})."""
+        st = (C.c_float * 3)()
+        b = batch.to_c()
+        c = cfg.to_c()
+        self.ctx.check(
+            self.ctx.lib.zl_ppo_minibatch_grads(self.h, C.byref(b), C.byref(c), row0, rows,
+                                                perm.p if perm is not None else None, st),
+            "zl_ppo_minibatch_grads",
+        )
+        ga = np.empty(self.na, np.float32)
+        gc = np.empty(self.nc, np.float32)
+        gl = np.empty(self.action_dim, np.float32)
+        self.ctx.check(self.ctx.lib.zl_ppo_get_grads(self.h, _fptr(ga), _fptr(gc), _fptr(gl)), "get_grads")
+        return ga, gc, gl, dict(surrogate=st[0], value_loss=st[1], kl=st[2])
+
+    def values(self, critic_obs: DeviceBuffer, n: int, out: DeviceBuffer, ld: int | None = None):
+        ld = self.critic_dims[0] if ld is None else ld
+        self.ctx.check(self.ctx.lib.zl_ppo_values(self.h, critic_obs.p, ld, n, out.p), "zl_ppo_values")
+
+    def actor_mean(self, obs: DeviceBuffer, n: int, out: DeviceBuffer, ld: int | None = None,
+                   ld_out: int | None = None):
+        ld = self.actor_dims[0] if ld is None else ld
+        ld_out = self.action_dim if ld_out is None else ld_out
+        self.ctx.check(self.ctx.lib.zl_ppo_actor_mean(self.h, obs.p, ld, n, out.p, ld_out), "actor_mean")
+
+    def close(self):
+        if self.h:
+            self.ctx.lib.zl_ppo_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            if self.ctx.h:
+                self.close()
+        except Exception:
+            pass
+
+
+class DeviceBatch:
+    """A rollout batch resident on the device (structure of arrays, batch order)."""
+
+    def __init__(self, ctx: Context, obs, critic_obs, action, mean_old, logp_old, value_old, adv, ret):
+        self.ctx = ctx
+        self.n = int(np.asarray(obs).shape[0])
+        self.obs = ctx.to_device(obs, np.float32)
+        self.critic_obs = self.obs if critic_obs is obs else ctx.to_device(critic_obs, np.float32)
+        self.action = ctx.to_device(action, np.float32)
+        self.mean_old = ctx.to_device(mean_old, np.float32) if mean_old is not None else None
+        self.logp_old = ctx.to_device(logp_old, np.float32)
+        self.value_old = ctx.to_device(value_old, np.float32)
+        self.adv = ctx.to_device(adv, np.float32)
+        self.ret = ctx.to_device(ret, np.float32)
+        self.od = self.obs.shape[1]
+        self.cd = self.critic_obs.shape[1]
+        self.ad = self.action.shape[1]
+
+    def to_c(self) -> _ffi.zl_batch:
+        return _ffi.zl_batch(
+            self.n, self.obs.ptr, self.od, self.critic_obs.ptr, self.cd, self.action.ptr, self.ad,
+            self.mean_old.ptr if self.mean_old is not None else None, self.ad,
+            self.logp_old.ptr, self.value_old.ptr, self.adv.ptr, self.ret.ptr,
+        )
