@@ -25,6 +25,7 @@ from zealot_amd.rl import DeviceBatch, GpuActorCritic, PpoConfig
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
+NTHREADS = min(os.cpu_count() or 1, 16)  # the GPU box gives one GPU 16 host cores
 
 
 def per_tensor_err(dims, got, ref):
@@ -53,6 +54,39 @@ def make_batch(n, actor_dims, critic_dims, actor, critic, seed):
     return batch, mb["log_std"]
 
 
+def move_off_branch_boundaries(batch, actor_dims, critic_dims, actor, critic, log_std, clip=0.2,
+                               margin=1e-2):
+    """The clipped objectives are discontinuous: a sample whose ratio sits on
+    1 +- clip (ppo.rs:419-420), or whose clipped and unclipped value losses tie
+    with v_clipped != v (ppo.rs:443), switches its whole gradient on a last-ulp
+    difference of the forward pass, and any two valid fp32 evaluations (rayon's
+    included) may land on either side. With N(0,1) actions the log-probs reach
+    ~-500, where fp32 rounding moves log(ratio) by ~1e-3. Rows within `margin`
+    of a boundary (in log-ratio, resp. relative loss gap) get logp_old / ret
+    nudged clear of it; returns the number of rows moved."""
+    aa = np_ref.forward(actor_dims, actor, batch["obs"])
+    d = batch["action"] - aa[-1]
+    ls = np.asarray(log_std, np.float64)
+    lp = np.sum(-0.5 * (d / np.exp(ls)) ** 2 - ls - np_ref.LOG_SQRT_2PI, axis=1)
+    logr = lp - batch["logp_old"]
+    moved = 0
+    for b in (np.log1p(clip), np.log1p(-clip)):
+        near = np.abs(logr - b) < margin
+        shift = np.where(logr >= b, 2 * margin, -2 * margin)  # push away from b
+        batch["logp_old"] = np.where(near, batch["logp_old"] - shift, batch["logp_old"]).astype(np.float32)
+        logr = np.where(near, logr + shift, logr)
+        moved += int(near.sum())
+    v = np_ref.forward(critic_dims, critic, batch["critic_obs"])[-1][:, 0]
+    vo, R = batch["value_old"].astype(np.float64), batch["ret"].astype(np.float64)
+    vc = vo + np.clip(v - vo, -clip, clip)
+    lu, lc = (v - R) ** 2, (vc - R) ** 2
+    tie = (np.abs(lc - lu) < margin * np.maximum(np.maximum(lc, lu), 1e-6)) & (np.abs(vc - v) > 1e-6)
+    mid = 0.5 * (v + vc)
+    away = np.where(R >= mid, 1.0, -1.0) * 0.05 * np.abs(vc - v)
+    batch["ret"] = np.where(tie, R + away, R).astype(np.float32)
+    return moved + int(tie.sum())
+
+
 def test_minibatch_grads_config4(ctx):
     """Config 4: one 24,576-row minibatch, actor 123-512-256-128-29 + critic
     123-512-256-128-1, clip 0.2, value x1.0, entropy x0.005."""
@@ -63,6 +97,9 @@ def test_minibatch_grads_config4(ctx):
     n = 24_576
     batch, log_std = make_batch(n, ad, cd, actor, critic, seed=synth.SEED_BASE + 4)
     batch["adv"] = zo.adv_normalize(batch["adv"])
+    moved = move_off_branch_boundaries(batch, ad, cd, actor, critic, log_std)
+    print(f"[gpu] config4: {moved} of {n} rows moved off a clip / value-loss branch boundary", flush=True)
+    assert moved < n // 1000
     gac = GpuActorCritic(ctx, ad, cd, n)
     gac.set_params(actor, critic, log_std, 1e-3)
     db = DeviceBatch(ctx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
@@ -71,7 +108,7 @@ def test_minibatch_grads_config4(ctx):
     ga, gc, gl, st = gac.minibatch_grads(db, cfg, 0, n)
     idx = np.arange(n)
     ra, rc, rl, rst = zo.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.005, 1.0,
-                                         nthreads=os.cpu_count() or 8)
+                                         nthreads=NTHREADS)
     ta, tc, tl, tst = np_ref.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.005, 1.0)
     e = dict(
         actor=per_tensor_err(ad, ga, ra), critic=per_tensor_err(cd, gc, rc), log_std=rel_amax(gl, rl),
@@ -94,6 +131,7 @@ def test_minibatch_grads_with_perm(ctx):
     critic = synth.kaiming_uniform_net(g, cd, 0.1)
     n = 5000
     batch, log_std = make_batch(n, ad, cd, actor, critic, seed=99)
+    move_off_branch_boundaries(batch, ad, cd, actor, critic, log_std)
     perm = g.permutation(n).astype(np.int32)
     gac = GpuActorCritic(ctx, ad, cd, 1500)
     gac.set_params(actor, critic, log_std, 1e-3)
@@ -125,6 +163,7 @@ def _small_problem(seed, n=8192):
     actor = synth.kaiming_uniform_net(g, SMALL_A, 0.05)
     critic = synth.kaiming_uniform_net(g, SMALL_C, 0.05)
     batch, log_std = make_batch(n, SMALL_A, SMALL_C, actor, critic, seed + 1)
+    move_off_branch_boundaries(batch, SMALL_A, SMALL_C, actor, critic, log_std)
     return actor, critic, log_std, batch
 
 
@@ -137,7 +176,7 @@ def test_update_actor_critic_semantics(ctx, adaptive):
     ac = zo.ActorCritic(SMALL_A, SMALL_C, 1.0, lr0, 1)
     ac.set(actor, critic, log_std, lr0)
     cfg_o = zo.PpoCfg(0.99, 0.95, 0.2, 0.01, 1.0, 5, 4, 1.0, 0.01, 1e-5, 1e-2, int(adaptive))
-    stats_o, adv_o = ac.update(batch, cfg_o, nthreads=os.cpu_count() or 8, normalize_obs=False)
+    stats_o, adv_o = ac.update(batch, cfg_o, nthreads=NTHREADS, normalize_obs=False)
     ao, co, lso, lro, to = ac.get()
 
     gac = GpuActorCritic(ctx, SMALL_A, SMALL_C, batch["obs"].shape[0] // 4)
@@ -177,7 +216,7 @@ def test_update_gpu_trainer_semantics(ctx, early):
     tr = zo.Trainer(SMALL_A, SMALL_C, actor, critic, log_std, lr0)
     desired = 0.002 if early else 0.01
     cfg_o = zo.TrainerCfg(0.2, 0.01, 1.0, 5, 4, 1.0, desired, 1e-5, 1e-2, 1, int(early), 1)
-    so = tr.update(batch, cfg_o, nthreads=os.cpu_count() or 8)
+    so = tr.update(batch, cfg_o, nthreads=NTHREADS)
     ao, co, lso, lro, gso = tr.get()
 
     gac = GpuActorCritic(ctx, SMALL_A, SMALL_C, batch["obs"].shape[0] // 4)
@@ -196,7 +235,7 @@ def test_update_gpu_trainer_semantics(ctx, early):
     print(f"[gpu] trainer update early={early}: epochs gpu {st.epochs_run} cpu {int(so[5])} "
           f"kl {st.last_kl:.4e} vs {so[6]:.4e} lr {lrg} vs {lro} actor {rep_a} critic {rep_c}", flush=True)
     assert st.epochs_run == int(so[5])
-    assert gstep == gso == 5 * 4
+    assert gstep == gso == 4 * st.epochs_run  # gstep += n_mb per epoch that ran (:1165)
     assert abs(st.last_kl - so[6]) <= 1e-3 * max(abs(so[6]), 1e-4)
     assert lrg == pytest.approx(lro, rel=1e-6)
     assert np.all(lsg <= 0.0) and np.all(lsg >= -1.6)
