@@ -31,61 +31,28 @@ N_ENVS, T_STEPS = 4096, 24
 EPOCHS, MINIBATCHES = 5, 4
 FP32_MFMA_PEAK = 157.3e12  # MI355X dense fp32 matrix, FLOP/s
 HBM_PEAK = 8.0e12  # bytes/s
-GEMM_KERNELS = [
-    "zk_gemm_ak_bk_64x128", "zk_gemm_ak_bk_128x32", "zk_gemm_ak_bk_256x16",
-    "zk_gemm_ak_bn_64x128", "zk_gemm_am_bn_64x128", "zk_splitk_reduce",
-]
-OTHER_KERNELS = ["zk_actor_loss", "zk_value_loss", "zk_sumsq", "zk_finalize", "zk_adam",
-                 "zk_gae", "zk_adv_norm", "zk_epoch_begin", "zk_epoch_end", "zk_copy_rows"]
 
 
-def fwd_kernel(n_out: int) -> str:
-    if n_out <= 16:
-        return "zk_gemm_ak_bk_256x16"
-    if n_out <= 32:
-        return "zk_gemm_ak_bk_128x32"
-    return "zk_gemm_ak_bk_64x128"
-
-
-def gemm_launches(actor_dims, critic_dims, mb, n_value_rows, chunk):
-    """(kernel, algorithmic FLOP) of every GEMM launch in one step."""
-    out = []
-    for dims in (critic_dims,):  # value forward, chunked by the minibatch capacity
-        r = n_value_rows
-        while r > 0:
-            rows = min(chunk, r)
-            for l in range(len(dims) - 1):
-                out.append((fwd_kernel(dims[l + 1]), 2 * rows * dims[l] * dims[l + 1]))
-            r -= rows
-    for _ in range(EPOCHS * MINIBATCHES):
-        for dims in (actor_dims, critic_dims):
-            for l in range(len(dims) - 1):
-                out.append((fwd_kernel(dims[l + 1]), 2 * mb * dims[l] * dims[l + 1]))
-            for l in range(len(dims) - 1):
-                out.append(("zk_gemm_am_bn_64x128", 2 * mb * dims[l] * dims[l + 1]))
-                if l > 0:
-                    out.append(("zk_gemm_ak_bn_64x128", 2 * mb * dims[l] * dims[l + 1]))
-    return out
-
-
-def cpu_baseline(ro, actor, critic, log_std, mean_old, action, logp_old, values, adv, ret):
-    """The oracle's restatement of the trainer update on a bounded sample:
-    one 24,576-row minibatch (fwd + bwd + clip + Adam) of the same rollout."""
+def cpu_baseline(ro, actor, critic, log_std, mean_old, action, logp_old, values, adv):
+    """The oracle's restatement of the same update (GPU-trainer semantics) on
+    the same rollout, timed on the host cores: 5 epochs x 4 minibatches of
+    24,576 rows, actor + critic fwd + bwd + global clip + Adam."""
     from oracle import zl_oracle as zo
     from zealot_amd import synth
 
-    n = 24_576
+    n = ro["obs"].shape[0]
     threads = min(os.cpu_count() or 1, 16)
-    batch = dict(obs=ro["obs"][:n], critic_obs=ro["obs"][:n], action=action[:n], mean_old=mean_old[:n],
-                 logp_old=logp_old[:n], value_old=values[:n], adv=zo.adv_normalize(adv[:n]), ret=ret[:n])
+    batch = dict(obs=ro["obs"], critic_obs=ro["obs"], action=action, mean_old=mean_old,
+                 logp_old=logp_old, value_old=values, adv=zo.adv_normalize(adv[0]), ret=adv[1])
     tr = zo.Trainer(synth.ACTOR_DIMS, synth.CRITIC_DIMS, actor, critic, log_std, 1e-3)
-    cfg = zo.TrainerCfg(0.2, 0.005, 1.0, 1, 1, 1.0, 0.01, 1e-5, 1e-2, 0, 0, 1)
+    cfg = zo.TrainerCfg(0.2, 0.005, 1.0, EPOCHS, MINIBATCHES, 1.0, 0.01, 1e-5, 1e-2, 0, 0, 1)
     t0 = time.perf_counter()
     tr.update(batch, cfg, nthreads=threads)
     dt = time.perf_counter() - t0
-    return {"value": n / dt, "unit": "samples/s", "cores": threads, "kind": "port",
-            "sample": f"1 minibatch of {n} rows of the same rollout (actor+critic fwd+bwd, global "
-                      f"clip, Adam; trainer semantics), {dt:.1f} s on {threads} threads"}
+    return {"value": EPOCHS * n / dt, "unit": "samples/s", "cores": threads, "kind": "port",
+            "sample": f"the same full update ({EPOCHS} epochs x {MINIBATCHES} minibatches of "
+                      f"{n // MINIBATCHES} rows, fwd+bwd+clip+Adam, GPU-trainer semantics) on "
+                      f"{threads} threads: {dt:.1f} s"}
 
 
 def main():
@@ -156,33 +123,33 @@ def main():
     ctx.synchronize()
     t_step = (time.perf_counter() - t0) / args.steps
 
-    # Per-kernel HIP-event timing (one instrumented, eagerly launched step per kernel).
-    launches = gemm_launches(ad, cd, mb, n + N_ENVS, mb)
-    flops_by_k, count_by_k = {}, {}
-    for k, f in launches:
-        flops_by_k[k] = flops_by_k.get(k, 0) + f
-        count_by_k[k] = count_by_k.get(k, 0) + 1
+    # Per-kernel HIP-event timing: one instrumented step (eager launches),
+    # every launch bracketed by events on the context stream.
+    ctx.check(ctx.lib.zl_timing_begin(ctx.h, b"*"), "timing_begin")
+    step()
+    ctx.check(ctx.lib.zl_timing_end(ctx.h, None, None, None), "timing_end")
     ktime = {}
-    names = GEMM_KERNELS + (OTHER_KERNELS if args.breakdown else [])
-    for k in names:
-        ctx.check(ctx.lib.zl_timing_begin(ctx.h, k.encode()), "timing_begin")
-        step()
-        ms, cnt = C.c_double(), C.c_longlong()
-        ctx.check(ctx.lib.zl_timing_end(ctx.h, C.byref(ms), C.byref(cnt)), "timing_end")
-        ktime[k] = (ms.value, cnt.value)
-    gemm_flops = sum(f for _, f in launches)
-    dom = max(flops_by_k, key=lambda k: ktime.get(k, (0, 0))[0])
-    dom_ms, dom_cnt = ktime[dom]
-    dom_avg_s = dom_ms / 1e3 / max(dom_cnt, 1)
-    dom_flop_per_launch = flops_by_k[dom] / count_by_k[dom]
+    for i in range(ctx.lib.zl_kernel_count()):
+        name, ms, cnt, fl = C.c_char_p(), C.c_double(), C.c_longlong(), C.c_double()
+        ctx.check(ctx.lib.zl_timing_kernel(ctx.h, i, C.byref(name), C.byref(ms), C.byref(cnt),
+                                           C.byref(fl)), "timing_kernel")
+        if cnt.value:
+            ktime[name.value.decode()] = (ms.value, cnt.value, fl.value)
+    gemm = {k: v for k, v in ktime.items() if k.startswith("zk_gemm")}
+    gemm_ms = sum(v[0] for v in gemm.values())
+    gemm_flops = sum(v[2] for v in gemm.values())
+    dom = max(gemm, key=lambda k: gemm[k][0])
+    dom_ms, dom_cnt, dom_flops = gemm[dom]
+    dom_avg_s = dom_ms / 1e3 / dom_cnt
+    dom_flop_per_launch = dom_flops / dom_cnt
     achieved = dom_flop_per_launch / dom_avg_s
-    gemm_ms = sum(ktime[k][0] for k in GEMM_KERNELS if k in ktime)
     if args.breakdown:
-        print(f"{'kernel':28s} {'launches':>9s} {'ms/step':>9s} {'us/launch':>10s} {'TFLOP/s':>8s}", file=sys.stderr)
-        for k, (ms, cnt) in sorted(ktime.items(), key=lambda kv: -kv[1][0]):
-            tf = flops_by_k.get(k, 0) / (ms / 1e3) / 1e12 if ms > 0 and k in flops_by_k else 0.0
-            print(f"{k:28s} {cnt:9d} {ms:9.3f} {1e3 * ms / max(cnt, 1):10.2f} {tf:8.2f}", file=sys.stderr)
-        print(f"step {t_step * 1e3:.3f} ms; GEMM kernels {gemm_ms:.3f} ms", file=sys.stderr)
+        print(f"{'kernel':32s} {'launches':>8s} {'ms/step':>8s} {'us/launch':>9s} {'TFLOP/s':>8s}", file=sys.stderr)
+        for k, (ms, cnt, fl) in sorted(ktime.items(), key=lambda kv: -kv[1][0]):
+            tf = fl / (ms / 1e3) / 1e12 if ms > 0 else 0.0
+            print(f"{k:32s} {cnt:8d} {ms:8.3f} {1e3 * ms / cnt:9.2f} {tf:8.2f}", file=sys.stderr)
+        print(f"step {t_step * 1e3:.3f} ms; instrumented step kernels {sum(v[0] for v in ktime.values()):.3f} ms; "
+              f"GEMM kernels {gemm_ms:.3f} ms", file=sys.stderr)
 
     out = {
         "metric": "PPO update samples/sec (fwd+bwd+Adam) on 1 MI355X; % fp32-MFMA peak",
@@ -210,7 +177,7 @@ def main():
         "rollout_samples_per_s": n / t_step,
         "gemm_tflops_per_step": gemm_flops / t_step / 1e12,
         "fp32_mfma_frac_step": gemm_flops / t_step / FP32_MFMA_PEAK,
-        "fp32_mfma_frac_gemm_kernels": gemm_flops / (gemm_ms / 1e3) / FP32_MFMA_PEAK if gemm_ms else None,
+        "fp32_mfma_frac_gemm_kernels": gemm_flops / (gemm_ms / 1e3) / FP32_MFMA_PEAK,
         "roofline": {
             "kernel": dom,
             "bound": "mfma",
@@ -233,7 +200,7 @@ def main():
         ret = d_ret.numpy()
         a_now, c_now, ls_now, _ = gac.get_params()
         out["cpu_baseline"] = cpu_baseline(ro, a_now, c_now, ls_now, mean_old, action, logp_old,
-                                           values, adv, ret)
+                                           values, (adv, ret))
     gac.close()
     ctx.close()
     print(json.dumps(out), flush=True)

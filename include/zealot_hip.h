@@ -65,12 +65,18 @@ const char* zl_version(void);
 /* Per-launch timing of one kernel of the code object (by its symbol name,
  * e.g. "zk_gemm_am_bn_64x128"): every launch of it on ctx is bracketed by
  * hipEvents on the context stream until zl_timing_end, which returns the summed
- * kernel time and the launch count. While timing is on, composite entry
+ * kernel time, the launch count and, for GEMM variants, the summed algorithmic
+ * FLOP (2*M*N*K per GEMM) of those launches. While timing is on, composite entry
  * points launch eagerly instead of replaying their captured graphs. The
  * tracing counterpart of the reference's KHAL_CUDA_PROFILE per-kernel timer
  * (src/bin/iter_e2e_bench.rs:731-735,833-835). */
 zl_status zl_timing_begin(zl_ctx* ctx, const char* kernel_name);
-zl_status zl_timing_end(zl_ctx* ctx, double* total_ms, long long* launches);
+zl_status zl_timing_end(zl_ctx* ctx, double* total_ms, long long* launches, double* flops);
+/* kernel_name "*" times every kernel; the per-kernel split of the last
+ * finished session is then read by kernel index in [0, zl_kernel_count()). */
+int zl_kernel_count(void);
+zl_status zl_timing_kernel(const zl_ctx* ctx, int index, const char** name, double* total_ms,
+                           long long* launches, double* flops);
 /* sizeof(zl_ppo_config), sizeof(zl_batch), sizeof(zl_ppo_stats) as compiled
  * into the library, for binding generators to check their struct layouts. */
 void zl_abi_struct_sizes(size_t out[3]);

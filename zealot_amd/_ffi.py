@@ -91,7 +91,15 @@ SIGNATURES = {
     "zl_version": (C.c_char_p, []),
     "zl_abi_struct_sizes": (None, [C.POINTER(C.c_size_t)]),
     "zl_timing_begin": (C.c_int, [vp, C.c_char_p]),
-    "zl_timing_end": (C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_longlong)]),
+    "zl_timing_end": (
+        C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_longlong), C.POINTER(C.c_double)]
+    ),
+    "zl_kernel_count": (C.c_int, []),
+    "zl_timing_kernel": (
+        C.c_int,
+        [vp, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_longlong),
+         C.POINTER(C.c_double)],
+    ),
     "zl_alloc": (C.c_int, [vp, C.c_size_t, C.POINTER(vp)]),
     "zl_free": (C.c_int, [vp, vp]),
     "zl_upload": (C.c_int, [vp, vp, vp, C.c_size_t]),

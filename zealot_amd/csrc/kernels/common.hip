@@ -34,6 +34,23 @@ __device__ __forceinline__ float powi_f32(float x, int n) {
   return n < 0 ? 1.0f / y : y;
 }
 
+// Deterministic butterfly sum over the 64 lanes of a wavefront (lane 0's
+// result is the same on every run; all lanes hold a total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) v = v + __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Fixed-order sum of x[0], x[stride], ... (n terms) by one wavefront: lane l
+// adds terms l, l+64, ... in order, then the lanes are combined by wave_sum.
+__device__ __forceinline__ float wave_sum_strided(const float* x, int n, int stride) {
+  const int lane = threadIdx.x & 63;
+  float s = 0.f;
+  for (int i = lane; i < n; i += 64) s += x[(long long)i * stride];
+  return wave_sum(s);
+}
+
 // Deterministic in-block tree sum over kThreads values held one per thread.
 // `sm` must hold kThreads floats. Returns the total in every thread.
 __device__ __forceinline__ float block_sum(float v, float* sm) {

@@ -9,10 +9,11 @@
 // B + n*ldb) or N-contiguous (row k at B + k*ldb). Each operand tile is staged
 // in LDS in its global orientation (float4 global loads -> ds_write_b128) and
 // fed to the MFMA with one ds_read_b32 per lane per k-step; the row padding of
-// each LDS orientation makes those reads bank-conflict free. A 256-thread
-// workgroup is 4 wave64s in a WM x WN grid; each wave owns TM x TN 16x16
-// accumulator tiles. K is walked in 16-wide k-tiles, double-buffered in LDS
-// with the next k-tile's global loads in flight during the MFMAs.
+// each LDS orientation makes those reads bank-conflict free. A workgroup is
+// WM x WN wave64s; each wave owns TM x TN 16x16 accumulator tiles. K is walked
+// in BK-wide k-tiles, double-buffered in LDS with the next k-tile's global
+// loads in flight during the MFMAs. BK = 32 makes every K-contiguous row
+// segment a full 128-byte line.
 //
 // Split-K: grid.z slices the k-tiles; each slice writes a dense partial
 // [M x N] at C + z*split_stride and zk_splitk_reduce sums the slices in fixed
@@ -23,16 +24,18 @@
 
 namespace zk {
 
-constexpr int kBK = 16;
-
-// One operand tile: EXT rows/cols along M (or N) by kBK along K.
-template <int EXT, bool KC>
+// One operand tile of NT threads: EXT rows/cols along M (or N) by BK along K.
+template <int EXT, bool KC, int BK, int NT>
 struct Tile {
-  static constexpr int LD = KC ? (kBK + 4) : (EXT + 16);
-  static constexpr int SIZE = KC ? EXT * LD : kBK * LD;
-  static constexpr int ELEMS = EXT * kBK;
-  static constexpr int NV = (ELEMS / 4 + kThreads - 1) / kThreads;
-  static constexpr int NS = (ELEMS + kThreads - 1) / kThreads;
+  // Row length in LDS. K-contiguous rows get +4 floats so 16 rows read at one
+  // k hit distinct banks; the other orientation needs LD = 16 or 48 (mod 64)
+  // so the four 16-lane k-groups of one read land in disjoint bank windows.
+  static constexpr int LD =
+      KC ? (BK + 4) : ((EXT % 64 == 16 || EXT % 64 == 48) ? EXT : EXT + 16);
+  static constexpr int SIZE = KC ? EXT * LD : BK * LD;
+  static constexpr int ELEMS = EXT * BK;
+  static constexpr int NV = (ELEMS / 4 + NT - 1) / NT;
+  static constexpr int NS = (ELEMS + NT - 1) / NT;
   static constexpr int NR = (4 * NV > NS) ? 4 * NV : NS;
   float r[NR];
 
@@ -44,11 +47,11 @@ struct Tile {
     if (vec) {
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        const int i = t + j * kThreads;
+        const int i = t + j * NT;
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (i < ELEMS / 4) {
           if (KC) {
-            const int row = i / (kBK / 4), kq = (i % (kBK / 4)) * 4;
+            const int row = i / (BK / 4), kq = (i % (BK / 4)) * 4;
             const int e = e0 + row, k = k0 + kq;
             if (e < etot && k < K) {
               const int sr = perm ? perm[e] : e;
@@ -77,11 +80,11 @@ struct Tile {
     } else {
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
-        const int i = t + j * kThreads;
+        const int i = t + j * NT;
         float v = 0.f;
         if (i < ELEMS) {
           if (KC) {
-            const int e = e0 + i / kBK, k = k0 + i % kBK;
+            const int e = e0 + i / BK, k = k0 + i % BK;
             if (e < etot && k < K) v = base[(long long)(perm ? perm[e] : e) * ld + k];
           } else {
             const int k = k0 + i / EXT, e = e0 + i % EXT;
@@ -99,11 +102,11 @@ struct Tile {
     if (vec) {
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        const int i = t + j * kThreads;
+        const int i = t + j * NT;
         if (i < ELEMS / 4) {
           float4 v = make_float4(r[4 * j], r[4 * j + 1], r[4 * j + 2], r[4 * j + 3]);
           if (KC)
-            *reinterpret_cast<float4*>(s + (i / (kBK / 4)) * LD + (i % (kBK / 4)) * 4) = v;
+            *reinterpret_cast<float4*>(s + (i / (BK / 4)) * LD + (i % (BK / 4)) * 4) = v;
           else
             *reinterpret_cast<float4*>(s + (i / (EXT / 4)) * LD + (i % (EXT / 4)) * 4) = v;
         }
@@ -111,10 +114,10 @@ struct Tile {
     } else {
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
-        const int i = t + j * kThreads;
+        const int i = t + j * NT;
         if (i < ELEMS) {
           if (KC)
-            s[(i / kBK) * LD + i % kBK] = r[j];
+            s[(i / BK) * LD + i % BK] = r[j];
           else
             s[(i / EXT) * LD + i % EXT] = r[j];
         }
@@ -128,25 +131,37 @@ struct Tile {
   }
 };
 
-template <bool AK, bool BKC, int BM, int BN, int WM, int WN>
+// KG > 1 splits every staged k-tile between KG groups of WM x WN waves (group
+// g runs k-steps [g, g+1) * BK/4/KG); the groups' accumulators are added in
+// LDS in group order before the epilogue, so a tile gets KG times the waves
+// without any global split-K partials.
+template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, int KG = 1>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
-  static_assert(WM * WN == kThreads / 64, "4 waves per workgroup");
+  constexpr int NT = 64 * WM * WN * KG;
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
-  static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 16x16 MFMA tile");
-  constexpr int RSG = kThreads / BM;  // row-sum groups (threads per A row)
-  static_assert(RSG >= 1 && kBK % RSG == 0, "row-sum split");
-  using TA = Tile<BM, AK>;
-  using TB = Tile<BN, BKC>;
-  __shared__ float sA[2][TA::SIZE];
-  __shared__ float sB[2][TB::SIZE];
+  static_assert(TM >= 1 && TN >= 1 && TM * WM * 16 == BM && TN * WN * 16 == BN, "wave tiling");
+  static_assert(BK % (4 * KG) == 0, "k-steps of 4 per group");
+  static_assert(KG == 1 || KG == 2, "one LDS exchange round");
+  constexpr int RSG = NT / BM >= 1 ? NT / BM : 1;  // threads per A row in the row sums
+  using TA = Tile<BM, AK, BK, NT>;
+  using TB = Tile<BN, BKC, BK, NT>;
+  constexpr int SMEM = 2 * (TA::SIZE + TB::SIZE);
+  static_assert(KG == 1 || SMEM >= BM * BN, "LDS holds one group's accumulator tile");
+  static_assert(SMEM >= NT, "LDS holds one float per thread for the row sums");
+  // One allocation: [A buf 0][A buf 1][B buf 0][B buf 1], reused after the
+  // k-loop for the row-sum and k-group exchanges.
+  __shared__ float smem[SMEM];
+  auto sA = [&](int b) { return smem + b * TA::SIZE; };
+  auto sB = [&](int b) { return smem + 2 * TA::SIZE + b * TB::SIZE; };
 
   if (p.guard && *p.guard == 0) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave_all = tid >> 6;
+  const int kg = wave_all / (WM * WN), wave = wave_all % (WM * WN);
   const int wm = wave % WM, wn = wave / WM;
   const int lr = lane & 15, lg = lane >> 4;
   const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
-  const int KT = (p.K + kBK - 1) / kBK;
+  const int KT = (p.K + BK - 1) / BK;
   const int kt0 = blockIdx.z * p.kt_per_split;
   const int kt1 = min(KT, kt0 + p.kt_per_split);
   const bool rowsum = p.rowsumA != nullptr && blockIdx.y == 0;
@@ -162,12 +177,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
   TB tb;
   float rs = 0.f;
   const int rs_m = tid % BM, rs_g = tid / BM;
+  const bool rs_on = rowsum && tid < BM * RSG;
 
   if (kt0 < kt1) {
-    ta.load(p.A, p.lda, m0, p.M, kt0 * kBK, p.K, p.permA, vA);
-    tb.load(p.B, p.ldb, n0, p.N, kt0 * kBK, p.K, p.permB, vB);
-    ta.store(sA[0], vA);
-    tb.store(sB[0], vB);
+    ta.load(p.A, p.lda, m0, p.M, kt0 * BK, p.K, p.permA, vA);
+    tb.load(p.B, p.ldb, n0, p.N, kt0 * BK, p.K, p.permB, vB);
+    ta.store(sA(0), vA);
+    tb.store(sB(0), vB);
   }
   __syncthreads();
 
@@ -175,13 +191,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     const int cur = (kt - kt0) & 1;
     const bool more = kt + 1 < kt1;
     if (more) {
-      ta.load(p.A, p.lda, m0, p.M, (kt + 1) * kBK, p.K, p.permA, vA);
-      tb.load(p.B, p.ldb, n0, p.N, (kt + 1) * kBK, p.K, p.permB, vB);
+      ta.load(p.A, p.lda, m0, p.M, (kt + 1) * BK, p.K, p.permA, vA);
+      tb.load(p.B, p.ldb, n0, p.N, (kt + 1) * BK, p.K, p.permB, vB);
     }
-    const float* as = sA[cur];
-    const float* bs = sB[cur];
+    const float* as = sA(cur);
+    const float* bs = sB(cur);
 #pragma unroll
-    for (int s = 0; s < kBK / 4; ++s) {
+    for (int s = kg * (BK / 4 / KG); s < (kg + 1) * (BK / 4 / KG); ++s) {
       const int kk = 4 * s + lg;
       float af[TM], bf[TN];
 #pragma unroll
@@ -194,27 +210,49 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
         for (int j = 0; j < TN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (rowsum) {
-#pragma unroll
-      for (int j = 0; j < kBK / RSG; ++j) rs += TA::at(as, rs_m, rs_g * (kBK / RSG) + j);
+    if (rs_on) {
+      for (int kk = rs_g; kk < BK; kk += RSG) rs += TA::at(as, rs_m, kk);
     }
     if (more) {
-      ta.store(sA[cur ^ 1], vA);
-      tb.store(sB[cur ^ 1], vB);
+      ta.store(sA(cur ^ 1), vA);
+      tb.store(sB(cur ^ 1), vB);
     }
     __syncthreads();
   }
 
   if (rowsum) {
-    float* red = sA[0];  // free after the final barrier
-    red[tid] = rs;
+    float* red = smem;  // free after the final barrier
+    red[tid] = rs_on ? rs : 0.f;
     __syncthreads();
     if (tid < BM) {
       float tot = 0.f;
-#pragma unroll
       for (int g = 0; g < RSG; ++g) tot += red[g * BM + tid];
       if (m0 + tid < p.M) p.rowsumA[(long long)blockIdx.z * p.M + m0 + tid] = tot;
     }
+    __syncthreads();
+  }
+
+  if constexpr (KG > 1) {
+    // Group 1 hands its accumulators to group 0 through LDS (free after the
+    // k-loop and the row-sum barrier).
+    float* xch = smem;
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xch[(((wave * TM + i) * TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg != 0) return;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[i][j][r] = acc[i][j][r] + xch[(((wave * TM + i) * TN + j) * 4 + r) * 64 + lane];
   }
 
   float* C = p.C + (long long)blockIdx.z * p.split_stride;
@@ -244,38 +282,98 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
   }
 }
 
-
-// out[(i / cols) * ldo + i % cols] = sum_z part[z*mn + i] (z ascending);
-// rowout likewise. One thread per output element; the grid covers mn + rows.
+// out[(i / cols) * ldo + i % cols] = sum_z part[z*mn + i], rowout likewise.
+// Each block covers 64 float4 output quads with 4 split groups per quad
+// (group g sums slices g, g+4, ...); the groups are then added 0+1+2+3.
+// The order is fixed, so the result is deterministic. Blocks past the matrix
+// part reduce the row sums (one thread per row, splits in order).
 __device__ __forceinline__ void splitk_reduce_body(const SplitReduceArgs& p) {
+  __shared__ float4 red[4][64];
   if (p.guard && *p.guard == 0) return;
-  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
-  if (i < p.mn) {
-    float s = 0.f;
-    for (int z = 0; z < p.splits; ++z) s += p.part[(long long)z * p.mn + i];
-    p.out[(i / p.cols) * p.ldo + i % p.cols] = s;
-  } else if (p.rowpart && i < p.mn + p.rows) {
-    const int r = (int)(i - p.mn);
-    float s = 0.f;
-    for (int z = 0; z < p.splits; ++z) s += p.rowpart[(long long)z * p.rows + r];
-    p.rowout[r] = s;
+  const long long nq = (p.mn + 3) / 4;
+  const long long nqb = (nq + 63) / 64;  // blocks of the matrix part
+  if ((long long)blockIdx.x < nqb) {
+    const int q_local = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const long long q = (long long)blockIdx.x * 64 + q_local;
+    const bool vec = (p.mn & 3) == 0;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q < nq) {
+      const long long i0 = 4 * q;
+      if (vec) {
+        for (int z = g; z < p.splits; z += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(p.part + (long long)z * p.mn + i0);
+          acc.x += v.x;
+          acc.y += v.y;
+          acc.z += v.z;
+          acc.w += v.w;
+        }
+      } else {
+        for (int z = g; z < p.splits; z += 4) {
+          const float* b = p.part + (long long)z * p.mn + i0;
+          acc.x += b[0];
+          if (i0 + 1 < p.mn) acc.y += b[1];
+          if (i0 + 2 < p.mn) acc.z += b[2];
+          if (i0 + 3 < p.mn) acc.w += b[3];
+        }
+      }
+    }
+    red[g][q_local] = acc;
+    __syncthreads();
+    if (g == 0 && q < nq) {
+      float4 s = red[0][q_local];
+#pragma unroll
+      for (int h = 1; h < 4; ++h) {
+        const float4 v = red[h][q_local];
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      }
+      const float o[4] = {s.x, s.y, s.z, s.w};
+      for (int c = 0; c < 4; ++c) {
+        const long long i = 4 * q + c;
+        if (i < p.mn) p.out[(i / p.cols) * p.ldo + i % p.cols] = o[c];
+      }
+    }
+  } else if (p.rowpart) {
+    const long long r = ((long long)blockIdx.x - nqb) * 256 + threadIdx.x;
+    if (r < p.rows) {
+      float s = 0.f;
+      for (int z = 0; z < p.splits; ++z) s += p.rowpart[(long long)z * p.rows + r];
+      p.rowout[r] = s;
+    }
   }
 }
 
 }  // namespace zk
 
-#define ZK_GEMM(NAME, AK, BKC, BM, BN, WM, WN)                           \
-  extern "C" __global__ __launch_bounds__(256) void NAME(zk::GemmArgs p) { \
-    zk::gemm_body<AK, BKC, BM, BN, WM, WN>(p);                           \
+#define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, KG)                                   \
+  extern "C" __global__ __launch_bounds__(64 * WM * WN * KG) void NAME(zk::GemmArgs p) { \
+    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, KG>(p);                                   \
   }
 
-// Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous.
-ZK_GEMM(zk_gemm_ak_bk_64x128, true, true, 64, 128, 2, 2)
-ZK_GEMM(zk_gemm_ak_bk_128x32, true, true, 128, 32, 4, 1)
-ZK_GEMM(zk_gemm_ak_bk_256x16, true, true, 256, 16, 4, 1)
-ZK_GEMM(zk_gemm_ak_bn_64x128, true, false, 64, 128, 2, 2)
-ZK_GEMM(zk_gemm_am_bn_64x128, false, false, 64, 128, 2, 2)
-ZK_GEMM(zk_gemm_am_bk_64x128, false, true, 64, 128, 2, 2)
+// Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous,
+// then BMxBNxBK, the wave grid WMxWN and (k2) two k-groups per tile.
+ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22, true, true, 64, 128, 16, 2, 2, 1)
+ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, 1)
+ZK_GEMM(zk_gemm_ak_bk_96x128x16_w24, true, true, 96, 128, 16, 2, 4, 1)
+ZK_GEMM(zk_gemm_ak_bk_96x128x32_w22k2, true, true, 96, 128, 32, 2, 2, 2)
+ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, 1)
+ZK_GEMM(zk_gemm_ak_bk_96x32x32_w21, true, true, 96, 32, 32, 2, 1, 1)
+ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, 1)
+ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, 1)
+ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, 1)
+ZK_GEMM(zk_gemm_ak_bn_96x128x16_w24, true, false, 96, 128, 16, 2, 4, 1)
+ZK_GEMM(zk_gemm_ak_bn_96x128x32_w22k2, true, false, 96, 128, 32, 2, 2, 2)
+ZK_GEMM(zk_gemm_am_bn_64x128x16_w22, false, false, 64, 128, 16, 2, 2, 1)
+ZK_GEMM(zk_gemm_am_bn_64x128x16_w24, false, false, 64, 128, 16, 2, 4, 1)
+ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, 1)
+ZK_GEMM(zk_gemm_am_bn_64x128x32_w22k2, false, false, 64, 128, 32, 2, 2, 2)
+ZK_GEMM(zk_gemm_am_bn_128x128x16_w24, false, false, 128, 128, 16, 2, 4, 1)
+ZK_GEMM(zk_gemm_am_bn_128x128x32_w22k2, false, false, 128, 128, 32, 2, 2, 2)
+ZK_GEMM(zk_gemm_am_bn_64x64x16_w22, false, false, 64, 64, 16, 2, 2, 1)
+ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, 1)
+ZK_GEMM(zk_gemm_am_bk_64x128x16_w22, false, true, 64, 128, 16, 2, 2, 1)
 
 extern "C" __global__ __launch_bounds__(256) void zk_splitk_reduce(zk::SplitReduceArgs p) {
   zk::splitk_reduce_body(p);

@@ -11,75 +11,91 @@ namespace zk {
 
 // ------------------------------------------------------------------ losses
 
+// Sum of v over lanes base .. base+n-1 of the wavefront, added left to right
+// like the reference's serial loops over action components; every lane gets
+// the result. The log-probabilities reach a few hundred in magnitude, where a
+// different summation order moves the PPO ratio by ~1e-5 relative, so the
+// order is kept.
+__device__ __forceinline__ float lanes_sum_ordered(float v, int base, int n) {
+  float s = 0.f;
+  for (int j = 0; j < n; ++j) s += __shfl(v, base + j, 64);
+  return s;
+}
+
 // Per-sample body of zealot-rl/src/ppo.rs:411-432 and :452 (actor half of
-// minibatch_step), one thread per sample; the per-sample log_std gradient and
-// statistics are reduced per block in a fixed tree (the rayon fold of
-// :406-462 has no fixed order either).
+// minibatch_step). One lane group per sample with lane k holding action
+// component k, so a sample's mean / action / gradient rows are read and
+// written as contiguous runs; the sums over components (logp, KL) run over
+// the group's lanes in component order. Each lane accumulates its
+// component's log_std gradient over the samples its group visits (in order),
+// and the groups of a block are then combined in a fixed order:
+// deterministic per-block partials (the rayon fold of :406-462 has no fixed
+// order either).
 __device__ void actor_loss_body(const ActorLossArgs& p) {
-  extern __shared__ float sm[];  // [kThreads * A] + [kThreads]
+  constexpr int kMaxGroups = kThreads / 32;
+  __shared__ float sh_g[kMaxGroups][64];
+  __shared__ float sh_s[kMaxGroups][2];
   if (p.guard && *p.guard == 0) return;
   const int t = threadIdx.x;
-  const int r = blockIdx.x * kThreads + t;
+  const int G = p.group;
+  const int ng = kThreads / G;
+  const int grp = t / G, k = t % G;
+  const int base = (t & 63) - k;  // first lane of this group in the wavefront
   const int A = p.A;
-  float* contrib = sm;                   // [kThreads][A]
-  float* red = sm + kThreads * A;        // [kThreads]
-  float surr_c = 0.f, kl_c = 0.f;
-  if (r < p.rows) {
+  const bool on = k < A;
+  const float ls = on ? p.log_std[k] : 0.f;
+  const float sd = expf(ls);
+  const float inv_var = expf(-2.0f * ls);
+  const float inv_sd = expf(-ls);
+  const float lo = 1.0f - p.clip, hi = 1.0f + p.clip;
+  float gacc = 0.f, sacc = 0.f, kacc = 0.f;
+  const int r0 = blockIdx.x * p.rows_per_block;
+  const int r1 = min(p.rows, r0 + p.rows_per_block);
+  for (int r = r0 + grp; r < r1; r += ng) {
     const long long s = p.perm ? p.perm[p.row0 + r] : (long long)(p.row0 + r);
-    const float* mu = p.mean + (long long)r * p.ldm;
-    const float* act = p.action + s * p.ldact;
-    float lp = 0.f;
-    for (int k = 0; k < A; ++k) {  // ActorCritic::logp, ppo.rs:297-305
-      const float ls = p.log_std[k];
-      const float sd = expf(ls);
-      const float d = (act[k] - mu[k]) / sd;
-      lp += -0.5f * d * d - ls - kLogSqrt2Pi;
-    }
+    const float mu = on ? p.mean[(long long)r * p.ldm + k] : 0.f;
+    const float act = on ? p.action[s * p.ldact + k] : 0.f;
+    // ActorCritic::logp, ppo.rs:297-305
+    const float dz = (act - mu) / sd;
+    const float lp = lanes_sum_ordered(on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f, base, A);
     const float ratio = expf(lp - p.logp_old[s]);
     const float a = p.adv[s];
-    const float lo = 1.0f - p.clip, hi = 1.0f + p.clip;
     const float surr = fminf(ratio * a, clampf(ratio, lo, hi) * a);
-    surr_c = surr * p.scale;
     const bool clipped = (a >= 0.0f && ratio > hi) || (a < 0.0f && ratio < lo);
-    float* dl = p.delta + (long long)r * p.ldd;
-    for (int k = 0; k < A; ++k) {
-      const float inv_var = expf(-2.0f * p.log_std[k]);
-      float gm = 0.f, c = 0.f;
-      if (!clipped) {
-        const float d = act[k] - mu[k];
-        gm = -(a * ratio * d * inv_var) * p.scale;
-        const float dls = a * ratio * ((d * d) * inv_var - 1.0f);
-        c = -dls * p.scale;
-      }
-      c += -p.entropy_coef * p.scale;
-      dl[k] = gm;
-      contrib[t * A + k] = c;
+    float gm = 0.f, c = 0.f;
+    if (!clipped) {
+      const float d = act - mu;
+      gm = -(a * ratio * d * inv_var) * p.scale;
+      const float dls = a * ratio * ((d * d) * inv_var - 1.0f);
+      c = -dls * p.scale;
     }
+    c += -p.entropy_coef * p.scale;
+    if (on) {
+      p.delta[(long long)r * p.ldd + k] = gm;
+      gacc += c;
+    }
+    sacc += surr * p.scale;
     if (p.mean_old) {  // ActorCritic::kl, ppo.rs:327-334
-      const float* mo = p.mean_old + s * p.ldmo;
-      float klv = 0.f;
-      for (int k = 0; k < A; ++k) {
-        const float inv = expf(-p.log_std[k]);
-        const float y = (mu[k] - mo[k]) * inv;
-        klv += 0.5f * (y * y);
-      }
-      kl_c = klv * p.scale;
+      const float mo = on ? p.mean_old[s * p.ldmo + k] : 0.f;
+      const float y = (mu - mo) * inv_sd;
+      kacc += lanes_sum_ordered(on ? 0.5f * (y * y) : 0.f, base, A) * p.scale;
     }
-  } else {
-    for (int k = 0; k < A; ++k) contrib[t * A + k] = 0.f;
+  }
+  sh_g[grp][k] = gacc;
+  if (k == 0) {
+    sh_s[grp][0] = sacc;
+    sh_s[grp][1] = kacc;
   }
   __syncthreads();
-  // Fixed-tree reduction of the [kThreads][A] contributions over threads.
-  for (int st = kThreads / 2; st > 0; st >>= 1) {
-    for (int i = t; i < st * A; i += kThreads) contrib[i] = contrib[i] + contrib[i + st * A];
-    __syncthreads();
-  }
-  for (int k = t; k < A; k += kThreads) p.gls_part[(long long)blockIdx.x * A + k] = contrib[k];
-  const float s_tot = block_sum(surr_c, red);
-  const float k_tot = block_sum(kl_c, red);
-  if (t == 0) {
-    p.stat_part[blockIdx.x * 2 + 0] = s_tot;
-    p.stat_part[blockIdx.x * 2 + 1] = k_tot;
+  if (t < A) {
+    float g = 0.f;
+    for (int j = 0; j < ng; ++j) g += sh_g[j][t];
+    p.gls_part[(long long)blockIdx.x * A + t] = g;
+  } else if (t == 64 || t == 65) {
+    const int q = t - 64;
+    float v = 0.f;
+    for (int j = 0; j < ng; ++j) v += sh_s[j][q];
+    p.stat_part[blockIdx.x * 2 + q] = v;
   }
 }
 
@@ -146,36 +162,52 @@ __device__ void sumsq_body(const SumsqArgs& p) {
 // semantics) or src/bin/biped_train_gpu.rs:1350-1452 (trainer semantics),
 // with every scalar kept on the device.
 __device__ void finalize_body(const FinalizeArgs& p) {
-  __shared__ float sg[256];
+  // Quantities 0..4: surrogate, kl, value loss, actor and critic squared
+  // norms; 5..5+A-1: the log_std gradient. Each is one wavefront's
+  // fixed-order sum over its per-block partials.
+  constexpr int kMaxA = 256;
+  __shared__ float q[5 + kMaxA];
   if (p.guard && *p.guard == 0) return;
   const int t = threadIdx.x;
+  const int wave = t >> 6, lane = t & 63;
   const int A = p.pp.A;
-  for (int k = t; k < A; k += kThreads) {
-    float g = 0.f;
-    for (int b = 0; b < p.nb_a; ++b) g += p.gls_part[(long long)b * A + k];
-    p.g_logstd[k] = g;
-    if (k < 256) sg[k] = g;
+  const int nq = 5 + A;
+  for (int j = wave; j < nq; j += kThreads / 64) {
+    float v;
+    if (j == 0)
+      v = wave_sum_strided(p.astat_part, p.nb_a, 2);
+    else if (j == 1)
+      v = wave_sum_strided(p.astat_part + 1, p.nb_a, 2);
+    else if (j == 2)
+      v = wave_sum_strided(p.vstat_part, p.nb_v, 1);
+    else if (j == 3)
+      v = wave_sum_strided(p.sq_part, p.nsq_a, 1);
+    else if (j == 4)
+      v = wave_sum_strided(p.sq_part + p.nsq_a, p.nsq - p.nsq_a, 1);
+    else
+      v = wave_sum_strided(p.gls_part + (j - 5), p.nb_a, A);
+    if (lane == 0) {
+      q[j] = v;
+      if (j >= 5) p.g_logstd[j - 5] = v;
+    }
   }
   __syncthreads();
-  if (t != 0) return;
+  if (wave != 0) return;
+  // Squared norm of the log_std gradient and the entropy
+  // (ActorCritic::entropy, ppo.rs:308-311, pre-step log_std), lane-strided.
+  const float c = 0.5f + kLogSqrt2Pi;
+  float gl = 0.f, el = 0.f;
+  for (int k = lane; k < A; k += 64) {
+    const float g = q[5 + k];
+    gl += g * g;
+    el += p.log_std[k] + c;
+  }
+  const float sq_l = wave_sum(gl);
+  const float ent = wave_sum(el);
+  if (lane != 0) return;
   DevState* st = p.st;
   const PpoParams& pp = p.pp;
-  float surr = 0.f, kl = 0.f, vloss = 0.f;
-  for (int b = 0; b < p.nb_a; ++b) {
-    surr += p.astat_part[b * 2 + 0];
-    kl += p.astat_part[b * 2 + 1];
-  }
-  for (int b = 0; b < p.nb_v; ++b) vloss += p.vstat_part[b];
-  float sq_a = 0.f, sq_c = 0.f, sq_l = 0.f;
-  for (int b = 0; b < p.nsq_a; ++b) sq_a += p.sq_part[b];
-  for (int b = p.nsq_a; b < p.nsq; ++b) sq_c += p.sq_part[b];
-  for (int k = 0; k < A; ++k) {
-    const float g = k < 256 ? sg[k] : p.g_logstd[k];
-    sq_l += g * g;
-  }
-  float ent = 0.f;  // ActorCritic::entropy, ppo.rs:308-311 (pre-step log_std)
-  const float c = 0.5f + kLogSqrt2Pi;
-  for (int k = 0; k < A; ++k) ent += p.log_std[k] + c;
+  const float surr = q[0], kl = q[1], vloss = q[2], sq_a = q[3], sq_c = q[4];
 
   if (pp.mode == 0) {
     if (pp.adaptive_lr) {  // ppo.rs:476-482

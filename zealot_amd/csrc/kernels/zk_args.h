@@ -91,6 +91,8 @@ struct ActorLossArgs {
   const int* guard;
   int ldm, ldact, ldmo, ldd;
   int row0, rows, A;
+  int rows_per_block;  // samples handled by one block
+  int group;           // lanes per sample: 32 (A <= 32) or 64 (A <= 64)
   float clip, entropy_coef, scale;
 };
 

@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <string>
 #include <vector>
@@ -11,14 +12,10 @@
 
 namespace zl {
 
+// Kernels of the code object. The fixed kernels come first; the GEMM
+// variants (one per layout / tile / wave grid) follow from K_GEMM_BASE.
 enum KernelId : int {
-  K_GEMM_AK_BK_64x128 = 0,
-  K_GEMM_AK_BK_128x32,
-  K_GEMM_AK_BK_256x16,
-  K_GEMM_AK_BN_64x128,
-  K_GEMM_AM_BN_64x128,
-  K_GEMM_AM_BK_64x128,
-  K_SPLITK_REDUCE,
+  K_SPLITK_REDUCE = 0,
   K_ACTOR_LOSS,
   K_VALUE_LOSS,
   K_SUMSQ,
@@ -34,15 +31,48 @@ enum KernelId : int {
   K_COPY_ROWS,
   K_SAMPLE,
   K_CLAMP,
-  K_COUNT
+  K_GEMM_BASE
 };
 
-extern const char* const kKernelNames[K_COUNT];
+// One GEMM variant: operand orientation, tile, k-tile and block size.
+struct GemmKernel {
+  const char* name;
+  bool a_kc, b_kc;
+  int bm, bn, bk, threads;
+};
+
+extern const char* const kFixedNames[K_GEMM_BASE];
+extern const GemmKernel kGemmTable[];
+extern const int kGemmCount;
+int kernel_count();
+const char* kernel_name(int id);
 
 constexpr int kThreads = 256;
 
 inline long long round_up(long long x, long long m) { return (x + m - 1) / m * m; }
 inline long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
+
+// Launch shape of zk_actor_loss: one lane group (32 lanes for A <= 32, else
+// 64) per sample, kThreads / group samples in flight per block, and at most
+// kLossMaxBlocks blocks over the rows (one partial row each).
+constexpr int kLossMaxBlocks = 512;
+struct LossShape {
+  int group, rows_per_block, blocks;
+};
+inline LossShape actor_loss_shape(int rows, int A) {
+  LossShape s;
+  s.group = A <= 32 ? 32 : 64;
+  const int ng = 256 / s.group;
+  s.rows_per_block = (int)std::max<long long>(ng, cdiv(rows, kLossMaxBlocks));
+  s.blocks = rows > 0 ? (int)cdiv(rows, s.rows_per_block) : 0;
+  return s;
+}
+
+// GEMM layouts (A K-/M-contiguous x B K-/N-contiguous).
+enum GemmLayout : int { L_AK_BK = 0, L_AK_BN = 1, L_AM_BN = 2, L_AM_BK = 3 };
+inline int layout_of(bool a_kc, bool b_kc) {
+  return a_kc ? (b_kc ? L_AK_BK : L_AK_BN) : (b_kc ? L_AM_BK : L_AM_BN);
+}
 
 }  // namespace zl
 
@@ -50,7 +80,7 @@ struct zl_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   hipModule_t module = nullptr;
-  hipFunction_t fn[zl::K_COUNT] = {};
+  std::vector<hipFunction_t> fn;  // by kernel id
   std::string err;
   double self_test_err = 0.0;
   // Scratch owned by the context for the stand-alone operators (split-K
@@ -60,9 +90,21 @@ struct zl_ctx {
   size_t ws_floats = 0;
   // Per-launch hipEvent timing of one kernel (zl_timing_begin / _end). While
   // set, composite entry points launch eagerly instead of replaying graphs.
-  int timing_kernel = -1;
+  int timing_kernel = -1;           // kernel id, kTimeAll, or -1 (off)
   std::vector<hipEvent_t> ev_pool;  // pairs: [2i] start, [2i+1] stop
   size_t ev_used = 0;
+  std::vector<int> ev_kernel;       // kernel id of timed launch i
+  std::vector<double> ev_flops;     // algorithmic FLOP of timed launch i
+  double pending_flops = 0.0;       // set by run_gemm for the next launch
+  // Per-kernel results of the last finished timing session.
+  std::vector<double> rep_ms, rep_flops;
+  std::vector<long long> rep_launches;
+  // Tuning overrides (environment, read at zl_init): forced GEMM variant per
+  // layout (ZL_GEMM_AKBK / _AKBN / _AMBN / _AMBK), split-K slice count
+  // (ZL_SPLITK) and the split-K target grid size (ZL_SPLITK_TARGET).
+  int force_gemm[4] = {-1, -1, -1, -1};
+  int force_splits = 0;
+  int splitk_target = 512;
 };
 
 namespace zl {
@@ -76,22 +118,24 @@ zl_status fail(zl_ctx* c, zl_status s, const char* fmt, ...);
       return ::zl::fail((c), ZL_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_)); \
   } while (0)
 
-zl_status timing_mark(zl_ctx* c, bool stop);
+constexpr int kTimeAll = -2;
+zl_status timing_mark(zl_ctx* c, bool stop, int kernel = 0, double flops = 0.0);
 
 template <class Args>
-zl_status launch(zl_ctx* c, KernelId k, unsigned gx, unsigned gy, unsigned gz, const Args& a,
-                 unsigned shmem = 0) {
+zl_status launch(zl_ctx* c, int k, unsigned gx, unsigned gy, unsigned gz, const Args& a,
+                 unsigned shmem = 0, unsigned threads = kThreads) {
   if (gx == 0 || gy == 0 || gz == 0) return ZL_OK;
-  const bool timed = c->timing_kernel == (int)k;
+  const bool timed = c->timing_kernel == k || c->timing_kernel == kTimeAll;
   if (timed) {
-    zl_status s = timing_mark(c, false);
+    zl_status s = timing_mark(c, false, k, c->pending_flops);
     if (s) return s;
   }
+  c->pending_flops = 0.0;
   void* params[] = {(void*)&a};
-  hipError_t e = hipModuleLaunchKernel(c->fn[k], gx, gy, gz, kThreads, 1, 1, shmem, c->stream,
+  hipError_t e = hipModuleLaunchKernel(c->fn[k], gx, gy, gz, threads, 1, 1, shmem, c->stream,
                                        params, nullptr);
   if (e != hipSuccess)
-    return fail(c, ZL_ERR_HIP, "launch %s failed: %s", kKernelNames[k], hipGetErrorString(e));
+    return fail(c, ZL_ERR_HIP, "launch %s failed: %s", kernel_name(k), hipGetErrorString(e));
   return timed ? timing_mark(c, true) : ZL_OK;
 }
 
@@ -124,9 +168,11 @@ struct GemmDesc {
   size_t ws_floats = 0;
 };
 
-// Split-K decision shared by run_gemm and the scratch sizing of composites.
-int gemm_splits(int M, int N, int K, bool a_kc, bool b_kc, int epi);
-size_t gemm_ws_floats(int M, int N, int K, bool a_kc, bool b_kc, int epi);
+// Variant choice and split-K decision shared by run_gemm and the scratch
+// sizing of composites.
+int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc);
+int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);
+size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d);
 zl_status ensure_ws(zl_ctx* c, size_t floats);
 

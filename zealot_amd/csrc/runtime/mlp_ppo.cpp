@@ -108,10 +108,10 @@ struct NetBuffers {
   }
 };
 
-static size_t net_ws_floats(const NetLayout& nl, int rows) {
+static size_t net_ws_floats(const zl_ctx* c, const NetLayout& nl, int rows) {
   size_t w = 0;
   for (int l = 0; l < nl.L; ++l)
-    w = std::max(w, gemm_ws_floats(nl.dims[l + 1], nl.dims[l], rows, false, false, zk::kEpiStore));
+    w = std::max(w, gemm_ws_floats(c, nl.dims[l + 1], nl.dims[l], rows, false, false, zk::kEpiStore));
   return w;
 }
 
@@ -266,7 +266,7 @@ zl_status zl_mlp_create(zl_ctx* c, const int* dims, int nd, int batch, zl_mlp** 
   zl_status s = e == hipSuccess ? ZL_OK : fail(c, ZL_ERR_HIP, "zl_mlp_create: %s", hipGetErrorString(e));
   if (!s) s = p->nb.alloc(c, p->nl, batch);
   if (!s) {
-    p->ws_floats = std::max<size_t>(net_ws_floats(p->nl, batch), 1);
+    p->ws_floats = std::max<size_t>(net_ws_floats(c, p->nl, batch), 1);
     if (hipMalloc((void**)&p->ws, p->ws_floats * 4) != hipSuccess)
       s = fail(c, ZL_ERR_HIP, "zl_mlp_create: scratch alloc failed");
   }
@@ -458,7 +458,7 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
   }
   const int La = p->actor.L, Lc = p->critic.L;
   const int nb = (int)cdiv(pl.mb, kThreads);
-  const unsigned shm = (unsigned)((kThreads * A + kThreads) * 4);
+  const LossShape ls_shape = actor_loss_shape(pl.mb, A);
   const float* log_std = p->params + p->ls_off;
   for (int e = 0; e < pl.epochs; ++e) {
     zk::EpochBeginArgs eb{};
@@ -497,7 +497,9 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       al.clip = cfg->clip;
       al.entropy_coef = cfg->entropy_coef;
       al.scale = pl.pp.scale;
-      if ((s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, al, shm))) return s;
+      al.rows_per_block = ls_shape.rows_per_block;
+      al.group = ls_shape.group;
+      if ((s = launch(c, K_ACTOR_LOSS, (unsigned)ls_shape.blocks, 1, 1, al))) return s;
       zk::ValueLossArgs vl{};
       vl.v = p->cb.act[Lc];
       vl.ldv = p->cb.ld[Lc];
@@ -541,7 +543,7 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       fz.g_logstd = p->grads + p->ls_off;
       fz.guard = guard;
       fz.pp = pl.pp;
-      fz.nb_a = nb;
+      fz.nb_a = ls_shape.blocks;
       fz.nb_v = nb;
       fz.nsq = p->nsq;
       fz.nsq_a = p->nsq_a;
@@ -637,9 +639,9 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
   dalloc((void**)&p->v, bytes);
   if (!s) s = p->ab.alloc(c, p->actor, mb);
   if (!s) s = p->cb.alloc(c, p->critic, mb);
-  p->ws_floats = std::max<size_t>(std::max(net_ws_floats(p->actor, mb), net_ws_floats(p->critic, mb)), 1);
+  p->ws_floats = std::max<size_t>(std::max(net_ws_floats(c, p->actor, mb), net_ws_floats(c, p->critic, mb)), 1);
   dalloc((void**)&p->ws, p->ws_floats * 4);
-  p->nb_cap = (int)cdiv(mb, kThreads);
+  p->nb_cap = (int)std::max<long long>(cdiv(mb, kThreads), kLossMaxBlocks);
   dalloc((void**)&p->gls_part, (size_t)p->nb_cap * p->A * 4);
   dalloc((void**)&p->astat_part, (size_t)p->nb_cap * 2 * 4);
   dalloc((void**)&p->vstat_part, (size_t)p->nb_cap * 4);
@@ -857,7 +859,7 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
            (double)cfg->lr_min, (double)cfg->lr_max, cfg->adaptive_lr, cfg->early_stop,
            cfg->normalize_adv, cfg->clamp_log_std, cfg->shuffle, (void*)p->obs_pad,
            (void*)p->perm);
-  const bool eager = c->timing_kernel >= 0;
+  const bool eager = c->timing_kernel != -1;
   if (!eager && (!p->gexec || p->gkey != key)) {
     if (p->gexec) {
       hipGraphExecDestroy(p->gexec);
@@ -994,8 +996,10 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
   al.clip = cfg->clip;
   al.entropy_coef = cfg->entropy_coef;
   al.scale = scale;
-  if ((s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, al, (unsigned)((kThreads * A + kThreads) * 4))))
-    return s;
+  const LossShape lsh = actor_loss_shape(rows, A);
+  al.rows_per_block = lsh.rows_per_block;
+  al.group = lsh.group;
+  if ((s = launch(c, K_ACTOR_LOSS, (unsigned)lsh.blocks, 1, 1, al))) return s;
   zk::ValueLossArgs vl{};
   vl.v = p->cb.act[Lc];
   vl.ldv = p->cb.ld[Lc];
@@ -1018,19 +1022,19 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
                         p->cb.delta[Lc - 1], p->cb.ld[Lc], nullptr, p->ws, p->ws_floats)))
     return s;
   // Fixed-order sums of the per-block partials.
-  auto reduce = [&](const float* part, int width, float* out) {
+  auto reduce = [&](const float* part, int width, int parts, float* out) {
     zk::SplitReduceArgs r{};
     r.part = part;
     r.out = out;
     r.mn = width;
     r.cols = width;
     r.ldo = width;
-    r.splits = nb;
-    return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(width, kThreads), 1, 1, r);
+    r.splits = parts;
+    return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(cdiv(width, 4), 64), 1, 1, r);
   };
-  if ((s = reduce(p->gls_part, A, p->grads + p->ls_off))) return s;
-  if ((s = reduce(p->astat_part, 2, p->stat_out))) return s;
-  if ((s = reduce(p->vstat_part, 1, p->stat_out + 2))) return s;
+  if ((s = reduce(p->gls_part, A, lsh.blocks, p->grads + p->ls_off))) return s;
+  if ((s = reduce(p->astat_part, 2, lsh.blocks, p->stat_out))) return s;
+  if ((s = reduce(p->vstat_part, 1, nb, p->stat_out + 2))) return s;
   float h[3];
   ZL_HIP(c, hipMemcpyAsync(h, p->stat_out, sizeof(h), hipMemcpyDeviceToHost, c->stream));
   ZL_HIP(c, hipStreamSynchronize(c->stream));

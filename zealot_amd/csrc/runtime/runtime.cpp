@@ -14,16 +14,50 @@
 
 namespace zl {
 
-const char* const kKernelNames[K_COUNT] = {
-    "zk_gemm_ak_bk_64x128", "zk_gemm_ak_bk_128x32", "zk_gemm_ak_bk_256x16",
-    "zk_gemm_ak_bn_64x128", "zk_gemm_am_bn_64x128", "zk_gemm_am_bk_64x128",
-    "zk_splitk_reduce",     "zk_actor_loss",        "zk_value_loss",
-    "zk_sumsq",             "zk_finalize",          "zk_adam",
-    "zk_epoch_begin",       "zk_kl",                "zk_epoch_end",
-    "zk_gae",               "zk_adv_norm",          "zk_elu_backward",
-    "zk_row_sum",           "zk_copy_rows",         "zk_sample",
+const char* const kFixedNames[K_GEMM_BASE] = {
+    "zk_splitk_reduce", "zk_actor_loss",  "zk_value_loss", "zk_sumsq",       "zk_finalize",
+    "zk_adam",          "zk_epoch_begin", "zk_kl",         "zk_epoch_end",   "zk_gae",
+    "zk_adv_norm",      "zk_elu_backward", "zk_row_sum",   "zk_copy_rows",   "zk_sample",
     "zk_clamp",
 };
+
+// {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads}
+const GemmKernel kGemmTable[] = {
+    {"zk_gemm_ak_bk_64x128x16_w22", true, true, 64, 128, 16, 256},
+    {"zk_gemm_ak_bk_96x128x32_w24", true, true, 96, 128, 32, 512},
+    {"zk_gemm_ak_bk_96x128x16_w24", true, true, 96, 128, 16, 512},
+    {"zk_gemm_ak_bk_96x128x32_w22k2", true, true, 96, 128, 32, 512},
+    {"zk_gemm_ak_bk_128x32x16_w41", true, true, 128, 32, 16, 256},
+    {"zk_gemm_ak_bk_96x32x32_w21", true, true, 96, 32, 32, 128},
+    {"zk_gemm_ak_bk_256x16x16_w41", true, true, 256, 16, 16, 256},
+    {"zk_gemm_ak_bn_64x128x16_w22", true, false, 64, 128, 16, 256},
+    {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512},
+    {"zk_gemm_ak_bn_96x128x16_w24", true, false, 96, 128, 16, 512},
+    {"zk_gemm_ak_bn_96x128x32_w22k2", true, false, 96, 128, 32, 512},
+    {"zk_gemm_am_bn_64x128x16_w22", false, false, 64, 128, 16, 256},
+    {"zk_gemm_am_bn_64x128x16_w24", false, false, 64, 128, 16, 512},
+    {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512},
+    {"zk_gemm_am_bn_64x128x32_w22k2", false, false, 64, 128, 32, 512},
+    {"zk_gemm_am_bn_128x128x16_w24", false, false, 128, 128, 16, 512},
+    {"zk_gemm_am_bn_128x128x32_w22k2", false, false, 128, 128, 32, 512},
+    {"zk_gemm_am_bn_64x64x16_w22", false, false, 64, 64, 16, 256},
+    {"zk_gemm_am_bn_32x128x16_w14", false, false, 32, 128, 16, 256},
+    {"zk_gemm_am_bk_64x128x16_w22", false, true, 64, 128, 16, 256},
+};
+const int kGemmCount = (int)(sizeof(kGemmTable) / sizeof(kGemmTable[0]));
+
+int kernel_count() { return K_GEMM_BASE + kGemmCount; }
+
+const char* kernel_name(int id) {
+  if (id < 0 || id >= kernel_count()) return "?";
+  return id < K_GEMM_BASE ? kFixedNames[id] : kGemmTable[id - K_GEMM_BASE].name;
+}
+
+static int gemm_id(const char* name) {
+  for (int i = 0; i < kGemmCount; ++i)
+    if (strcmp(kGemmTable[i].name, name) == 0) return K_GEMM_BASE + i;
+  return -1;
+}
 
 static thread_local std::string g_init_error;
 
@@ -40,7 +74,7 @@ zl_status fail(zl_ctx* c, zl_status s, const char* fmt, ...) {
   return s;
 }
 
-zl_status timing_mark(zl_ctx* c, bool stop) {
+zl_status timing_mark(zl_ctx* c, bool stop, int kernel, double flops) {
   // A start mark takes a fresh pair from the pool; a stop mark closes it.
   if (!stop) {
     if (c->ev_used * 2 + 2 > c->ev_pool.size()) {
@@ -50,6 +84,12 @@ zl_status timing_mark(zl_ctx* c, bool stop) {
         c->ev_pool.push_back(e);
       }
     }
+    if (c->ev_kernel.size() <= c->ev_used) {
+      c->ev_kernel.resize(c->ev_used + 1);
+      c->ev_flops.resize(c->ev_used + 1);
+    }
+    c->ev_kernel[c->ev_used] = kernel;
+    c->ev_flops[c->ev_used] = flops;
     ZL_HIP(c, hipEventRecord(c->ev_pool[c->ev_used * 2], c->stream));
   } else {
     ZL_HIP(c, hipEventRecord(c->ev_pool[c->ev_used * 2 + 1], c->stream));
@@ -72,50 +112,81 @@ zl_status ensure_ws(zl_ctx* c, size_t floats) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-struct TileCfg {
-  KernelId k;
-  int bm, bn;
-};
-
-static TileCfg pick_tile(bool a_kc, bool b_kc, int N) {
-  if (a_kc && b_kc) {
-    if (N <= 16) return {K_GEMM_AK_BK_256x16, 256, 16};
-    if (N <= 32) return {K_GEMM_AK_BK_128x32, 128, 32};
-    return {K_GEMM_AK_BK_64x128, 64, 128};
+// Variant choice. M = 24,576 rows (and every multiple of 96) tiles into an
+// exact multiple of the 256 CUs with 96-row tiles, so the row-major layer
+// GEMMs use them; the narrow output layers use narrow-N tiles. The weight
+// gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
+// 512- and 256-wide layers, 64 x 128 below that (measured on gfx950 at
+// 24,576 rows: 128x128 saves 10-30% on those layers, 64x128 wins for M <= 128).
+int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc) {
+  const int lay = layout_of(a_kc, b_kc);
+  if (c && c->force_gemm[lay] >= 0) return c->force_gemm[lay];
+  const char* name = nullptr;
+  switch (lay) {
+    case L_AK_BK:
+      if (N <= 16)
+        name = "zk_gemm_ak_bk_256x16x16_w41";
+      else if (N <= 32)
+        name = "zk_gemm_ak_bk_128x32x16_w41";
+      else
+        name = M >= 4096 ? "zk_gemm_ak_bk_96x128x32_w24" : "zk_gemm_ak_bk_64x128x16_w22";
+      break;
+    case L_AK_BN:
+      name = M >= 4096 ? "zk_gemm_ak_bn_96x128x32_w24" : "zk_gemm_ak_bn_64x128x16_w22";
+      break;
+    case L_AM_BN:
+      if (M >= 256)
+        name = "zk_gemm_am_bn_128x128x16_w24";
+      else if (M >= 96)
+        name = "zk_gemm_am_bn_64x128x16_w24";
+      else
+        name = "zk_gemm_am_bn_64x128x32_w24";
+      break;
+    default:
+      name = "zk_gemm_am_bk_64x128x16_w22";
+      break;
   }
-  if (a_kc) return {K_GEMM_AK_BN_64x128, 64, 128};
-  if (b_kc) return {K_GEMM_AM_BK_64x128, 64, 128};
-  return {K_GEMM_AM_BN_64x128, 64, 128};
+  (void)K;
+  return gemm_id(name);
 }
 
-int gemm_splits(int M, int N, int K, bool a_kc, bool b_kc, int epi) {
+int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi) {
   if (epi != zk::kEpiStore) return 1;
-  TileCfg t = pick_tile(a_kc, b_kc, N);
-  long long tiles = cdiv(M, t.bm) * cdiv(N, t.bn);
-  long long kt = cdiv(K, 16);
-  // Deep-K, few-tile shapes (the weight gradients, K = batch rows) would
-  // leave most of the 256 CUs idle: slice K so the grid has ~2 waves of
-  // workgroups, keeping at least 8 k-tiles (128 rows) per slice.
-  if (K < 256 || tiles >= 512) return 1;
-  long long s = cdiv(512, tiles);
-  s = std::min<long long>(s, std::max<long long>(1, kt / 8));
-  if (s <= 1) return 1;
-  long long per = cdiv(kt, s);
+  const GemmKernel& g = kGemmTable[pick_gemm(c, M, N, K, a_kc, b_kc) - K_GEMM_BASE];
+  const long long tiles = cdiv(M, g.bm) * cdiv(N, g.bn);
+  const long long kt = cdiv(K, g.bk);
+  long long s;
+  if (c && c->force_splits > 0) {
+    s = c->force_splits;
+  } else {
+    // Deep-K, few-tile shapes (the weight gradients, K = batch rows) would
+    // leave most CUs idle: slice K so the grid reaches the split-K target
+    // (512 = two workgroups per CU), keeping at least 8 k-tiles per slice.
+    const int target = c ? c->splitk_target : 512;
+    if (tiles >= target || kt < 16) return 1;
+    s = std::min<long long>(cdiv(target, tiles), std::max<long long>(1, kt / 8));
+  }
+  s = std::max<long long>(1, std::min(s, kt));
+  const long long per = cdiv(kt, s);
   return (int)cdiv(kt, per);
 }
 
-size_t gemm_ws_floats(int M, int N, int K, bool a_kc, bool b_kc, int epi) {
-  int s = gemm_splits(M, N, K, a_kc, b_kc, epi);
+size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi) {
+  int s = gemm_splits(c, M, N, K, a_kc, b_kc, epi);
   if (s <= 1) return 0;
   return (size_t)s * M * N + (size_t)s * M;
 }
 
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   if (d.M <= 0 || d.N <= 0) return ZL_OK;
-  TileCfg t = pick_tile(d.a_kc, d.b_kc, d.N);
-  int splits = d.splits > 0 ? d.splits : gemm_splits(d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi);
+  const int kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc);
+  if (kid < 0) return fail(c, ZL_ERR_INVALID, "no GEMM variant for this layout");
+  const GemmKernel& g = kGemmTable[kid - K_GEMM_BASE];
+  if (g.a_kc != d.a_kc || g.b_kc != d.b_kc)
+    return fail(c, ZL_ERR_INVALID, "GEMM variant %s does not match the operand layout", g.name);
+  int splits = d.splits > 0 ? d.splits : gemm_splits(c, d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi);
   if (d.epi != zk::kEpiStore) splits = 1;
-  const long long kt = cdiv(std::max(d.K, 0), 16);
+  const long long kt = cdiv(std::max(d.K, 0), g.bk);
   int per = (int)std::max<long long>(1, cdiv(kt, splits));
   splits = (int)std::max<long long>(1, cdiv(kt, per));
 
@@ -142,13 +213,15 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   a.vecA = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4);
   a.vecB = aligned16(d.B) && d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
 
-  const unsigned gx = (unsigned)cdiv(d.M, t.bm), gy = (unsigned)cdiv(d.N, t.bn);
+  const unsigned gx = (unsigned)cdiv(d.M, g.bm), gy = (unsigned)cdiv(d.N, g.bn);
+  const double flops = 2.0 * d.M * d.N * (double)d.K;
   if (splits == 1) {
     a.C = d.C;
     a.ldc = d.ldc;
     a.split_stride = 0;
     a.rowsumA = d.rowsum_out;
-    return launch(c, t.k, gx, gy, 1, a);
+    c->pending_flops = flops;
+    return launch(c, kid, gx, gy, 1, a, 0, (unsigned)g.threads);
   }
   const size_t mn = (size_t)d.M * d.N;
   const size_t need = (size_t)splits * mn + (d.rowsum_out ? (size_t)splits * d.M : 0);
@@ -165,7 +238,8 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   a.ldc = d.N;
   a.split_stride = (long long)mn;
   a.rowsumA = d.rowsum_out ? ws + (size_t)splits * mn : nullptr;
-  zl_status s = launch(c, t.k, gx, gy, (unsigned)splits, a);
+  c->pending_flops = flops;
+  zl_status s = launch(c, kid, gx, gy, (unsigned)splits, a, 0, (unsigned)g.threads);
   if (s) return s;
   zk::SplitReduceArgs r{};
   r.part = ws;
@@ -178,7 +252,8 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   r.ldo = d.ldc;
   r.rows = d.rowsum_out ? d.M : 0;
   r.splits = splits;
-  return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv((long long)mn + r.rows, kThreads), 1, 1, r);
+  const long long nqb = cdiv(cdiv((long long)mn, 4), 64);
+  return launch(c, K_SPLITK_REDUCE, (unsigned)(nqb + cdiv(r.rows, kThreads)), 1, 1, r);
 }
 
 static std::string code_object_path() {
@@ -382,16 +457,33 @@ zl_status zl_init(int device, zl_ctx** out) {
     delete c;
     return ZL_ERR_CODE_OBJECT;
   }
-  for (int k = 0; k < K_COUNT; ++k) {
-    e = hipModuleGetFunction(&c->fn[k], c->module, kKernelNames[k]);
+  c->fn.assign(kernel_count(), nullptr);
+  for (int k = 0; k < kernel_count(); ++k) {
+    e = hipModuleGetFunction(&c->fn[k], c->module, kernel_name(k));
     if (e != hipSuccess) {
-      fail(nullptr, ZL_ERR_CODE_OBJECT, "kernel %s not in %s: %s", kKernelNames[k], path.c_str(),
+      fail(nullptr, ZL_ERR_CODE_OBJECT, "kernel %s not in %s: %s", kernel_name(k), path.c_str(),
            hipGetErrorString(e));
       hipModuleUnload(c->module);
       delete c;
       return ZL_ERR_CODE_OBJECT;
     }
   }
+  // Tuning overrides (see zl_ctx).
+  const char* lay_env[4] = {"ZL_GEMM_AKBK", "ZL_GEMM_AKBN", "ZL_GEMM_AMBN", "ZL_GEMM_AMBK"};
+  for (int l = 0; l < 4; ++l) {
+    const char* v = getenv(lay_env[l]);
+    if (!v || !*v) continue;
+    const int id = gemm_id(v);
+    if (id < 0 || layout_of(kGemmTable[id - K_GEMM_BASE].a_kc, kGemmTable[id - K_GEMM_BASE].b_kc) != l) {
+      fail(nullptr, ZL_ERR_INVALID, "%s=%s is not a GEMM variant of that layout", lay_env[l], v);
+      hipModuleUnload(c->module);
+      delete c;
+      return ZL_ERR_INVALID;
+    }
+    c->force_gemm[l] = id;
+  }
+  if (const char* v = getenv("ZL_SPLITK")) c->force_splits = std::max(0, atoi(v));
+  if (const char* v = getenv("ZL_SPLITK_TARGET")) c->splitk_target = std::max(1, atoi(v));
   // Default-priority stream (no priority variants are used anywhere).
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -415,30 +507,56 @@ zl_status zl_init(int device, zl_ctx** out) {
 
 zl_status zl_timing_begin(zl_ctx* c, const char* kernel_name) {
   if (!c || !kernel_name) return ZL_ERR_INVALID;
-  for (int k = 0; k < K_COUNT; ++k) {
-    if (strcmp(kernel_name, kKernelNames[k]) == 0) {
-      ZL_HIP(c, hipStreamSynchronize(c->stream));
-      c->timing_kernel = k;
-      c->ev_used = 0;
-      return ZL_OK;
-    }
+  int id = -1;
+  if (strcmp(kernel_name, "*") == 0) {
+    id = kTimeAll;
+  } else {
+    for (int k = 0; k < kernel_count(); ++k)
+      if (strcmp(kernel_name, zl::kernel_name(k)) == 0) id = k;
   }
-  return fail(c, ZL_ERR_INVALID, "zl_timing_begin: unknown kernel %s", kernel_name);
+  if (id == -1) return fail(c, ZL_ERR_INVALID, "zl_timing_begin: unknown kernel %s", kernel_name);
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  c->timing_kernel = id;
+  c->ev_used = 0;
+  return ZL_OK;
 }
 
-zl_status zl_timing_end(zl_ctx* c, double* total_ms, long long* launches) {
+zl_status zl_timing_end(zl_ctx* c, double* total_ms, long long* launches, double* flops) {
   if (!c) return ZL_ERR_INVALID;
   ZL_HIP(c, hipStreamSynchronize(c->stream));
-  double tot = 0.0;
+  const int nk = kernel_count();
+  c->rep_ms.assign(nk, 0.0);
+  c->rep_flops.assign(nk, 0.0);
+  c->rep_launches.assign(nk, 0);
+  double tot = 0.0, fl = 0.0;
   for (size_t i = 0; i < c->ev_used; ++i) {
     float ms = 0.f;
     ZL_HIP(c, hipEventElapsedTime(&ms, c->ev_pool[2 * i], c->ev_pool[2 * i + 1]));
     tot += ms;
+    fl += c->ev_flops[i];
+    const int k = c->ev_kernel[i];
+    c->rep_ms[k] += ms;
+    c->rep_flops[k] += c->ev_flops[i];
+    c->rep_launches[k] += 1;
   }
   if (total_ms) *total_ms = tot;
   if (launches) *launches = (long long)c->ev_used;
+  if (flops) *flops = fl;
   c->timing_kernel = -1;
   c->ev_used = 0;
+  return ZL_OK;
+}
+
+int zl_kernel_count(void) { return kernel_count(); }
+
+zl_status zl_timing_kernel(const zl_ctx* c, int id, const char** name, double* total_ms,
+                           long long* launches, double* flops) {
+  if (!c || id < 0 || id >= kernel_count()) return ZL_ERR_INVALID;
+  if (name) *name = zl::kernel_name(id);
+  const bool have = (size_t)id < c->rep_ms.size();
+  if (total_ms) *total_ms = have ? c->rep_ms[id] : 0.0;
+  if (launches) *launches = have ? c->rep_launches[id] : 0;
+  if (flops) *flops = have ? c->rep_flops[id] : 0.0;
   return ZL_OK;
 }
 
@@ -582,7 +700,7 @@ static zl_status reduce_partials(zl_ctx* c, const float* part, int blocks, int w
   r.cols = width;
   r.ldo = width;
   r.splits = blocks;
-  return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(width, kThreads), 1, 1, r);
+  return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(cdiv(width, 4), 64), 1, 1, r);
 }
 
 zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const float* action,
@@ -595,7 +713,8 @@ zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const flo
       rows < 0 || A < 1 || A > 48 || ld_mean < A || ld_action < A || ld_d_mean < A ||
       (mean_old && ld_mean_old < A))
     return fail(c, ZL_ERR_INVALID, "zl_ppo_actor_grad: bad argument (rows=%d A=%d)", rows, A);
-  const int nb = (int)cdiv(rows, kThreads);
+  const LossShape sh = actor_loss_shape(rows, A);
+  const int nb = sh.blocks;
   const size_t need = (size_t)nb * A + (size_t)nb * 2;
   zl_status s = ensure_ws(c, need);
   if (s) return s;
@@ -619,8 +738,10 @@ zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const flo
   a.clip = clip;
   a.entropy_coef = entropy_coef;
   a.scale = scale;
+  a.rows_per_block = sh.rows_per_block;
+  a.group = sh.group;
   if (nb == 0) return ZL_OK;
-  s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, a, (unsigned)((kThreads * A + kThreads) * 4));
+  s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, a);
   if (s) return s;
   s = reduce_partials(c, a.gls_part, nb, A, d_log_std);
   if (s) return s;
