@@ -283,24 +283,30 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
 }
 
 // out[(i / cols) * ldo + i % cols] = sum_z part[z*mn + i], rowout likewise.
-// Each block covers 64 float4 output quads with 4 split groups per quad
-// (group g sums slices g, g+4, ...); the groups are then added 0+1+2+3.
-// The order is fixed, so the result is deterministic. Blocks past the matrix
-// part reduce the row sums (one thread per row, splits in order).
+// A block is 256 / lanes elements (float4 quads of the matrix, or single
+// row sums) x `lanes` split lanes: lane l adds slices l, l+lanes, ... in
+// order (independent loads, so many are in flight per thread), then the
+// lanes are combined by a fixed tree in LDS. The order is fixed, so the
+// result is deterministic. Blocks past the matrix part reduce the row sums.
 __device__ __forceinline__ void splitk_reduce_body(const SplitReduceArgs& p) {
-  __shared__ float4 red[4][64];
+  __shared__ float4 red[256];
   if (p.guard && *p.guard == 0) return;
+  const int SL = p.lanes;
+  const int QB = 256 / SL;
+  const int t = threadIdx.x;
+  const int e = t % QB, l = t / QB;
   const long long nq = (p.mn + 3) / 4;
-  const long long nqb = (nq + 63) / 64;  // blocks of the matrix part
-  if ((long long)blockIdx.x < nqb) {
-    const int q_local = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const long long q = (long long)blockIdx.x * 64 + q_local;
-    const bool vec = (p.mn & 3) == 0;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (q < nq) {
-      const long long i0 = 4 * q;
-      if (vec) {
-        for (int z = g; z < p.splits; z += 4) {
+  const long long nqb = (nq + QB - 1) / QB;  // blocks of the matrix part
+  const bool matrix = (long long)blockIdx.x < nqb;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  long long idx;
+  if (matrix) {
+    idx = (long long)blockIdx.x * QB + e;  // quad index
+    if (idx < nq) {
+      const long long i0 = 4 * idx;
+      if ((p.mn & 3) == 0) {
+#pragma unroll 4
+        for (int z = l; z < p.splits; z += SL) {
           const float4 v = *reinterpret_cast<const float4*>(p.part + (long long)z * p.mn + i0);
           acc.x += v.x;
           acc.y += v.y;
@@ -308,7 +314,7 @@ __device__ __forceinline__ void splitk_reduce_body(const SplitReduceArgs& p) {
           acc.w += v.w;
         }
       } else {
-        for (int z = g; z < p.splits; z += 4) {
+        for (int z = l; z < p.splits; z += SL) {
           const float* b = p.part + (long long)z * p.mn + i0;
           acc.x += b[0];
           if (i0 + 1 < p.mn) acc.y += b[1];
@@ -317,31 +323,39 @@ __device__ __forceinline__ void splitk_reduce_body(const SplitReduceArgs& p) {
         }
       }
     }
-    red[g][q_local] = acc;
+  } else {
+    if (!p.rowpart) return;  // uniform over the block
+    idx = ((long long)blockIdx.x - nqb) * QB + e;  // row index
+    if (idx < p.rows) {
+#pragma unroll 4
+      for (int z = l; z < p.splits; z += SL) acc.x += p.rowpart[(long long)z * p.rows + idx];
+    }
+  }
+  red[t] = acc;
+  __syncthreads();
+  for (int st = SL >> 1; st > 0; st >>= 1) {
+    if (l < st) {
+      const float4 v = red[t + st * QB];
+      float4 a = red[t];
+      a.x += v.x;
+      a.y += v.y;
+      a.z += v.z;
+      a.w += v.w;
+      red[t] = a;
+    }
     __syncthreads();
-    if (g == 0 && q < nq) {
-      float4 s = red[0][q_local];
-#pragma unroll
-      for (int h = 1; h < 4; ++h) {
-        const float4 v = red[h][q_local];
-        s.x += v.x;
-        s.y += v.y;
-        s.z += v.z;
-        s.w += v.w;
-      }
-      const float o[4] = {s.x, s.y, s.z, s.w};
-      for (int c = 0; c < 4; ++c) {
-        const long long i = 4 * q + c;
-        if (i < p.mn) p.out[(i / p.cols) * p.ldo + i % p.cols] = o[c];
-      }
+  }
+  if (l != 0) return;
+  const float4 s = red[e];
+  if (matrix) {
+    if (idx >= nq) return;
+    const float o[4] = {s.x, s.y, s.z, s.w};
+    for (int c = 0; c < 4; ++c) {
+      const long long i = 4 * idx + c;
+      if (i < p.mn) p.out[(i / p.cols) * p.ldo + i % p.cols] = o[c];
     }
-  } else if (p.rowpart) {
-    const long long r = ((long long)blockIdx.x - nqb) * 256 + threadIdx.x;
-    if (r < p.rows) {
-      float s = 0.f;
-      for (int z = 0; z < p.splits; ++z) s += p.rowpart[(long long)z * p.rows + r];
-      p.rowout[r] = s;
-    }
+  } else if (idx < p.rows) {
+    p.rowout[idx] = s.x;
   }
 }
 

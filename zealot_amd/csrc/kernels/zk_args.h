@@ -44,6 +44,7 @@ struct SplitReduceArgs {
   int cols, ldo;
   int rows;
   int splits;
+  int lanes;  // split lanes per output element: a power of two in [1, 256]
 };
 
 // Scalars that live on the device for a whole update so that no kernel needs

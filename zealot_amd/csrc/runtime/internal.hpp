@@ -174,6 +174,9 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc);
 int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);
 size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d);
+// Fixed-order sum over the split slices (zk_splitk_reduce); picks the split
+// lanes and grid from the shape. `r.lanes` is set here.
+zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r);
 zl_status ensure_ws(zl_ctx* c, size_t floats);
 
 }  // namespace zl

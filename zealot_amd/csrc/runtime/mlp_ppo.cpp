@@ -1030,7 +1030,7 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
     r.cols = width;
     r.ldo = width;
     r.splits = parts;
-    return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(cdiv(width, 4), 64), 1, 1, r);
+    return launch_splitk_reduce(c, r);
   };
   if ((s = reduce(p->gls_part, A, lsh.blocks, p->grads + p->ls_off))) return s;
   if ((s = reduce(p->astat_part, 2, lsh.blocks, p->stat_out))) return s;

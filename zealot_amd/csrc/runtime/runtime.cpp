@@ -116,8 +116,8 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // exact multiple of the 256 CUs with 96-row tiles, so the row-major layer
 // GEMMs use them; the narrow output layers use narrow-N tiles. The weight
 // gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
-// 512- and 256-wide layers, 64 x 128 below that (measured on gfx950 at
-// 24,576 rows: 128x128 saves 10-30% on those layers, 64x128 wins for M <= 128).
+// 512- and 256-wide layers, 64 x 128 for the 128-wide one and 32 x 128 for
+// the narrow heads (measured on gfx950 at 24,576 rows).
 int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc) {
   const int lay = layout_of(a_kc, b_kc);
   if (c && c->force_gemm[lay] >= 0) return c->force_gemm[lay];
@@ -140,7 +140,7 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc) {
       else if (M >= 96)
         name = "zk_gemm_am_bn_64x128x16_w24";
       else
-        name = "zk_gemm_am_bn_64x128x32_w24";
+        name = "zk_gemm_am_bn_32x128x16_w14";
       break;
     default:
       name = "zk_gemm_am_bk_64x128x16_w22";
@@ -175,6 +175,17 @@ size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc
   int s = gemm_splits(c, M, N, K, a_kc, b_kc, epi);
   if (s <= 1) return 0;
   return (size_t)s * M * N + (size_t)s * M;
+}
+
+zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r) {
+  // Enough split lanes that each thread adds at most ~8 slices.
+  int sl = 1;
+  while (sl < 64 && sl * 8 < r.splits) sl <<= 1;
+  r.lanes = sl;
+  const int per_block = kThreads / sl;
+  const long long nqb = cdiv(cdiv(r.mn, 4), per_block);
+  const long long nrb = r.rowpart ? cdiv(r.rows, per_block) : 0;
+  return launch(c, K_SPLITK_REDUCE, (unsigned)(nqb + nrb), 1, 1, r);
 }
 
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
@@ -252,8 +263,7 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   r.ldo = d.ldc;
   r.rows = d.rowsum_out ? d.M : 0;
   r.splits = splits;
-  const long long nqb = cdiv(cdiv((long long)mn, 4), 64);
-  return launch(c, K_SPLITK_REDUCE, (unsigned)(nqb + cdiv(r.rows, kThreads)), 1, 1, r);
+  return launch_splitk_reduce(c, r);
 }
 
 static std::string code_object_path() {
@@ -700,7 +710,7 @@ static zl_status reduce_partials(zl_ctx* c, const float* part, int blocks, int w
   r.cols = width;
   r.ldo = width;
   r.splits = blocks;
-  return launch(c, K_SPLITK_REDUCE, (unsigned)cdiv(cdiv(width, 4), 64), 1, 1, r);
+  return launch_splitk_reduce(c, r);
 }
 
 zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const float* action,
