@@ -17,6 +17,13 @@
 // place it is not (rayon fold/reduce grouping, ppo.rs:406-462) is restated as
 // contiguous per-thread chunks reduced left to right; with one thread this is
 // the sequential fold.
+//
+// Pinning: every function used by the tests is checked against the
+// reference's own known-answer tests, closed forms or float64 finite
+// differences (tests/test_oracle.py). PendingNorm::push / norm_commit
+// (ppo.rs:126-137,179-195) are restated but not reachable from the C API and
+// have no check: parity unpinned (they belong to the on-device observation
+// normaliser, which the HIP path does not implement yet).
 #pragma once
 #include <cmath>
 #include <cstddef>

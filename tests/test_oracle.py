@@ -435,3 +435,63 @@ def test_trainer_early_stop_and_clamp():
     assert int(st[5]) == 1 and gstep == 2
     assert np.all(ls <= 0.0) and np.all(ls >= -1.6)
     assert lr == pytest.approx(max(1e-2 / 1.5, 1e-5), rel=1e-6)
+
+
+def test_trainer_full_gaussian_kl_closed_form():
+    """The trainer's per-epoch KL (src/bin/biped_train_gpu.rs:1469-1492) is the
+    analytic KL(old || new) of diagonal Gaussians, averaged over the rows of the
+    last minibatch: sum_k log(s_new/s_old) + (s_old^2 + dmu^2) / (2 s_new^2) - 1/2,
+    with the means of that minibatch's forward pass (taken before its Adam step)
+    and the log_std after it. One epoch of one minibatch makes both sides
+    independent of the summation order of the update; the float64 side shares
+    no code with the oracle."""
+    ad, cd, actor, critic, log_std, batch = _ppo_tiny(13, v_shift=0.05)
+    batch["adv"] = zo.adv_normalize(batch["adv"])
+    tr = zo.Trainer(ad, cd, actor, critic, log_std, 5e-2)
+    so = tr.update(batch, zo.TrainerCfg(0.2, 0.01, 1.0, 1, 1, 0.0, 0.01, 1e-5, 1e-1, 0, 0, 0))
+    _, _, ls_new, _, _ = tr.get()
+    assert np.max(np.abs(ls_new - log_std)) > 1e-2  # log_std moved: the sigma terms matter
+    mu = np_ref.forward(ad, actor, batch["obs"])[-1]  # pre-step means, float64
+    ls_o, ls_n = log_std.astype(np.float64), ls_new.astype(np.float64)
+    dmu = mu - batch["mean_old"].astype(np.float64)
+    kl = np.sum((ls_n - ls_o) + (np.exp(2 * ls_o) + dmu ** 2) / (2 * np.exp(2 * ls_n)) - 0.5, axis=1)
+    assert so[6] == pytest.approx(kl.mean(), rel=1e-4, abs=1e-6)
+    # A mean-only KL (the ActorCritic form) or post-step sigmas in the old slot
+    # would not pass: they differ from the closed form by far more than 1e-4.
+    kl_mean_only = np.sum(0.5 * (dmu * np.exp(-ls_n)) ** 2, axis=1).mean()
+    assert abs(kl_mean_only - kl.mean()) > 1e-3 * abs(kl.mean())
+
+
+def test_normalizer_welford_with_unit_prior():
+    """Normalizer::update / normalize (zealot-rl/src/ppo.rs:142-205), observed
+    through ActorCritic::mean / value (:282-294): the unit-variance prior is
+    one pseudo-observation at 0 with m2 = 1, so after x_1..x_n the state is
+    count = n + 1, mean = sum(x) / (n + 1), m2 = 1 + sum((x - mean)^2) - mean^2
+    (Chan merge of the prior with the data), and normalize(x) =
+    clamp((x - mean) / sqrt(max(m2 / count, 1e-8)), -5, 5). The float64 side
+    is written from that closed form, not from the streaming recurrence."""
+    g = np.random.default_rng(21)
+    ad, cd = [3, 4, 2], [3, 4, 1]
+    ac = zo.ActorCritic(ad, cd, 1.0, 1e-3, 1)
+    actor = (g.standard_normal(zo.packed_count(ad)) * 0.5).astype(np.float32)
+    critic = (g.standard_normal(zo.packed_count(cd)) * 0.5).astype(np.float32)
+    ac.set(actor, critic, np.zeros(2, np.float32), 1e-3)
+    xs = (g.standard_normal((200, 3)) * np.array([0.5, 2.0, 3.0]) + np.array([1.0, -2.0, 0.0])).astype(np.float32)
+    cs = (g.standard_normal((200, 3)) * 0.1).astype(np.float32)
+    for x, c in zip(xs, cs):
+        ac.record_obs(x, c)
+
+    def closed(data, probe):
+        d = data.astype(np.float64)
+        n = d.shape[0]
+        mean = d.sum(0) / (n + 1)
+        m2 = 1.0 + ((d - mean) ** 2).sum(0) + (0.0 - mean) ** 2
+        var = np.maximum(m2 / (n + 1), 1e-8)
+        return np.clip((probe - mean) / np.sqrt(var), -5, 5)
+
+    probe = np.array([0.3, -1.0, 20.0], np.float32)  # third component hits the +5 clamp
+    z = closed(xs, probe)
+    assert z[2] == 5.0
+    assert np.allclose(ac.mean(probe), np_ref.forward(ad, actor, z[None])[-1][0], rtol=1e-5, atol=1e-6)
+    zc = closed(cs, probe)
+    assert np.allclose(ac.value(probe), np_ref.forward(cd, critic, zc[None])[-1][0, 0], rtol=1e-5, atol=1e-6)
