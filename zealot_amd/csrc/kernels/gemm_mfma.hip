@@ -25,7 +25,15 @@
 namespace zk {
 
 // One operand tile of NT threads: EXT rows/cols along M (or N) by BK along K.
-template <int EXT, bool KC, int BK, int NT>
+//
+// Global loads are issued unconditionally from clamped, always-valid
+// addresses and every bounds / padding mask is applied when the registers are
+// written to LDS, after the MFMAs of the current k-tile: nothing between the
+// load and the store needs the loaded values, so the loads of k-tile t+1 stay
+// in flight during the MFMAs of k-tile t. Storage rows gathered through
+// `perm` are resolved once per block for a K-contiguous operand (its rows do
+// not change along K) and one k-tile ahead for the other orientation.
+template <int EXT, bool KC, int BK, int NT, bool VEC>
 struct Tile {
   // Row length in LDS. K-contiguous rows get +4 floats so 16 rows read at one
   // k hit distinct banks; the other orientation needs LD = 16 or 48 (mod 64)
@@ -34,100 +42,152 @@ struct Tile {
       KC ? (BK + 4) : ((EXT % 64 == 16 || EXT % 64 == 48) ? EXT : EXT + 16);
   static constexpr int SIZE = KC ? EXT * LD : BK * LD;
   static constexpr int ELEMS = EXT * BK;
-  static constexpr int NV = (ELEMS / 4 + NT - 1) / NT;
-  static constexpr int NS = (ELEMS + NT - 1) / NT;
-  static constexpr int NR = (4 * NV > NS) ? 4 * NV : NS;
-  float r[NR];
+  static constexpr int NQ = ELEMS / 4;            // float4 quads per tile
+  static constexpr int NV = (NQ + NT - 1) / NT;   // quads per thread
+  static constexpr int NS = (ELEMS + NT - 1) / NT;  // scalars per thread
+  static constexpr int QR = KC ? BK / 4 : EXT / 4;  // quads per stored row
+  float4 v[VEC ? NV : 1];
+  float s[VEC ? 1 : NS];
+  // Vector path, per quad: KC -> storage row pointer (perm resolved, row
+  // clamped); other orientation -> column offset and the perm'd storage row
+  // of the k-tile to load next.
+  const float* rp[NV];
+  int col[NV];
+  int pk[NV];
+  bool ok[NV];  // quad inside the tile's EXT range (and i < NQ)
 
-  // Global -> registers. `perm` remaps the storage row (the EXT index when
-  // K-contiguous, the k index otherwise). Out-of-range elements load as 0.
-  __device__ __forceinline__ void load(const float* __restrict__ base, int ld, int e0, int etot,
-                                       int k0, int K, const int* __restrict__ perm, bool vec) {
+  const float* base;
+  const int* perm;
+  int ld, e0, etot, K;
+
+  __device__ __forceinline__ void init(const float* __restrict__ b, int ld_, int e0_, int etot_,
+                                       int K_, const int* __restrict__ perm_) {
+    base = b;
+    ld = ld_;
+    e0 = e0_;
+    etot = etot_;
+    K = K_;
+    perm = perm_;
+    if (!VEC) return;
     const int t = threadIdx.x;
-    if (vec) {
 #pragma unroll
-      for (int j = 0; j < NV; ++j) {
-        const int i = t + j * NT;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (i < ELEMS / 4) {
-          if (KC) {
-            const int row = i / (BK / 4), kq = (i % (BK / 4)) * 4;
-            const int e = e0 + row, k = k0 + kq;
-            if (e < etot && k < K) {
-              const int sr = perm ? perm[e] : e;
-              v = *reinterpret_cast<const float4*>(base + (long long)sr * ld + k);
-              if (k + 1 >= K) v.y = 0.f;
-              if (k + 2 >= K) v.z = 0.f;
-              if (k + 3 >= K) v.w = 0.f;
-            }
-          } else {
-            const int kk = i / (EXT / 4), c4 = (i % (EXT / 4)) * 4;
-            const int k = k0 + kk, e = e0 + c4;
-            if (k < K && e < etot) {
-              const int sr = perm ? perm[k] : k;
-              v = *reinterpret_cast<const float4*>(base + (long long)sr * ld + e);
-              if (e + 1 >= etot) v.y = 0.f;
-              if (e + 2 >= etot) v.z = 0.f;
-              if (e + 3 >= etot) v.w = 0.f;
-            }
-          }
-        }
-        r[4 * j + 0] = v.x;
-        r[4 * j + 1] = v.y;
-        r[4 * j + 2] = v.z;
-        r[4 * j + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        const int i = t + j * NT;
-        float v = 0.f;
-        if (i < ELEMS) {
-          if (KC) {
-            const int e = e0 + i / BK, k = k0 + i % BK;
-            if (e < etot && k < K) v = base[(long long)(perm ? perm[e] : e) * ld + k];
-          } else {
-            const int k = k0 + i / EXT, e = e0 + i % EXT;
-            if (k < K && e < etot) v = base[(long long)(perm ? perm[k] : k) * ld + e];
-          }
-        }
-        r[j] = v;
+    for (int j = 0; j < NV; ++j) {
+      const int i = t + j * NT;
+      const int iq = (NQ % NT == 0 || i < NQ) ? i : 0;
+      if (KC) {
+        const int e = e0 + iq / QR;
+        ok[j] = (NQ % NT == 0 || i < NQ) && e < etot;
+        const int ec = min(e, etot - 1);
+        const int sr = perm ? perm[ec] : ec;
+        rp[j] = base + (long long)sr * ld;
+      } else {
+        const int e = e0 + (iq % QR) * 4;
+        ok[j] = (NQ % NT == 0 || i < NQ) && e < etot;
+        col[j] = min(e, ((etot + 3) & ~3) - 4);
       }
     }
   }
 
-  // Registers -> LDS buffer.
-  __device__ __forceinline__ void store(float* __restrict__ s, bool vec) const {
+  // Other orientation with a gather: storage rows of the k-tile at k0.
+  __device__ __forceinline__ void fetch_rows(int k0) {
+    if (KC || !VEC || !perm) return;
     const int t = threadIdx.x;
-    if (vec) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = t + j * NT;
+      const int iq = (NQ % NT == 0 || i < NQ) ? i : 0;
+      pk[j] = perm[min(k0 + iq / QR, K - 1)];
+    }
+  }
+
+  // Global -> registers for the k-tile at k0 (no masking here).
+  __device__ __forceinline__ void load(int k0) {
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
         const int i = t + j * NT;
-        if (i < ELEMS / 4) {
-          float4 v = make_float4(r[4 * j], r[4 * j + 1], r[4 * j + 2], r[4 * j + 3]);
-          if (KC)
-            *reinterpret_cast<float4*>(s + (i / (BK / 4)) * LD + (i % (BK / 4)) * 4) = v;
-          else
-            *reinterpret_cast<float4*>(s + (i / (EXT / 4)) * LD + (i % (EXT / 4)) * 4) = v;
+        const int iq = (NQ % NT == 0 || i < NQ) ? i : 0;
+        if (KC) {
+          const int k = min(k0 + (iq % QR) * 4, ((K + 3) & ~3) - 4);
+          v[j] = *reinterpret_cast<const float4*>(rp[j] + k);
+        } else {
+          const int kc = min(k0 + iq / QR, K - 1);
+          const int sr = perm ? pk[j] : kc;
+          v[j] = *reinterpret_cast<const float4*>(base + (long long)sr * ld + col[j]);
         }
       }
     } else {
 #pragma unroll
       for (int j = 0; j < NS; ++j) {
         const int i = t + j * NT;
-        if (i < ELEMS) {
-          if (KC)
-            s[(i / BK) * LD + i % BK] = r[j];
-          else
-            s[(i / EXT) * LD + i % EXT] = r[j];
+        const int ic = (ELEMS % NT == 0 || i < ELEMS) ? i : 0;
+        int e, k;
+        if (KC) {
+          e = e0 + ic / BK;
+          k = k0 + ic % BK;
+        } else {
+          k = k0 + ic / EXT;
+          e = e0 + ic % EXT;
         }
+        const int ec = min(e, etot - 1), kc = min(k, K - 1);
+        const long long sr = KC ? (perm ? perm[ec] : ec) : (perm ? perm[kc] : kc);
+        s[j] = base[sr * ld + (KC ? kc : ec)];
+      }
+    }
+  }
+
+  // Registers -> LDS buffer, zeroing everything outside [0, etot) x [0, K).
+  __device__ __forceinline__ void store(float* __restrict__ sm, int k0) const {
+    const int t = threadIdx.x;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int i = t + j * NT;
+        if (NQ % NT != 0 && i >= NQ) continue;
+        float4 x = v[j];
+        if (KC) {
+          const int kq = (i % QR) * 4, k = k0 + kq;
+          const bool good = ok[j] && k < K;
+          x.x = good ? x.x : 0.f;
+          x.y = (good && k + 1 < K) ? x.y : 0.f;
+          x.z = (good && k + 2 < K) ? x.z : 0.f;
+          x.w = (good && k + 3 < K) ? x.w : 0.f;
+          *reinterpret_cast<float4*>(sm + (i / QR) * LD + kq) = x;
+        } else {
+          const int kk = i / QR, c4 = (i % QR) * 4;
+          const int e = e0 + c4;
+          const bool good = ok[j] && k0 + kk < K;
+          x.x = good ? x.x : 0.f;
+          x.y = (good && e + 1 < etot) ? x.y : 0.f;
+          x.z = (good && e + 2 < etot) ? x.z : 0.f;
+          x.w = (good && e + 3 < etot) ? x.w : 0.f;
+          *reinterpret_cast<float4*>(sm + kk * LD + c4) = x;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const int i = t + j * NT;
+        if (ELEMS % NT != 0 && i >= ELEMS) continue;
+        int e, k, off;
+        if (KC) {
+          e = e0 + i / BK;
+          k = k0 + i % BK;
+          off = (i / BK) * LD + i % BK;
+        } else {
+          k = k0 + i / EXT;
+          e = e0 + i % EXT;
+          off = (i / EXT) * LD + i % EXT;
+        }
+        sm[off] = (e < etot && k < K) ? s[j] : 0.f;
       }
     }
   }
 
   // Element (e, k) of a staged tile.
-  __device__ __forceinline__ static float at(const float* s, int e, int k) {
-    return KC ? s[e * LD + k] : s[k * LD + e];
+  __device__ __forceinline__ static float at(const float* sm, int e, int k) {
+    return KC ? sm[e * LD + k] : sm[k * LD + e];
   }
 };
 
@@ -135,7 +195,7 @@ struct Tile {
 // g runs k-steps [g, g+1) * BK/4/KG); the groups' accumulators are added in
 // LDS in group order before the epilogue, so a tile gets KG times the waves
 // without any global split-K partials.
-template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, int KG = 1>
+template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, int KG, bool VEC>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
   constexpr int NT = 64 * WM * WN * KG;
   constexpr int TM = BM / (WM * 16);
@@ -144,8 +204,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
   static_assert(BK % (4 * KG) == 0, "k-steps of 4 per group");
   static_assert(KG == 1 || KG == 2, "one LDS exchange round");
   constexpr int RSG = NT / BM >= 1 ? NT / BM : 1;  // threads per A row in the row sums
-  using TA = Tile<BM, AK, BK, NT>;
-  using TB = Tile<BN, BKC, BK, NT>;
+  using TA = Tile<BM, AK, BK, NT, VEC>;
+  using TB = Tile<BN, BKC, BK, NT, VEC>;
   constexpr int SMEM = 2 * (TA::SIZE + TB::SIZE);
   static_assert(KG == 1 || SMEM >= BM * BN, "LDS holds one group's accumulator tile");
   static_assert(SMEM >= NT, "LDS holds one float per thread for the row sums");
@@ -165,7 +225,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
   const int kt0 = blockIdx.z * p.kt_per_split;
   const int kt1 = min(KT, kt0 + p.kt_per_split);
   const bool rowsum = p.rowsumA != nullptr && blockIdx.y == 0;
-  const bool vA = p.vecA != 0, vB = p.vecB != 0;
 
   floatx4 acc[TM][TN];
 #pragma unroll
@@ -175,15 +234,23 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
 
   TA ta;
   TB tb;
+  ta.init(p.A, p.lda, m0, p.M, p.K, p.permA);
+  tb.init(p.B, p.ldb, n0, p.N, p.K, p.permB);
   float rs = 0.f;
   const int rs_m = tid % BM, rs_g = tid / BM;
   const bool rs_on = rowsum && tid < BM * RSG;
 
   if (kt0 < kt1) {
-    ta.load(p.A, p.lda, m0, p.M, kt0 * BK, p.K, p.permA, vA);
-    tb.load(p.B, p.ldb, n0, p.N, kt0 * BK, p.K, p.permB, vB);
-    ta.store(sA(0), vA);
-    tb.store(sB(0), vB);
+    ta.fetch_rows(kt0 * BK);
+    tb.fetch_rows(kt0 * BK);
+    ta.load(kt0 * BK);
+    tb.load(kt0 * BK);
+    if (kt0 + 1 < kt1) {
+      ta.fetch_rows((kt0 + 1) * BK);
+      tb.fetch_rows((kt0 + 1) * BK);
+    }
+    ta.store(sA(0), kt0 * BK);
+    tb.store(sB(0), kt0 * BK);
   }
   __syncthreads();
 
@@ -191,8 +258,12 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     const int cur = (kt - kt0) & 1;
     const bool more = kt + 1 < kt1;
     if (more) {
-      ta.load(p.A, p.lda, m0, p.M, (kt + 1) * BK, p.K, p.permA, vA);
-      tb.load(p.B, p.ldb, n0, p.N, (kt + 1) * BK, p.K, p.permB, vB);
+      ta.load((kt + 1) * BK);
+      tb.load((kt + 1) * BK);
+      if (kt + 2 < kt1) {
+        ta.fetch_rows((kt + 2) * BK);
+        tb.fetch_rows((kt + 2) * BK);
+      }
     }
     const float* as = sA(cur);
     const float* bs = sB(cur);
@@ -214,8 +285,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
       for (int kk = rs_g; kk < BK; kk += RSG) rs += TA::at(as, rs_m, kk);
     }
     if (more) {
-      ta.store(sA(cur ^ 1), vA);
-      tb.store(sB(cur ^ 1), vB);
+      ta.store(sA(cur ^ 1), (kt + 1) * BK);
+      tb.store(sB(cur ^ 1), (kt + 1) * BK);
     }
     __syncthreads();
   }
@@ -361,33 +432,38 @@ __device__ __forceinline__ void splitk_reduce_body(const SplitReduceArgs& p) {
 
 }  // namespace zk
 
-#define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, KG)                                   \
+#define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, KG, VEC)                              \
   extern "C" __global__ __launch_bounds__(64 * WM * WN * KG) void NAME(zk::GemmArgs p) { \
-    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, KG>(p);                                   \
+    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, KG, VEC>(p);                              \
   }
 
 // Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous,
-// then BMxBNxBK, the wave grid WMxWN and (k2) two k-groups per tile.
-ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22, true, true, 64, 128, 16, 2, 2, 1)
-ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, 1)
-ZK_GEMM(zk_gemm_ak_bk_96x128x16_w24, true, true, 96, 128, 16, 2, 4, 1)
-ZK_GEMM(zk_gemm_ak_bk_96x128x32_w22k2, true, true, 96, 128, 32, 2, 2, 2)
-ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, 1)
-ZK_GEMM(zk_gemm_ak_bk_96x32x32_w21, true, true, 96, 32, 32, 2, 1, 1)
-ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, 1)
-ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, 1)
-ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, 1)
-ZK_GEMM(zk_gemm_ak_bn_96x128x16_w24, true, false, 96, 128, 16, 2, 4, 1)
-ZK_GEMM(zk_gemm_ak_bn_96x128x32_w22k2, true, false, 96, 128, 32, 2, 2, 2)
-ZK_GEMM(zk_gemm_am_bn_64x128x16_w22, false, false, 64, 128, 16, 2, 2, 1)
-ZK_GEMM(zk_gemm_am_bn_64x128x16_w24, false, false, 64, 128, 16, 2, 4, 1)
-ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, 1)
-ZK_GEMM(zk_gemm_am_bn_64x128x32_w22k2, false, false, 64, 128, 32, 2, 2, 2)
-ZK_GEMM(zk_gemm_am_bn_128x128x16_w24, false, false, 128, 128, 16, 2, 4, 1)
-ZK_GEMM(zk_gemm_am_bn_128x128x32_w22k2, false, false, 128, 128, 32, 2, 2, 2)
-ZK_GEMM(zk_gemm_am_bn_64x64x16_w22, false, false, 64, 64, 16, 2, 2, 1)
-ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, 1)
-ZK_GEMM(zk_gemm_am_bk_64x128x16_w22, false, true, 64, 128, 16, 2, 2, 1)
+// then BMxBNxBK, the wave grid WMxWN, (k2) two k-groups per tile and (_s)
+// scalar global loads for operands that are not 16-byte aligned row by row.
+ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22, true, true, 64, 128, 16, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_96x128x16_w24, true, true, 96, 128, 16, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_96x128x32_w22k2, true, true, 96, 128, 32, 2, 2, 2, true)
+ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_96x32x32_w21, true, true, 96, 32, 32, 2, 1, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, 1, true)
+ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bn_96x128x16_w24, true, false, 96, 128, 16, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bn_96x128x32_w22k2, true, false, 96, 128, 32, 2, 2, 2, true)
+ZK_GEMM(zk_gemm_am_bn_64x128x16_w22, false, false, 64, 128, 16, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_am_bn_64x128x16_w24, false, false, 64, 128, 16, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_am_bn_64x128x32_w22k2, false, false, 64, 128, 32, 2, 2, 2, true)
+ZK_GEMM(zk_gemm_am_bn_128x128x16_w24, false, false, 128, 128, 16, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_am_bn_128x128x32_w22k2, false, false, 128, 128, 32, 2, 2, 2, true)
+ZK_GEMM(zk_gemm_am_bn_64x64x16_w22, false, false, 64, 64, 16, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, 1, true)
+ZK_GEMM(zk_gemm_am_bk_64x128x16_w22, false, true, 64, 128, 16, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22_s, true, true, 64, 128, 16, 2, 2, 1, false)
+ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22_s, true, false, 64, 128, 16, 2, 2, 1, false)
+ZK_GEMM(zk_gemm_am_bn_64x128x16_w22_s, false, false, 64, 128, 16, 2, 2, 1, false)
+ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, 1, false)
 
 extern "C" __global__ __launch_bounds__(256) void zk_splitk_reduce(zk::SplitReduceArgs p) {
   zk::splitk_reduce_body(p);

@@ -34,11 +34,13 @@ enum KernelId : int {
   K_GEMM_BASE
 };
 
-// One GEMM variant: operand orientation, tile, k-tile and block size.
+// One GEMM variant: operand orientation, tile, k-tile, block size and
+// whether it loads both operands as float4 rows (vec) or element by element.
 struct GemmKernel {
   const char* name;
   bool a_kc, b_kc;
   int bm, bn, bk, threads;
+  bool vec;
 };
 
 extern const char* const kFixedNames[K_GEMM_BASE];
@@ -170,8 +172,10 @@ struct GemmDesc {
 
 // Variant choice and split-K decision shared by run_gemm and the scratch
 // sizing of composites.
-int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc);
-int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);
+// vec: both operands can be read as aligned float4 rows (see run_gemm).
+int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec = true);
+int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi,
+                bool vec = true);
 size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d);
 // Fixed-order sum over the split slices (zk_splitk_reduce); picks the split

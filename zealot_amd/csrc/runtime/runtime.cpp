@@ -21,28 +21,32 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_clamp",
 };
 
-// {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads}
+// {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads}
 const GemmKernel kGemmTable[] = {
-    {"zk_gemm_ak_bk_64x128x16_w22", true, true, 64, 128, 16, 256},
-    {"zk_gemm_ak_bk_96x128x32_w24", true, true, 96, 128, 32, 512},
-    {"zk_gemm_ak_bk_96x128x16_w24", true, true, 96, 128, 16, 512},
-    {"zk_gemm_ak_bk_96x128x32_w22k2", true, true, 96, 128, 32, 512},
-    {"zk_gemm_ak_bk_128x32x16_w41", true, true, 128, 32, 16, 256},
-    {"zk_gemm_ak_bk_96x32x32_w21", true, true, 96, 32, 32, 128},
-    {"zk_gemm_ak_bk_256x16x16_w41", true, true, 256, 16, 16, 256},
-    {"zk_gemm_ak_bn_64x128x16_w22", true, false, 64, 128, 16, 256},
-    {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512},
-    {"zk_gemm_ak_bn_96x128x16_w24", true, false, 96, 128, 16, 512},
-    {"zk_gemm_ak_bn_96x128x32_w22k2", true, false, 96, 128, 32, 512},
-    {"zk_gemm_am_bn_64x128x16_w22", false, false, 64, 128, 16, 256},
-    {"zk_gemm_am_bn_64x128x16_w24", false, false, 64, 128, 16, 512},
-    {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512},
-    {"zk_gemm_am_bn_64x128x32_w22k2", false, false, 64, 128, 32, 512},
-    {"zk_gemm_am_bn_128x128x16_w24", false, false, 128, 128, 16, 512},
-    {"zk_gemm_am_bn_128x128x32_w22k2", false, false, 128, 128, 32, 512},
-    {"zk_gemm_am_bn_64x64x16_w22", false, false, 64, 64, 16, 256},
-    {"zk_gemm_am_bn_32x128x16_w14", false, false, 32, 128, 16, 256},
-    {"zk_gemm_am_bk_64x128x16_w22", false, true, 64, 128, 16, 256},
+    {"zk_gemm_ak_bk_64x128x16_w22", true, true, 64, 128, 16, 256, true},
+    {"zk_gemm_ak_bk_96x128x32_w24", true, true, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bk_96x128x16_w24", true, true, 96, 128, 16, 512, true},
+    {"zk_gemm_ak_bk_96x128x32_w22k2", true, true, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bk_128x32x16_w41", true, true, 128, 32, 16, 256, true},
+    {"zk_gemm_ak_bk_96x32x32_w21", true, true, 96, 32, 32, 128, true},
+    {"zk_gemm_ak_bk_256x16x16_w41", true, true, 256, 16, 16, 256, true},
+    {"zk_gemm_ak_bn_64x128x16_w22", true, false, 64, 128, 16, 256, true},
+    {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bn_96x128x16_w24", true, false, 96, 128, 16, 512, true},
+    {"zk_gemm_ak_bn_96x128x32_w22k2", true, false, 96, 128, 32, 512, true},
+    {"zk_gemm_am_bn_64x128x16_w22", false, false, 64, 128, 16, 256, true},
+    {"zk_gemm_am_bn_64x128x16_w24", false, false, 64, 128, 16, 512, true},
+    {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512, true},
+    {"zk_gemm_am_bn_64x128x32_w22k2", false, false, 64, 128, 32, 512, true},
+    {"zk_gemm_am_bn_128x128x16_w24", false, false, 128, 128, 16, 512, true},
+    {"zk_gemm_am_bn_128x128x32_w22k2", false, false, 128, 128, 32, 512, true},
+    {"zk_gemm_am_bn_64x64x16_w22", false, false, 64, 64, 16, 256, true},
+    {"zk_gemm_am_bn_32x128x16_w14", false, false, 32, 128, 16, 256, true},
+    {"zk_gemm_am_bk_64x128x16_w22", false, true, 64, 128, 16, 256, true},
+    {"zk_gemm_ak_bk_64x128x16_w22_s", true, true, 64, 128, 16, 256, false},
+    {"zk_gemm_ak_bn_64x128x16_w22_s", true, false, 64, 128, 16, 256, false},
+    {"zk_gemm_am_bn_64x128x16_w22_s", false, false, 64, 128, 16, 256, false},
+    {"zk_gemm_am_bk_64x128x16_w22_s", false, true, 64, 128, 16, 256, false},
 };
 const int kGemmCount = (int)(sizeof(kGemmTable) / sizeof(kGemmTable[0]));
 
@@ -118,8 +122,14 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
 // 512- and 256-wide layers, 64 x 128 for the 128-wide one and 32 x 128 for
 // the narrow heads (measured on gfx950 at 24,576 rows).
-int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc) {
+int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec) {
   const int lay = layout_of(a_kc, b_kc);
+  if (!vec) {
+    static const char* const kScalar[4] = {
+        "zk_gemm_ak_bk_64x128x16_w22_s", "zk_gemm_ak_bn_64x128x16_w22_s",
+        "zk_gemm_am_bn_64x128x16_w22_s", "zk_gemm_am_bk_64x128x16_w22_s"};
+    return gemm_id(kScalar[lay]);
+  }
   if (c && c->force_gemm[lay] >= 0) return c->force_gemm[lay];
   const char* name = nullptr;
   switch (lay) {
@@ -150,9 +160,9 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc) {
   return gemm_id(name);
 }
 
-int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi) {
+int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi, bool vec) {
   if (epi != zk::kEpiStore) return 1;
-  const GemmKernel& g = kGemmTable[pick_gemm(c, M, N, K, a_kc, b_kc) - K_GEMM_BASE];
+  const GemmKernel& g = kGemmTable[pick_gemm(c, M, N, K, a_kc, b_kc, vec) - K_GEMM_BASE];
   const long long tiles = cdiv(M, g.bm) * cdiv(N, g.bn);
   const long long kt = cdiv(K, g.bk);
   long long s;
@@ -172,7 +182,9 @@ int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int 
 }
 
 size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi) {
-  int s = gemm_splits(c, M, N, K, a_kc, b_kc, epi);
+  // Enough for either variant family (operand alignment is known at launch).
+  int s = std::max(gemm_splits(c, M, N, K, a_kc, b_kc, epi, true),
+                   gemm_splits(c, M, N, K, a_kc, b_kc, epi, false));
   if (s <= 1) return 0;
   return (size_t)s * M * N + (size_t)s * M;
 }
@@ -190,12 +202,17 @@ zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r) {
 
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   if (d.M <= 0 || d.N <= 0) return ZL_OK;
-  const int kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc);
+  // float4 row loads need 16-byte aligned rows that cover the padded extent.
+  const int a_ext = d.a_kc ? d.K : d.M;
+  const int b_ext = d.b_kc ? d.K : d.N;
+  const bool vec = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4) &&
+                   aligned16(d.B) && d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
+  const int kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc, vec);
   if (kid < 0) return fail(c, ZL_ERR_INVALID, "no GEMM variant for this layout");
   const GemmKernel& g = kGemmTable[kid - K_GEMM_BASE];
-  if (g.a_kc != d.a_kc || g.b_kc != d.b_kc)
+  if (g.a_kc != d.a_kc || g.b_kc != d.b_kc || (g.vec && !vec))
     return fail(c, ZL_ERR_INVALID, "GEMM variant %s does not match the operand layout", g.name);
-  int splits = d.splits > 0 ? d.splits : gemm_splits(c, d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi);
+  int splits = d.splits > 0 ? d.splits : gemm_splits(c, d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi, vec);
   if (d.epi != zk::kEpiStore) splits = 1;
   const long long kt = cdiv(std::max(d.K, 0), g.bk);
   int per = (int)std::max<long long>(1, cdiv(kt, splits));
@@ -219,10 +236,8 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   a.epi = d.epi;
   a.act = d.act;
   a.kt_per_split = per;
-  const int a_ext = d.a_kc ? d.K : d.M;
-  const int b_ext = d.b_kc ? d.K : d.N;
-  a.vecA = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4);
-  a.vecB = aligned16(d.B) && d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
+  a.vecA = vec;
+  a.vecB = vec;
 
   const unsigned gx = (unsigned)cdiv(d.M, g.bm), gy = (unsigned)cdiv(d.N, g.bn);
   const double flops = 2.0 * d.M * d.N * (double)d.K;
