@@ -150,6 +150,22 @@ def main():
             print(f"{k:32s} {cnt:8d} {ms:8.3f} {1e3 * ms / cnt:9.2f} {tf:8.2f}", file=sys.stderr)
         print(f"step {t_step * 1e3:.3f} ms; instrumented step kernels {sum(v[0] for v in ktime.values()):.3f} ms; "
               f"GEMM kernels {gemm_ms:.3f} ms", file=sys.stderr)
+        shapes = {}
+        for i in range(ctx.lib.zl_timing_launch_count(ctx.h)):
+            name, ms, fl, sh = C.c_char_p(), C.c_double(), C.c_double(), (C.c_int * 4)()
+            ctx.check(ctx.lib.zl_timing_launch(ctx.h, i, C.byref(name), C.byref(ms), C.byref(fl), sh),
+                      "timing_launch")
+            if sh[0]:
+                key = (name.value.decode(), tuple(sh))
+                acc = shapes.setdefault(key, [0.0, 0, 0.0])
+                acc[0] += ms.value
+                acc[1] += 1
+                acc[2] += fl.value
+        print(f"{'GEMM kernel':32s} {'M x N x K / splits':>24s} {'launches':>8s} {'us/launch':>9s} {'TFLOP/s':>8s}",
+              file=sys.stderr)
+        for (k, sh), (ms, cnt, fl) in sorted(shapes.items(), key=lambda kv: -kv[1][0]):
+            print(f"{k:32s} {'%dx%dx%d/%d' % sh:>24s} {cnt:8d} {1e3 * ms / cnt:9.2f} "
+                  f"{fl / (ms / 1e3) / 1e12:8.2f}", file=sys.stderr)
 
     out = {
         "metric": "PPO update samples/sec (fwd+bwd+Adam) on 1 MI355X; % fp32-MFMA peak",

@@ -77,6 +77,12 @@ zl_status zl_timing_end(zl_ctx* ctx, double* total_ms, long long* launches, doub
 int zl_kernel_count(void);
 zl_status zl_timing_kernel(const zl_ctx* ctx, int index, const char** name, double* total_ms,
                            long long* launches, double* flops);
+/* The last finished session's timed launches in issue order: kernel name,
+ * milliseconds, algorithmic FLOP and, for GEMMs, shape4 = {M, N, K, split-K
+ * slices} (zeros for other kernels). Same timer as above, per launch. */
+long long zl_timing_launch_count(const zl_ctx* ctx);
+zl_status zl_timing_launch(const zl_ctx* ctx, long long index, const char** name, double* ms,
+                           double* flops, int* shape4);
 /* sizeof(zl_ppo_config), sizeof(zl_batch), sizeof(zl_ppo_stats) as compiled
  * into the library, for binding generators to check their struct layouts. */
 void zl_abi_struct_sizes(size_t out[3]);

@@ -72,6 +72,51 @@ def test_gemm_layouts_ragged(ctx, lt, rt, shape):
     assert err <= FWD_BWD_TOL, (shape, lt, rt, err)
 
 
+# Shapes routed to the register-resident narrow kernels (one dimension <= 32):
+# (m, n, k, lhs_t, rhs_t) and the family each exercises.
+NARROW_CASES = [
+    (24576, 29, 128, False, True),   # N <= 32, float4 loads: the actor head forward
+    (24576, 1, 128, False, True),    # N <= 16: the critic head forward
+    (1000, 17, 50, False, True),     # N <= 32 with a K tail (element loads)
+    (3, 5, 7, False, True),          # fewer rows than one strip
+    (24576, 128, 29, False, False),  # K <= 32: the actor head data gradient
+    (24576, 128, 1, False, False),   # the critic head data gradient
+    (777, 200, 17, False, False),    # K in two 16-wide chunks, ragged N
+    (29, 128, 24576, True, False),   # M <= 32: the actor head weight gradient (row slices)
+    (1, 128, 24576, True, False),    # the critic head weight gradient
+    (7, 300, 5000, True, False),     # three 128-column chunks, ragged last slice
+    (32, 64, 100, True, False),      # one slice (direct write)
+]
+
+
+@pytest.mark.parametrize("case", NARROW_CASES)
+def test_gemm_narrow_shapes(ctx, case):
+    m, n, k, lt, rt = case
+    g = np.random.default_rng(m + 7 * n + 13 * k)
+    L = g.standard_normal((m, k)).astype(np.float32)
+    R = g.standard_normal((k, n)).astype(np.float32)
+    ref = L.astype(np.float64) @ R.astype(np.float64)
+    dl = ctx.to_device(L.T.copy() if lt else L)
+    dr = ctx.to_device(R.T.copy() if rt else R)
+    out = ctx.alloc((m, n))
+    ops.gemm(ctx, out, dl, lt, dr, rt, m, n, k)
+    err = rel_amax(out.numpy(), ref)
+    print(f"[gpu] narrow gemm {case}: rel err {err:.2e}", flush=True)
+    assert err <= FWD_BWD_TOL, (case, err)
+
+
+def test_gemm_narrow_bias_elu(ctx):
+    """K <= 32 with the strided bias column + ELU epilogue of gemm_bias_act."""
+    m, n, k = 300, 100, 20
+    f = lambda r, c, s: st_val(r, c, s, 29, 13, 89, 83)  # noqa: E731
+    L, R, Bb = f(m, k, 5), f(k, n, 6), f(m, 8, 7)
+    z = L.astype(np.float64) @ R.astype(np.float64) + Bb[:, :1].astype(np.float64)
+    ref = np.where(z > 0, z, np.expm1(z))
+    out = ctx.alloc((m, n))
+    ops.gemm_bias_act(ctx, out, ctx.to_device(L), ctx.to_device(R), m, n, k, ctx.to_device(Bb), 8, True)
+    assert rel_amax(out.numpy(), ref) <= FWD_BWD_TOL
+
+
 def test_gemm_bias_elu_backward_rowsum(ctx):
     # src/biped/cutile_gemm.rs:749-826: strided bias column (stride 8), ELU, backward, row sums.
     m, n, k = 100, 300, 45

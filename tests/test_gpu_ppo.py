@@ -123,9 +123,11 @@ def test_minibatch_grads_config4(ctx):
     gac.close()
 
 
-def test_minibatch_grads_with_perm(ctx):
-    """Row gather through a device permutation (the shuffled minibatch)."""
-    ad, cd = [37, 64, 48, 7], [37, 64, 48, 1]
+@pytest.mark.parametrize("hidden", [64, 24])
+def test_minibatch_grads_with_perm(ctx, hidden):
+    """Row gather through a device permutation (the shuffled minibatch); a
+    24-wide first layer sends the gathered rows through the narrow kernels."""
+    ad, cd = [37, hidden, 48, 7], [37, hidden, 48, 1]
     g = np.random.default_rng(8)
     actor = synth.kaiming_uniform_net(g, ad, 0.1)
     critic = synth.kaiming_uniform_net(g, cd, 0.1)

@@ -95,6 +95,12 @@ SIGNATURES = {
         C.c_int, [vp, C.POINTER(C.c_double), C.POINTER(C.c_longlong), C.POINTER(C.c_double)]
     ),
     "zl_kernel_count": (C.c_int, []),
+    "zl_timing_launch_count": (C.c_longlong, [vp]),
+    "zl_timing_launch": (
+        C.c_int,
+        [vp, C.c_longlong, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_double),
+         C.POINTER(C.c_int)],
+    ),
     "zl_timing_kernel": (
         C.c_int,
         [vp, C.c_int, C.POINTER(C.c_char_p), C.POINTER(C.c_double), C.POINTER(C.c_longlong),

@@ -44,10 +44,22 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // Fixed-order sum of x[0], x[stride], ... (n terms) by one wavefront: lane l
 // adds terms l, l+64, ... in order, then the lanes are combined by wave_sum.
+// Loads are issued 8 at a time ahead of their adds (latency, not bandwidth,
+// bounds these short reductions).
 __device__ __forceinline__ float wave_sum_strided(const float* x, int n, int stride) {
   const int lane = threadIdx.x & 63;
   float s = 0.f;
-  for (int i = lane; i < n; i += 64) s += x[(long long)i * stride];
+  for (int i0 = lane; i0 < n; i0 += 8 * 64) {
+    float t[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * 64;
+      t[u] = i < n ? x[(long long)i * stride] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + u * 64 < n) s += t[u];
+  }
   return wave_sum(s);
 }
 

@@ -11,14 +11,21 @@ namespace zk {
 
 // ------------------------------------------------------------------ losses
 
-// Sum of v over lanes base .. base+n-1 of the wavefront, added left to right
-// like the reference's serial loops over action components; every lane gets
-// the result. The log-probabilities reach a few hundred in magnitude, where a
-// different summation order moves the PPO ratio by ~1e-5 relative, so the
-// order is kept.
+// Sum of v over lanes base .. base+n-1 of the wavefront (n <= G), added left
+// to right like the reference's serial loops over action components; every
+// lane gets the result. The log-probabilities reach a few hundred in
+// magnitude, where a different summation order moves the PPO ratio by ~1e-5
+// relative, so the order is kept. All G lane reads are issued before the
+// first add (they are independent), so the chain costs one shuffle latency.
+template <int G>
 __device__ __forceinline__ float lanes_sum_ordered(float v, int base, int n) {
+  float t[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) t[j] = __shfl(v, base + j, 64);
   float s = 0.f;
-  for (int j = 0; j < n; ++j) s += __shfl(v, base + j, 64);
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+    if (j < n) s += t[j];
   return s;
 }
 
@@ -31,13 +38,13 @@ __device__ __forceinline__ float lanes_sum_ordered(float v, int base, int n) {
 // and the groups of a block are then combined in a fixed order:
 // deterministic per-block partials (the rayon fold of :406-462 has no fixed
 // order either).
+template <int G>
 __device__ void actor_loss_body(const ActorLossArgs& p) {
   constexpr int kMaxGroups = kThreads / 32;
   __shared__ float sh_g[kMaxGroups][64];
   __shared__ float sh_s[kMaxGroups][2];
   if (p.guard && *p.guard == 0) return;
   const int t = threadIdx.x;
-  const int G = p.group;
   const int ng = kThreads / G;
   const int grp = t / G, k = t % G;
   const int base = (t & 63) - k;  // first lane of this group in the wavefront
@@ -51,15 +58,33 @@ __device__ void actor_loss_body(const ActorLossArgs& p) {
   float gacc = 0.f, sacc = 0.f, kacc = 0.f;
   const int r0 = blockIdx.x * p.rows_per_block;
   const int r1 = min(p.rows, r0 + p.rows_per_block);
-  for (int r = r0 + grp; r < r1; r += ng) {
-    const long long s = p.perm ? p.perm[p.row0 + r] : (long long)(p.row0 + r);
-    const float mu = on ? p.mean[(long long)r * p.ldm + k] : 0.f;
-    const float act = on ? p.action[s * p.ldact + k] : 0.f;
+  // The next row's inputs are loaded before the current row is computed, so
+  // one row's loads are always in flight behind the arithmetic.
+  struct In {
+    float mu, act, lpo, adv, mo;
+  };
+  auto fetch = [&](int rr) {
+    In x;
+    const long long s = p.perm ? p.perm[p.row0 + rr] : (long long)(p.row0 + rr);
+    x.mu = on ? p.mean[(long long)rr * p.ldm + k] : 0.f;
+    x.act = on ? p.action[s * p.ldact + k] : 0.f;
+    x.lpo = p.logp_old[s];
+    x.adv = p.adv[s];
+    x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
+    return x;
+  };
+  int r = r0 + grp;
+  In cur{};
+  if (r < r1) cur = fetch(r);
+  for (; r < r1; r += ng) {
+    In nxt{};
+    if (r + ng < r1) nxt = fetch(r + ng);
+    const float mu = cur.mu, act = cur.act;
     // ActorCritic::logp, ppo.rs:297-305
     const float dz = (act - mu) / sd;
-    const float lp = lanes_sum_ordered(on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f, base, A);
-    const float ratio = expf(lp - p.logp_old[s]);
-    const float a = p.adv[s];
+    const float lp = lanes_sum_ordered<G>(on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f, base, A);
+    const float ratio = expf(lp - cur.lpo);
+    const float a = cur.adv;
     const float surr = fminf(ratio * a, clampf(ratio, lo, hi) * a);
     const bool clipped = (a >= 0.0f && ratio > hi) || (a < 0.0f && ratio < lo);
     float gm = 0.f, c = 0.f;
@@ -76,10 +101,10 @@ __device__ void actor_loss_body(const ActorLossArgs& p) {
     }
     sacc += surr * p.scale;
     if (p.mean_old) {  // ActorCritic::kl, ppo.rs:327-334
-      const float mo = on ? p.mean_old[s * p.ldmo + k] : 0.f;
-      const float y = (mu - mo) * inv_sd;
-      kacc += lanes_sum_ordered(on ? 0.5f * (y * y) : 0.f, base, A) * p.scale;
+      const float y = (mu - cur.mo) * inv_sd;
+      kacc += lanes_sum_ordered<G>(on ? 0.5f * (y * y) : 0.f, base, A) * p.scale;
     }
+    cur = nxt;
   }
   sh_g[grp][k] = gacc;
   if (k == 0) {
@@ -149,10 +174,24 @@ __device__ void sumsq_body(const SumsqArgs& p) {
   }
   const long long lo = (long long)cb * p.chunk;
   const long long hi = min(len, lo + p.chunk);
+  const float* x = p.x + off;
   float s = 0.f;
-  for (long long i = lo + threadIdx.x; i < hi; i += kThreads) {
-    const float x = p.x[off + i];
-    s += x * x;
+  if ((p.chunk & 3) == 0 && ((uintptr_t)x & 15u) == 0) {
+    // Quads (lo is a multiple of 4), then the scalar tail of the last chunk.
+    const long long hi4 = lo + ((hi - lo) & ~3LL);
+    for (long long i = lo + 4 * threadIdx.x; i < hi4; i += 4 * kThreads) {
+      const float4 v = *reinterpret_cast<const float4*>(x + i);
+      s += v.x * v.x;
+      s += v.y * v.y;
+      s += v.z * v.z;
+      s += v.w * v.w;
+    }
+    for (long long i = hi4 + threadIdx.x; i < hi; i += kThreads) s += x[i] * x[i];
+  } else {
+    for (long long i = lo + threadIdx.x; i < hi; i += kThreads) {
+      const float v = x[i];
+      s += v * v;
+    }
   }
   const float tot = block_sum(s, red);
   if (threadIdx.x == 0) p.part[b] = tot;
@@ -172,7 +211,7 @@ __device__ void finalize_body(const FinalizeArgs& p) {
   const int wave = t >> 6, lane = t & 63;
   const int A = p.pp.A;
   const int nq = 5 + A;
-  for (int j = wave; j < nq; j += kThreads / 64) {
+  for (int j = wave; j < nq; j += kFinalizeThreads / 64) {
     float v;
     if (j == 0)
       v = wave_sum_strided(p.astat_part, p.nb_a, 2);
@@ -263,20 +302,53 @@ __device__ void adam_body(const AdamArgs& p) {
   const float b1 = p.beta1, b2 = p.beta2, eps = p.eps;
   const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
   const long long i0 = ((long long)blockIdx.x * kThreads + threadIdx.x) * 4;
+  if (i0 >= p.n) return;
+  const bool quad = i0 + 4 <= p.n &&
+                    ((((uintptr_t)p.p | (uintptr_t)p.g | (uintptr_t)p.m | (uintptr_t)p.v) & 15u) == 0);
+  float x[4], g[4], m[4], v[4];
+  if (quad) {
+    const float4 x4 = *reinterpret_cast<const float4*>(p.p + i0);
+    const float4 g4 = *reinterpret_cast<const float4*>(p.g + i0);
+    const float4 m4 = *reinterpret_cast<const float4*>(p.m + i0);
+    const float4 v4 = *reinterpret_cast<const float4*>(p.v + i0);
+    x[0] = x4.x, x[1] = x4.y, x[2] = x4.z, x[3] = x4.w;
+    g[0] = g4.x, g[1] = g4.y, g[2] = g4.z, g[3] = g4.w;
+    m[0] = m4.x, m[1] = m4.y, m[2] = m4.z, m[3] = m4.w;
+    v[0] = v4.x, v[1] = v4.y, v[2] = v4.z, v[3] = v4.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = i0 + j < p.n;
+      x[j] = in ? p.p[i0 + j] : 0.f;
+      g[j] = in ? p.g[i0 + j] : 0.f;
+      m[j] = in ? p.m[i0 + j] : 0.f;
+      v[j] = in ? p.v[i0 + j] : 0.f;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const long long i = i0 + j;
-    if (i < p.n) {
-      const int grp = i < p.end_a ? 0 : (i < p.end_c ? 1 : 2);
-      const float sc = grp == 0 ? s0 : (grp == 1 ? s1 : s2);
-      const float gr = p.g[i] * sc;
-      const float m = b1 * p.m[i] + omb1 * gr;
-      const float v = b2 * p.v[i] + omb2 * gr * gr;
-      float x = p.p[i] - lr * (m / bc1) / (sqrtf(v / bc2) + eps);
-      if (grp == 2 && p.clamp_ls) x = clampf(x, -1.6f, 1.0f);
-      p.m[i] = m;
-      p.v[i] = v;
-      p.p[i] = x;
+    const int grp = i < p.end_a ? 0 : (i < p.end_c ? 1 : 2);
+    const float sc = grp == 0 ? s0 : (grp == 1 ? s1 : s2);
+    const float gr = g[j] * sc;
+    m[j] = b1 * m[j] + omb1 * gr;
+    v[j] = b2 * v[j] + omb2 * gr * gr;
+    float xn = x[j] - lr * (m[j] / bc1) / (sqrtf(v[j] / bc2) + eps);
+    if (grp == 2 && p.clamp_ls) xn = clampf(xn, -1.6f, 1.0f);
+    x[j] = xn;
+  }
+  if (quad) {
+    *reinterpret_cast<float4*>(p.m + i0) = make_float4(m[0], m[1], m[2], m[3]);
+    *reinterpret_cast<float4*>(p.v + i0) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(p.p + i0) = make_float4(x[0], x[1], x[2], x[3]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (i0 + j < p.n) {
+        p.m[i0 + j] = m[j];
+        p.v[i0 + j] = v[j];
+        p.p[i0 + j] = x[j];
+      }
     }
   }
 }
@@ -489,10 +561,18 @@ __device__ void clamp_body(const ClampArgs& p) {
 #define ZK_KERNEL(NAME, ARGS, BODY) \
   extern "C" __global__ __launch_bounds__(256) void NAME(zk::ARGS p) { zk::BODY(p); }
 
-ZK_KERNEL(zk_actor_loss, ActorLossArgs, actor_loss_body)
+// One lane group of 32 (A <= 32) or 64 (A <= 64) lanes per sample.
+extern "C" __global__ __launch_bounds__(256) void zk_actor_loss(zk::ActorLossArgs p) {
+  if (p.group == 32)
+    zk::actor_loss_body<32>(p);
+  else
+    zk::actor_loss_body<64>(p);
+}
 ZK_KERNEL(zk_value_loss, ValueLossArgs, value_loss_body)
 ZK_KERNEL(zk_sumsq, SumsqArgs, sumsq_body)
-ZK_KERNEL(zk_finalize, FinalizeArgs, finalize_body)
+extern "C" __global__ __launch_bounds__(zk::kFinalizeThreads) void zk_finalize(zk::FinalizeArgs p) {
+  zk::finalize_body(p);
+}
 ZK_KERNEL(zk_adam, AdamArgs, adam_body)
 ZK_KERNEL(zk_epoch_begin, EpochBeginArgs, epoch_begin_body)
 ZK_KERNEL(zk_kl, KlArgs, kl_body)

@@ -7,6 +7,9 @@
 
 namespace zk {
 
+// Block size of zk_finalize (one wavefront per fixed-order sum, 16 in flight).
+constexpr int kFinalizeThreads = 1024;
+
 enum EpiMode : int {
   kEpiStore = 0,    // C = acc
   kEpiBiasN = 1,    // C = act(acc + bias[n])           (batch-major forward)

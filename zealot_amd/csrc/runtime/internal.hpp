@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <array>
 #include <string>
 #include <vector>
 
@@ -34,14 +35,29 @@ enum KernelId : int {
   K_GEMM_BASE
 };
 
-// One GEMM variant: operand orientation, tile, k-tile, block size and
-// whether it loads both operands as float4 rows (vec) or element by element.
+// Kernel family of a GEMM variant: LDS-tiled (gemm_mfma.hip) or one of the
+// register-resident narrow kernels (narrow.hip): N <= 32 (forward of an
+// output layer), K <= 32 (its data gradient), M <= 32 (its weight gradient).
+enum GemmKind : int { G_TILED = 0, G_NARROW_N = 1, G_NARROW_K = 2, G_NARROW_M = 3 };
+
+// One GEMM variant: operand orientation, tile (for the narrow kernels: rows
+// per block and the largest narrow dimension), k-tile, block size, whether it
+// loads both operands as float4 rows (vec) or element by element, and family.
 struct GemmKernel {
   const char* name;
   bool a_kc, b_kc;
   int bm, bn, bk, threads;
   bool vec;
+  int kind = G_TILED;
 };
+
+// Narrow kernels: 16-row strips, four wavefronts per block; the data-gradient
+// form takes 32 columns per block, the weight-gradient form 64 columns and
+// row slices in multiples of 4 wavefronts x 16 rows.
+constexpr int kNarrowRows = 64;
+constexpr int kNarrowKCols = 32;
+constexpr int kNarrowCols = 64;
+constexpr int kNarrowSliceQuantum = 64;
 
 extern const char* const kFixedNames[K_GEMM_BASE];
 extern const GemmKernel kGemmTable[];
@@ -97,16 +113,26 @@ struct zl_ctx {
   size_t ev_used = 0;
   std::vector<int> ev_kernel;       // kernel id of timed launch i
   std::vector<double> ev_flops;     // algorithmic FLOP of timed launch i
+  std::vector<std::array<int, 4>> ev_shape;  // GEMM M, N, K, splits of timed launch i
   double pending_flops = 0.0;       // set by run_gemm for the next launch
-  // Per-kernel results of the last finished timing session.
+  std::array<int, 4> pending_shape{};  // likewise
+  // Per-kernel results of the last finished timing session, and its
+  // launches in issue order (kernel id, ms, FLOP, GEMM shape).
   std::vector<double> rep_ms, rep_flops;
   std::vector<long long> rep_launches;
+  std::vector<int> last_kernel;
+  std::vector<double> last_ms, last_flops;
+  std::vector<std::array<int, 4>> last_shape;
   // Tuning overrides (environment, read at zl_init): forced GEMM variant per
   // layout (ZL_GEMM_AKBK / _AKBN / _AMBN / _AMBK), split-K slice count
   // (ZL_SPLITK) and the split-K target grid size (ZL_SPLITK_TARGET).
   int force_gemm[4] = {-1, -1, -1, -1};
   int force_splits = 0;
   int splitk_target = 512;
+  // Narrow kernels for shapes with a dimension <= 32 (ZL_NARROW=0 turns them
+  // off) and the block count their row slices aim at (ZL_NARROW_TARGET).
+  bool narrow = true;
+  int narrow_target = 256;
 };
 
 namespace zl {
@@ -133,6 +159,7 @@ zl_status launch(zl_ctx* c, int k, unsigned gx, unsigned gy, unsigned gz, const 
     if (s) return s;
   }
   c->pending_flops = 0.0;
+  c->pending_shape = {0, 0, 0, 0};
   void* params[] = {(void*)&a};
   hipError_t e = hipModuleLaunchKernel(c->fn[k], gx, gy, gz, threads, 1, 1, shmem, c->stream,
                                        params, nullptr);

@@ -392,7 +392,7 @@ struct zl_ppo {
   float* kl_part = nullptr;
   float* adv_part = nullptr;
   int nb_cap = 0, nsq_a = 0, nsq = 0;
-  static constexpr int kSqChunk = 4096;
+  static constexpr int kSqChunk = 1024;  // one float4 per thread
   static constexpr int kAdvChunk = 4096;
   size_t adv_part_cap = 0;
   zk::DevState* dstate = nullptr;
@@ -547,7 +547,7 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       fz.nb_v = nb;
       fz.nsq = p->nsq;
       fz.nsq_a = p->nsq_a;
-      if ((s = launch(c, K_FINALIZE, 1, 1, 1, fz))) return s;
+      if ((s = launch(c, K_FINALIZE, 1, 1, 1, fz, 0, zk::kFinalizeThreads))) return s;
       zk::AdamArgs ad{};
       ad.p = p->params;
       ad.g = p->grads;

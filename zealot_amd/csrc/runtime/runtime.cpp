@@ -21,7 +21,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_clamp",
 };
 
-// {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads}
+// {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
 const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bk_64x128x16_w22", true, true, 64, 128, 16, 256, true},
     {"zk_gemm_ak_bk_96x128x32_w24", true, true, 96, 128, 32, 512, true},
@@ -47,6 +47,13 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bn_64x128x16_w22_s", true, false, 64, 128, 16, 256, false},
     {"zk_gemm_am_bn_64x128x16_w22_s", false, false, 64, 128, 16, 256, false},
     {"zk_gemm_am_bk_64x128x16_w22_s", false, true, 64, 128, 16, 256, false},
+    {"zk_narrow_n1_v", true, true, kNarrowRows, 16, 16, 256, true, G_NARROW_N},
+    {"zk_narrow_n2_v", true, true, kNarrowRows, 32, 16, 256, true, G_NARROW_N},
+    {"zk_narrow_n1_s", true, true, kNarrowRows, 16, 16, 256, false, G_NARROW_N},
+    {"zk_narrow_n2_s", true, true, kNarrowRows, 32, 16, 256, false, G_NARROW_N},
+    {"zk_narrow_k", true, false, kNarrowRows, kNarrowKCols, 32, 256, false, G_NARROW_K},
+    {"zk_narrow_m1", false, false, 16, kNarrowCols, 16, 256, false, G_NARROW_M},
+    {"zk_narrow_m2", false, false, 32, kNarrowCols, 16, 256, false, G_NARROW_M},
 };
 const int kGemmCount = (int)(sizeof(kGemmTable) / sizeof(kGemmTable[0]));
 
@@ -91,9 +98,11 @@ zl_status timing_mark(zl_ctx* c, bool stop, int kernel, double flops) {
     if (c->ev_kernel.size() <= c->ev_used) {
       c->ev_kernel.resize(c->ev_used + 1);
       c->ev_flops.resize(c->ev_used + 1);
+      c->ev_shape.resize(c->ev_used + 1);
     }
     c->ev_kernel[c->ev_used] = kernel;
     c->ev_flops[c->ev_used] = flops;
+    c->ev_shape[c->ev_used] = c->pending_shape;
     ZL_HIP(c, hipEventRecord(c->ev_pool[c->ev_used * 2], c->stream));
   } else {
     ZL_HIP(c, hipEventRecord(c->ev_pool[c->ev_used * 2 + 1], c->stream));
@@ -124,13 +133,23 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // the narrow heads (measured on gfx950 at 24,576 rows).
 int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec) {
   const int lay = layout_of(a_kc, b_kc);
+  const bool forced = c && c->force_gemm[lay] >= 0;
+  if (!forced && (!c || c->narrow)) {
+    if (lay == L_AK_BK && N <= 32) {
+      const bool v = vec && K % 16 == 0;
+      if (N <= 16) return gemm_id(v ? "zk_narrow_n1_v" : "zk_narrow_n1_s");
+      return gemm_id(v ? "zk_narrow_n2_v" : "zk_narrow_n2_s");
+    }
+    if (lay == L_AK_BN && K <= 32) return gemm_id("zk_narrow_k");
+    if (lay == L_AM_BN && M <= 32) return gemm_id(M <= 16 ? "zk_narrow_m1" : "zk_narrow_m2");
+  }
   if (!vec) {
     static const char* const kScalar[4] = {
         "zk_gemm_ak_bk_64x128x16_w22_s", "zk_gemm_ak_bn_64x128x16_w22_s",
         "zk_gemm_am_bn_64x128x16_w22_s", "zk_gemm_am_bk_64x128x16_w22_s"};
     return gemm_id(kScalar[lay]);
   }
-  if (c && c->force_gemm[lay] >= 0) return c->force_gemm[lay];
+  if (forced) return c->force_gemm[lay];
   const char* name = nullptr;
   switch (lay) {
     case L_AK_BK:
@@ -160,9 +179,23 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
   return gemm_id(name);
 }
 
+// Rows per slice of a narrow weight-gradient GEMM: a multiple of
+// kNarrowSliceQuantum (one round of its wavefronts' two-chunk loads) so that
+// slices x column chunks come near the narrow block target.
+static int narrow_rows_per_slice(const zl_ctx* c, int N, int K, int epi) {
+  const long long full = round_up(std::max(K, 1), 16);
+  if (epi != zk::kEpiStore) return (int)full;  // epilogues need the whole sum: one slice
+  const long long gy = cdiv(N, kNarrowCols);
+  const long long target = std::max<long long>(1, (c ? c->narrow_target : 256) / gy);
+  const long long r = round_up(cdiv(K, target), kNarrowSliceQuantum);
+  return (int)std::min(r, full);
+}
+
 int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi, bool vec) {
-  if (epi != zk::kEpiStore) return 1;
   const GemmKernel& g = kGemmTable[pick_gemm(c, M, N, K, a_kc, b_kc, vec) - K_GEMM_BASE];
+  if (g.kind == G_NARROW_M) return (int)cdiv(std::max(K, 1), narrow_rows_per_slice(c, N, K, epi));
+  if (g.kind != G_TILED) return 1;
+  if (epi != zk::kEpiStore) return 1;
   const long long tiles = cdiv(M, g.bm) * cdiv(N, g.bn);
   const long long kt = cdiv(K, g.bk);
   long long s;
@@ -212,11 +245,27 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   const GemmKernel& g = kGemmTable[kid - K_GEMM_BASE];
   if (g.a_kc != d.a_kc || g.b_kc != d.b_kc || (g.vec && !vec))
     return fail(c, ZL_ERR_INVALID, "GEMM variant %s does not match the operand layout", g.name);
-  int splits = d.splits > 0 ? d.splits : gemm_splits(c, d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi, vec);
-  if (d.epi != zk::kEpiStore) splits = 1;
-  const long long kt = cdiv(std::max(d.K, 0), g.bk);
-  int per = (int)std::max<long long>(1, cdiv(kt, splits));
-  splits = (int)std::max<long long>(1, cdiv(kt, per));
+  int splits, per;
+  unsigned gx, gy;
+  if (g.kind == G_NARROW_N || g.kind == G_NARROW_K) {
+    splits = 1;
+    per = 0;
+    gx = (unsigned)cdiv(d.M, kNarrowRows);
+    gy = g.kind == G_NARROW_K ? (unsigned)cdiv(d.N, kNarrowKCols) : 1u;
+  } else if (g.kind == G_NARROW_M) {
+    per = narrow_rows_per_slice(c, d.N, d.K, d.epi);
+    splits = (int)cdiv(std::max(d.K, 1), per);
+    gx = (unsigned)splits;
+    gy = (unsigned)cdiv(d.N, kNarrowCols);
+  } else {
+    splits = d.splits > 0 ? d.splits : gemm_splits(c, d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi, vec);
+    if (d.epi != zk::kEpiStore) splits = 1;
+    const long long kt = cdiv(std::max(d.K, 0), g.bk);
+    per = (int)std::max<long long>(1, cdiv(kt, splits));
+    splits = (int)std::max<long long>(1, cdiv(kt, per));
+    gx = (unsigned)cdiv(d.M, g.bm);
+    gy = (unsigned)cdiv(d.N, g.bn);
+  }
 
   zk::GemmArgs a{};
   a.A = d.A;
@@ -239,7 +288,6 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   a.vecA = vec;
   a.vecB = vec;
 
-  const unsigned gx = (unsigned)cdiv(d.M, g.bm), gy = (unsigned)cdiv(d.N, g.bn);
   const double flops = 2.0 * d.M * d.N * (double)d.K;
   if (splits == 1) {
     a.C = d.C;
@@ -247,6 +295,7 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
     a.split_stride = 0;
     a.rowsumA = d.rowsum_out;
     c->pending_flops = flops;
+    c->pending_shape = {d.M, d.N, d.K, 1};
     return launch(c, kid, gx, gy, 1, a, 0, (unsigned)g.threads);
   }
   const size_t mn = (size_t)d.M * d.N;
@@ -265,7 +314,9 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
   a.split_stride = (long long)mn;
   a.rowsumA = d.rowsum_out ? ws + (size_t)splits * mn : nullptr;
   c->pending_flops = flops;
-  zl_status s = launch(c, kid, gx, gy, (unsigned)splits, a, 0, (unsigned)g.threads);
+  c->pending_shape = {d.M, d.N, d.K, splits};
+  zl_status s = launch(c, kid, gx, gy, g.kind == G_NARROW_M ? 1u : (unsigned)splits, a, 0,
+                       (unsigned)g.threads);
   if (s) return s;
   zk::SplitReduceArgs r{};
   r.part = ws;
@@ -509,6 +560,8 @@ zl_status zl_init(int device, zl_ctx** out) {
   }
   if (const char* v = getenv("ZL_SPLITK")) c->force_splits = std::max(0, atoi(v));
   if (const char* v = getenv("ZL_SPLITK_TARGET")) c->splitk_target = std::max(1, atoi(v));
+  if (const char* v = getenv("ZL_NARROW")) c->narrow = atoi(v) != 0;
+  if (const char* v = getenv("ZL_NARROW_TARGET")) c->narrow_target = std::max(1, atoi(v));
   // Default-priority stream (no priority variants are used anywhere).
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -554,9 +607,14 @@ zl_status zl_timing_end(zl_ctx* c, double* total_ms, long long* launches, double
   c->rep_flops.assign(nk, 0.0);
   c->rep_launches.assign(nk, 0);
   double tot = 0.0, fl = 0.0;
+  c->last_kernel.assign(c->ev_kernel.begin(), c->ev_kernel.begin() + c->ev_used);
+  c->last_flops.assign(c->ev_flops.begin(), c->ev_flops.begin() + c->ev_used);
+  c->last_shape.assign(c->ev_shape.begin(), c->ev_shape.begin() + c->ev_used);
+  c->last_ms.assign(c->ev_used, 0.0);
   for (size_t i = 0; i < c->ev_used; ++i) {
     float ms = 0.f;
     ZL_HIP(c, hipEventElapsedTime(&ms, c->ev_pool[2 * i], c->ev_pool[2 * i + 1]));
+    c->last_ms[i] = ms;
     tot += ms;
     fl += c->ev_flops[i];
     const int k = c->ev_kernel[i];
@@ -582,6 +640,19 @@ zl_status zl_timing_kernel(const zl_ctx* c, int id, const char** name, double* t
   if (total_ms) *total_ms = have ? c->rep_ms[id] : 0.0;
   if (launches) *launches = have ? c->rep_launches[id] : 0;
   if (flops) *flops = have ? c->rep_flops[id] : 0.0;
+  return ZL_OK;
+}
+
+long long zl_timing_launch_count(const zl_ctx* c) { return c ? (long long)c->last_ms.size() : 0; }
+
+zl_status zl_timing_launch(const zl_ctx* c, long long i, const char** name, double* ms,
+                           double* flops, int* shape4) {
+  if (!c || i < 0 || i >= (long long)c->last_ms.size()) return ZL_ERR_INVALID;
+  if (name) *name = zl::kernel_name(c->last_kernel[i]);
+  if (ms) *ms = c->last_ms[i];
+  if (flops) *flops = c->last_flops[i];
+  if (shape4)
+    for (int j = 0; j < 4; ++j) shape4[j] = c->last_shape[i][j];
   return ZL_OK;
 }
 
@@ -824,7 +895,7 @@ zl_status zl_adam_step(zl_ctx* c, float* p, const float* g, float* m, float* v, 
 zl_status zl_grad_sqnorm(zl_ctx* c, const float* x, size_t n, float* out_dev) {
   if (!c) return ZL_ERR_INVALID;
   if (!x || !out_dev) return fail(c, ZL_ERR_INVALID, "zl_grad_sqnorm: null pointer");
-  const int chunk = 8192;
+  const int chunk = 2048;
   const int nb = std::max(1, (int)cdiv((long long)n, chunk));
   zl_status s = ensure_ws(c, (size_t)nb);
   if (s) return s;
