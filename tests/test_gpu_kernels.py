@@ -301,10 +301,12 @@ def test_adv_normalize(ctx):
     assert np.all(d2.numpy() == 0.0)
 
 
-def test_actor_value_grad_ops(ctx):
+@pytest.mark.parametrize("A", [29, 40])
+def test_actor_value_grad_ops(ctx, A):
     """zl_ppo_actor_grad / zl_ppo_value_grad vs the oracle's per-sample fold
-    (through a 1-layer linear actor whose output is the mean itself)."""
-    rows, A = 777, 29
+    (through a 1-layer linear actor whose output is the mean itself); A = 40
+    takes the 64-lane-group loss kernel."""
+    rows = 777
     g = np.random.default_rng(21)
     mean = g.standard_normal((rows, A)).astype(np.float32)
     action = (mean + 0.6 * g.standard_normal((rows, A))).astype(np.float32)

@@ -12,8 +12,12 @@ namespace zk {
 constexpr int kThreads = 256;
 constexpr float kLogSqrt2Pi = 0.9189385f;  // zealot-rl/src/ppo.rs:18
 
-// zealot-rl/src/net.rs:14-16: x > 0 ? x : exp(x) - 1 (not expm1).
-__device__ __forceinline__ float elu(float x) { return x > 0.0f ? x : expf(x) - 1.0f; }
+// zealot-rl/src/net.rs:14-16: x > 0 ? x : exp(x) - 1 (not expm1). Used in
+// the GEMM epilogues over every hidden activation, so exp is the hardware
+// exp2 (v_exp_f32) of x * log2(e): on the negative branch the result lies in
+// (-1, 0] with an absolute error below ~2e-7 (rounding the product x * log2(e)
+// costs exp(x) * |x| * 2^-24 <= 2^-24 / e, plus about one ulp of exp2).
+__device__ __forceinline__ float elu(float x) { return x > 0.0f ? x : __expf(x) - 1.0f; }
 
 // zealot-rl/src/net.rs:21-23: derivative from the post-activation.
 __device__ __forceinline__ float elu_grad_from_act(float a) { return a > 0.0f ? 1.0f : a + 1.0f; }
@@ -63,14 +67,15 @@ __device__ __forceinline__ float wave_sum_strided(const float* x, int n, int str
   return wave_sum(s);
 }
 
-// Deterministic in-block tree sum over kThreads values held one per thread.
-// `sm` must hold kThreads floats. Returns the total in every thread.
+// Deterministic in-block tree sum over N values held one per thread (N =
+// the block size). `sm` must hold N floats. Returns the total in every thread.
+template <int N = kThreads>
 __device__ __forceinline__ float block_sum(float v, float* sm) {
   const int t = threadIdx.x;
   sm[t] = v;
   __syncthreads();
 #pragma unroll
-  for (int s = kThreads / 2; s > 0; s >>= 1) {
+  for (int s = N / 2; s > 0; s >>= 1) {
     if (t < s) sm[t] = sm[t] + sm[t + s];
     __syncthreads();
   }

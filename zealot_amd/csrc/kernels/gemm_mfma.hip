@@ -7,13 +7,23 @@
 // Operand storage: A is either K-contiguous (row m at A + m*lda) or
 // M-contiguous (row k at A + k*lda); B is either K-contiguous (row n at
 // B + n*ldb) or N-contiguous (row k at B + k*ldb). Each operand tile is staged
-// in LDS in its global orientation (float4 global loads -> ds_write_b128) and
-// fed to the MFMA with one ds_read_b32 per lane per k-step; the row padding of
-// each LDS orientation makes those reads bank-conflict free. A workgroup is
-// WM x WN wave64s; each wave owns TM x TN 16x16 accumulator tiles. K is walked
-// in BK-wide k-tiles, double-buffered in LDS with the next k-tile's global
-// loads in flight during the MFMAs. BK = 32 makes every K-contiguous row
-// segment a full 128-byte line.
+// in LDS in its global orientation (float4 global loads -> ds_write_b128). A
+// workgroup is WM x WN wave64s; each wave owns TM x TN 16x16 accumulator
+// tiles. K is walked in BK-wide k-tiles, double-buffered in LDS with the next
+// k-tile's global loads in flight during the MFMAs. BK = 32 makes every
+// K-contiguous row segment a full 128-byte line.
+//
+// Reduction-index assignment. v_mfma_f32_16x16x4f32 takes A[i][s] from lane
+// i + 16 s and B[s][j] from lane j + 16 s. Within each 16-wide chunk q of a
+// k-tile, lane group s of MFMA step c carries k = 16 q + 4 s + c in both
+// operands (any bijection gives the same sum), so a lane's four k values of
+// a chunk are consecutive: a K-contiguous tile feeds four MFMAs with one
+// ds_read_b128, the other orientation with four ds_read_b32. LDS is read as
+// two half-waves of 32 lanes over 32 banks; the row lengths below make both
+// kinds of read conflict-free: BK + 4 (K-contiguous, 8 lanes of 16 rows per
+// b128 pass land on 8 disjoint 4-bank groups) and EXT + 4 (the rows k and
+// k + 4 of one half-wave are 16 banks apart). That bank model is the one the
+// SQ_LDS_BANK_CONFLICT counters of the earlier row-per-lane-group layout fit.
 //
 // Split-K: grid.z slices the k-tiles; each slice writes a dense partial
 // [M x N] at C + z*split_stride and zk_splitk_reduce sums the slices in fixed
@@ -35,17 +45,30 @@ namespace zk {
 // not change along K) and one k-tile ahead for the other orientation.
 template <int EXT, bool KC, int BK, int NT, bool VEC>
 struct Tile {
-  // Row length in LDS. K-contiguous rows get +4 floats so 16 rows read at one
-  // k hit distinct banks; the other orientation needs LD = 16 or 48 (mod 64)
-  // so the four 16-lane k-groups of one read land in disjoint bank windows.
-  static constexpr int LD =
-      KC ? (BK + 4) : ((EXT % 64 == 16 || EXT % 64 == 48) ? EXT : EXT + 16);
+  // Row length in LDS (see the file header): conflict-free fragment reads
+  // with 16-byte aligned rows for the ds_write_b128 stores.
+  static constexpr int LD = KC ? (BK + 4) : (EXT + 4);
   static constexpr int SIZE = KC ? EXT * LD : BK * LD;
   static constexpr int ELEMS = EXT * BK;
   static constexpr int NQ = ELEMS / 4;            // float4 quads per tile
   static constexpr int NV = (NQ + NT - 1) / NT;   // quads per thread
   static constexpr int NS = (ELEMS + NT - 1) / NT;  // scalars per thread
   static constexpr int QR = KC ? BK / 4 : EXT / 4;  // quads per stored row
+  static constexpr int ROWS = KC ? EXT : BK;         // stored rows
+  // Stored row of float4 quad i (its column is quad i % QR). With 4 or 8
+  // quads per row, a 16-lane pass of a ds_write_b128 would cover 2-4
+  // consecutive rows whose bank windows overlap at these row lengths; the
+  // rows of one pass are spread QR apart instead, which places them in
+  // disjoint bank windows. Eight consecutive lanes still read 128
+  // contiguous bytes of one row from global memory.
+  __device__ __forceinline__ static int row_of(int i) {
+    if constexpr (QR < 16 && 16 % QR == 0 && ROWS % 16 == 0) {
+      const int p = i / 16;
+      return 16 * (p / QR) + p % QR + ((i % 16) / QR) * QR;
+    } else {
+      return i / QR;
+    }
+  }
   float4 v[VEC ? NV : 1];
   float s[VEC ? 1 : NS];
   // Vector path, per quad: KC -> storage row pointer (perm resolved, row
@@ -75,7 +98,7 @@ struct Tile {
       const int i = t + j * NT;
       const int iq = (NQ % NT == 0 || i < NQ) ? i : 0;
       if (KC) {
-        const int e = e0 + iq / QR;
+        const int e = e0 + row_of(iq);
         ok[j] = (NQ % NT == 0 || i < NQ) && e < etot;
         const int ec = min(e, etot - 1);
         const int sr = perm ? perm[ec] : ec;
@@ -96,7 +119,7 @@ struct Tile {
     for (int j = 0; j < NV; ++j) {
       const int i = t + j * NT;
       const int iq = (NQ % NT == 0 || i < NQ) ? i : 0;
-      pk[j] = perm[min(k0 + iq / QR, K - 1)];
+      pk[j] = perm[min(k0 + row_of(iq), K - 1)];
     }
   }
 
@@ -112,7 +135,7 @@ struct Tile {
           const int k = min(k0 + (iq % QR) * 4, ((K + 3) & ~3) - 4);
           v[j] = *reinterpret_cast<const float4*>(rp[j] + k);
         } else {
-          const int kc = min(k0 + iq / QR, K - 1);
+          const int kc = min(k0 + row_of(iq), K - 1);
           const int sr = perm ? pk[j] : kc;
           v[j] = *reinterpret_cast<const float4*>(base + (long long)sr * ld + col[j]);
         }
@@ -138,14 +161,21 @@ struct Tile {
   }
 
   // Registers -> LDS buffer, zeroing everything outside [0, etot) x [0, K).
+  // A k-tile that lies wholly inside the matrix (the common case) is stored
+  // without masks.
   __device__ __forceinline__ void store(float* __restrict__ sm, int k0) const {
     const int t = threadIdx.x;
     if constexpr (VEC) {
+      const bool full = e0 + EXT <= etot && k0 + BK <= K;
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
         const int i = t + j * NT;
         if (NQ % NT != 0 && i >= NQ) continue;
         float4 x = v[j];
+        if (full) {  // row row_of(i), quad i % QR in either orientation
+          *reinterpret_cast<float4*>(sm + row_of(i) * LD + (i % QR) * 4) = x;
+          continue;
+        }
         if (KC) {
           const int kq = (i % QR) * 4, k = k0 + kq;
           const bool good = ok[j] && k < K;
@@ -153,9 +183,9 @@ struct Tile {
           x.y = (good && k + 1 < K) ? x.y : 0.f;
           x.z = (good && k + 2 < K) ? x.z : 0.f;
           x.w = (good && k + 3 < K) ? x.w : 0.f;
-          *reinterpret_cast<float4*>(sm + (i / QR) * LD + kq) = x;
+          *reinterpret_cast<float4*>(sm + row_of(i) * LD + kq) = x;
         } else {
-          const int kk = i / QR, c4 = (i % QR) * 4;
+          const int kk = row_of(i), c4 = (i % QR) * 4;
           const int e = e0 + c4;
           const bool good = ok[j] && k0 + kk < K;
           x.x = good ? x.x : 0.f;
@@ -189,19 +219,30 @@ struct Tile {
   __device__ __forceinline__ static float at(const float* sm, int e, int k) {
     return KC ? sm[e * LD + k] : sm[k * LD + e];
   }
+
+  // MFMA operand fragment of chunk q for lane group g: elements
+  // (e, 16 q + 4 g + c), c = 0..3.
+  __device__ __forceinline__ static float4 frag(const float* sm, int e, int q, int g) {
+    if constexpr (KC) {
+      return *reinterpret_cast<const float4*>(sm + e * LD + 16 * q + 4 * g);
+    } else {
+      const float* x = sm + (16 * q + 4 * g) * LD + e;
+      return float4{x[0], x[LD], x[2 * LD], x[3 * LD]};
+    }
+  }
 };
 
 // KG > 1 splits every staged k-tile between KG groups of WM x WN waves (group
-// g runs k-steps [g, g+1) * BK/4/KG); the groups' accumulators are added in
-// LDS in group order before the epilogue, so a tile gets KG times the waves
-// without any global split-K partials.
+// g runs the 16-wide chunks [g, g+1) * BK/16/KG); the groups' accumulators are
+// added in LDS in group order before the epilogue, so a tile gets KG times
+// the waves without any global split-K partials.
 template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, int KG, bool VEC>
-__device__ __forceinline__ void gemm_body(const GemmArgs& p) {
+__device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
   constexpr int NT = 64 * WM * WN * KG;
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
   static_assert(TM >= 1 && TN >= 1 && TM * WM * 16 == BM && TN * WN * 16 == BN, "wave tiling");
-  static_assert(BK % (4 * KG) == 0, "k-steps of 4 per group");
+  static_assert(BK % (16 * KG) == 0, "16-wide chunks per group");
   static_assert(KG == 1 || KG == 2, "one LDS exchange round");
   constexpr int RSG = NT / BM >= 1 ? NT / BM : 1;  // threads per A row in the row sums
   using TA = Tile<BM, AK, BK, NT, VEC>;
@@ -211,7 +252,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
   static_assert(SMEM >= NT, "LDS holds one float per thread for the row sums");
   // One allocation: [A buf 0][A buf 1][B buf 0][B buf 1], reused after the
   // k-loop for the row-sum and k-group exchanges.
-  __shared__ float smem[SMEM];
+  __shared__ __align__(16) float smem[SMEM];
   auto sA = [&](int b) { return smem + b * TA::SIZE; };
   auto sB = [&](int b) { return smem + 2 * TA::SIZE + b * TB::SIZE; };
 
@@ -221,8 +262,9 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
   const int wm = wave % WM, wn = wave / WM;
   const int lr = lane & 15, lg = lane >> 4;
   const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  if (m0 >= p.M || n0 >= p.N || split >= p.nsplit) return;  // outside this problem (uniform)
   const int KT = (p.K + BK - 1) / BK;
-  const int kt0 = blockIdx.z * p.kt_per_split;
+  const int kt0 = split * p.kt_per_split;
   const int kt1 = min(KT, kt0 + p.kt_per_split);
   const bool rowsum = p.rowsumA != nullptr && blockIdx.y == 0;
 
@@ -268,18 +310,21 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     const float* as = sA(cur);
     const float* bs = sB(cur);
 #pragma unroll
-    for (int s = kg * (BK / 4 / KG); s < (kg + 1) * (BK / 4 / KG); ++s) {
-      const int kk = 4 * s + lg;
-      float af[TM], bf[TN];
+    for (int q = kg * (BK / 16 / KG); q < (kg + 1) * (BK / 16 / KG); ++q) {
+      float4 af[TM], bf[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = TA::at(as, (wm * TM + i) * 16 + lr, kk);
+      for (int i = 0; i < TM; ++i) af[i] = TA::frag(as, (wm * TM + i) * 16 + lr, q, lg);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = TB::at(bs, (wn * TN + j) * 16 + lr, kk);
+      for (int j = 0; j < TN; ++j) bf[j] = TB::frag(bs, (wn * TN + j) * 16 + lr, q, lg);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
+        }
     }
     if (rs_on) {
       for (int kk = rs_g; kk < BK; kk += RSG) rs += TA::at(as, rs_m, kk);
@@ -298,7 +343,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
     if (tid < BM) {
       float tot = 0.f;
       for (int g = 0; g < RSG; ++g) tot += red[g * BM + tid];
-      if (m0 + tid < p.M) p.rowsumA[(long long)blockIdx.z * p.M + m0 + tid] = tot;
+      if (m0 + tid < p.M) p.rowsumA[(long long)split * p.M + m0 + tid] = tot;
     }
     __syncthreads();
   }
@@ -326,7 +371,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
           acc[i][j][r] = acc[i][j][r] + xch[(((wave * TM + i) * TN + j) * 4 + r) * 64 + lane];
   }
 
-  float* C = p.C + (long long)blockIdx.z * p.split_stride;
+  float* C = p.C + (long long)split * p.split_stride;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -430,11 +475,116 @@ __device__ __forceinline__ void splitk_reduce_body(const SplitReduceArgs& p) {
   }
 }
 
+// All weight and bias gradients of an update step in one launch
+// (ReduceAllArgs): block b finds its segment, sums its outputs over the
+// segment's slices in the fixed order of splitk_reduce_body (or reads them
+// when the tensor is already final), writes them, and writes the fixed-order
+// sum of their squares to sq_part[b] — the grad-norm partials of the clip,
+// actor segments first.
+__device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
+  __shared__ float4 red[kReduceAllThreads];
+  __shared__ float sqs[kReduceAllThreads];
+  if (a.guard && *a.guard == 0) return;
+  int si = 0;
+  for (int i = 1; i < a.nseg; ++i)
+    if ((int)blockIdx.x >= a.seg[i].blk0) si = i;
+  const ReduceSeg& p = a.seg[si];
+  const int SL = p.lanes;
+  const int QB = kReduceAllThreads / SL;
+  const int t = threadIdx.x;
+  const int e = t % QB, l = t / QB;
+  const int b = (int)blockIdx.x - p.blk0;
+  const long long nq = (p.mn + 3) / 4;
+  const bool matrix = b < p.nqb;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  long long idx;
+  if (matrix) {
+    idx = (long long)b * QB + e;
+    if (idx < nq) {
+      const long long i0 = 4 * idx;
+      if (p.part) {
+        if ((p.mn & 3) == 0) {
+#pragma unroll 4
+          for (int z = l; z < p.splits; z += SL) {
+            const float4 v = *reinterpret_cast<const float4*>(p.part + (long long)z * p.mn + i0);
+            acc.x += v.x;
+            acc.y += v.y;
+            acc.z += v.z;
+            acc.w += v.w;
+          }
+        } else {
+          for (int z = l; z < p.splits; z += SL) {
+            const float* q = p.part + (long long)z * p.mn + i0;
+            acc.x += q[0];
+            if (i0 + 1 < p.mn) acc.y += q[1];
+            if (i0 + 2 < p.mn) acc.z += q[2];
+            if (i0 + 3 < p.mn) acc.w += q[3];
+          }
+        }
+      } else if (l == 0) {
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < 4; ++c) {
+          const long long i = i0 + c;
+          if (i < p.mn) o[c] = p.out[(i / p.cols) * p.ldo + i % p.cols];
+        }
+        acc = make_float4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  } else {
+    idx = (long long)(b - p.nqb) * QB + e;  // row index
+    if (idx < p.rows) {
+      if (p.rowpart) {
+#pragma unroll 4
+        for (int z = l; z < p.splits; z += SL) acc.x += p.rowpart[(long long)z * p.rows + idx];
+      } else if (l == 0) {
+        acc.x = p.rowout[idx];
+      }
+    }
+  }
+  red[t] = acc;
+  __syncthreads();
+  for (int st = SL >> 1; st > 0; st >>= 1) {
+    if (l < st) {
+      const float4 v = red[t + st * QB];
+      float4 x = red[t];
+      x.x += v.x;
+      x.y += v.y;
+      x.z += v.z;
+      x.w += v.w;
+      red[t] = x;
+    }
+    __syncthreads();
+  }
+  float sq = 0.f;
+  if (l == 0) {
+    const float4 v = red[e];
+    if (matrix) {
+      if (idx < nq) {
+        const float o[4] = {v.x, v.y, v.z, v.w};
+        for (int c = 0; c < 4; ++c) {
+          const long long i = 4 * idx + c;
+          if (i < p.mn) {
+            if (p.part) p.out[(i / p.cols) * p.ldo + i % p.cols] = o[c];
+            sq += o[c] * o[c];
+          }
+        }
+      }
+    } else if (idx < p.rows) {
+      if (p.rowpart) p.rowout[idx] = v.x;
+      sq = v.x * v.x;
+    }
+  }
+  const float tot = block_sum<kReduceAllThreads>(sq, sqs);
+  if (t == 0 && a.sq_part) a.sq_part[blockIdx.x] = tot;
+}
+
 }  // namespace zk
 
-#define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, KG, VEC)                              \
-  extern "C" __global__ __launch_bounds__(64 * WM * WN * KG) void NAME(zk::GemmArgs p) { \
-    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, KG, VEC>(p);                              \
+#define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, KG, VEC)                                   \
+  extern "C" __global__ __launch_bounds__(64 * WM * WN * KG) void NAME(zk::GemmBatch b) {      \
+    const int prob = blockIdx.z / b.zper;                                                      \
+    if (prob >= b.count) return;                                                               \
+    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, KG, VEC>(b.g[prob], blockIdx.z % b.zper);       \
   }
 
 // Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous,
@@ -444,6 +594,9 @@ ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22, true, true, 64, 128, 16, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_96x128x16_w24, true, true, 96, 128, 16, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_96x128x32_w22k2, true, true, 96, 128, 32, 2, 2, 2, true)
+ZK_GEMM(zk_gemm_ak_bk_128x128x32_w24, true, true, 128, 128, 32, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_128x128x32_w22, true, true, 128, 128, 32, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_128x128x16_w22, true, true, 128, 128, 16, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_96x32x32_w21, true, true, 96, 32, 32, 2, 1, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, 1, true)
@@ -451,6 +604,9 @@ ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_96x128x16_w24, true, false, 96, 128, 16, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_96x128x32_w22k2, true, false, 96, 128, 32, 2, 2, 2, true)
+ZK_GEMM(zk_gemm_ak_bn_128x128x32_w24, true, false, 128, 128, 32, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bn_128x128x32_w22, true, false, 128, 128, 32, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_ak_bn_128x128x16_w22, true, false, 128, 128, 16, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_am_bn_64x128x16_w22, false, false, 64, 128, 16, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_am_bn_64x128x16_w24, false, false, 64, 128, 16, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, 1, true)
@@ -467,4 +623,8 @@ ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, 1, false)
 
 extern "C" __global__ __launch_bounds__(256) void zk_splitk_reduce(zk::SplitReduceArgs p) {
   zk::splitk_reduce_body(p);
+}
+
+extern "C" __global__ __launch_bounds__(zk::kReduceAllThreads) void zk_reduce_all(zk::ReduceAllArgs a) {
+  zk::reduce_all_body(a);
 }

@@ -136,6 +136,7 @@ __device__ __forceinline__ void narrow_k_body(const GemmArgs& p) {
   if (row0 >= p.M) return;
   const int lr = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.y * (16 * NTK);
+  if (n0 >= p.N) return;  // outside this problem of the batch
   const int m = min(row0 + lr, p.M - 1);
   const long long sr = p.permA ? p.permA[m] : m;
   const float* a = p.A + sr * p.lda;
@@ -206,6 +207,8 @@ __device__ __forceinline__ void narrow_m_body(const GemmArgs& p) {
   __shared__ float red[(kNarrowWaves - 1) * MT * NTC * 4 * 64];
   __shared__ float rsred[kNarrowWaves * MT * 64];
   if (p.guard && *p.guard == 0) return;
+  // Outside this problem of the batch (uniform over the block).
+  if ((int)blockIdx.x >= p.nsplit || (int)blockIdx.y * 16 * NTC >= p.N) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int kb = blockIdx.x * p.kt_per_split;
@@ -313,24 +316,17 @@ __device__ __forceinline__ void narrow_m_body(const GemmArgs& p) {
 
 }  // namespace zk
 
-extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void zk_narrow_n1_v(zk::GemmArgs p) {
-  zk::narrow_n_body<1, true>(p);
-}
-extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void zk_narrow_n2_v(zk::GemmArgs p) {
-  zk::narrow_n_body<2, true>(p);
-}
-extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void zk_narrow_n1_s(zk::GemmArgs p) {
-  zk::narrow_n_body<1, false>(p);
-}
-extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void zk_narrow_n2_s(zk::GemmArgs p) {
-  zk::narrow_n_body<2, false>(p);
-}
-extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void zk_narrow_k(zk::GemmArgs p) {
-  zk::narrow_k_body(p);
-}
-extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void zk_narrow_m1(zk::GemmArgs p) {
-  zk::narrow_m_body<1>(p);
-}
-extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void zk_narrow_m2(zk::GemmArgs p) {
-  zk::narrow_m_body<2>(p);
-}
+// grid.z = problem of the batch (one slice per problem: zper = 1).
+#define ZK_NARROW(NAME, BODY)                                                                 \
+  extern "C" __global__ __launch_bounds__(64 * zk::kNarrowWaves) void NAME(zk::GemmBatch b) { \
+    if ((int)blockIdx.z >= b.count) return;                                                   \
+    BODY(b.g[blockIdx.z]);                                                                    \
+  }
+
+ZK_NARROW(zk_narrow_n1_v, (zk::narrow_n_body<1, true>))
+ZK_NARROW(zk_narrow_n2_v, (zk::narrow_n_body<2, true>))
+ZK_NARROW(zk_narrow_n1_s, (zk::narrow_n_body<1, false>))
+ZK_NARROW(zk_narrow_n2_s, (zk::narrow_n_body<2, false>))
+ZK_NARROW(zk_narrow_k, zk::narrow_k_body)
+ZK_NARROW(zk_narrow_m1, zk::narrow_m_body<1>)
+ZK_NARROW(zk_narrow_m2, zk::narrow_m_body<2>)

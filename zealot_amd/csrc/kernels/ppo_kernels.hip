@@ -15,17 +15,22 @@ namespace zk {
 // to right like the reference's serial loops over action components; every
 // lane gets the result. The log-probabilities reach a few hundred in
 // magnitude, where a different summation order moves the PPO ratio by ~1e-5
-// relative, so the order is kept. All G lane reads are issued before the
-// first add (they are independent), so the chain costs one shuffle latency.
+// relative, so the order is kept. The lane reads are independent, so they
+// are issued 16 at a time ahead of their adds (one shuffle latency per 16
+// components, 16 registers).
 template <int G>
 __device__ __forceinline__ float lanes_sum_ordered(float v, int base, int n) {
-  float t[G];
-#pragma unroll
-  for (int j = 0; j < G; ++j) t[j] = __shfl(v, base + j, 64);
+  constexpr int kBatch = 16;
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < G; ++j)
-    if (j < n) s += t[j];
+  for (int j0 = 0; j0 < G; j0 += kBatch) {
+    float t[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) t[j] = __shfl(v, base + j0 + j, 64);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      if (j0 + j < n) s += t[j];
+  }
   return s;
 }
 
@@ -40,12 +45,12 @@ __device__ __forceinline__ float lanes_sum_ordered(float v, int base, int n) {
 // order either).
 template <int G>
 __device__ void actor_loss_body(const ActorLossArgs& p) {
-  constexpr int kMaxGroups = kThreads / 32;
+  constexpr int kMaxGroups = kLossThreads / 32;
   __shared__ float sh_g[kMaxGroups][64];
   __shared__ float sh_s[kMaxGroups][2];
   if (p.guard && *p.guard == 0) return;
   const int t = threadIdx.x;
-  const int ng = kThreads / G;
+  const int ng = kLossThreads / G;
   const int grp = t / G, k = t % G;
   const int base = (t & 63) - k;  // first lane of this group in the wavefront
   const int A = p.A;
@@ -58,8 +63,8 @@ __device__ void actor_loss_body(const ActorLossArgs& p) {
   float gacc = 0.f, sacc = 0.f, kacc = 0.f;
   const int r0 = blockIdx.x * p.rows_per_block;
   const int r1 = min(p.rows, r0 + p.rows_per_block);
-  // The next row's inputs are loaded before the current row is computed, so
-  // one row's loads are always in flight behind the arithmetic.
+  // A group's rows are taken R at a time with all their loads issued before
+  // the first row is computed (one memory latency per R rows).
   struct In {
     float mu, act, lpo, adv, mo;
   };
@@ -73,38 +78,47 @@ __device__ void actor_loss_body(const ActorLossArgs& p) {
     x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
     return x;
   };
-  int r = r0 + grp;
-  In cur{};
-  if (r < r1) cur = fetch(r);
-  for (; r < r1; r += ng) {
-    In nxt{};
-    if (r + ng < r1) nxt = fetch(r + ng);
-    const float mu = cur.mu, act = cur.act;
-    // ActorCritic::logp, ppo.rs:297-305
-    const float dz = (act - mu) / sd;
-    const float lp = lanes_sum_ordered<G>(on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f, base, A);
-    const float ratio = expf(lp - cur.lpo);
-    const float a = cur.adv;
-    const float surr = fminf(ratio * a, clampf(ratio, lo, hi) * a);
-    const bool clipped = (a >= 0.0f && ratio > hi) || (a < 0.0f && ratio < lo);
-    float gm = 0.f, c = 0.f;
-    if (!clipped) {
-      const float d = act - mu;
-      gm = -(a * ratio * d * inv_var) * p.scale;
-      const float dls = a * ratio * ((d * d) * inv_var - 1.0f);
-      c = -dls * p.scale;
+  // Rows per group whose loads are issued together (two for 64-lane groups,
+  // whose ordered sums already hold 64 shuffled values in registers).
+  constexpr int R = G == 32 ? 4 : 2;
+  for (int rb = r0 + grp; rb < r1; rb += ng * R) {
+    In in[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int r = rb + j * ng;
+      in[j] = r < r1 ? fetch(r) : In{};
     }
-    c += -p.entropy_coef * p.scale;
-    if (on) {
-      p.delta[(long long)r * p.ldd + k] = gm;
-      gacc += c;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int r = rb + j * ng;
+      if (r >= r1) break;
+      const In& cur = in[j];
+      const float mu = cur.mu, act = cur.act;
+      // ActorCritic::logp, ppo.rs:297-305
+      const float dz = (act - mu) / sd;
+      const float lp = lanes_sum_ordered<G>(on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f, base, A);
+      const float ratio = expf(lp - cur.lpo);
+      const float a = cur.adv;
+      const float surr = fminf(ratio * a, clampf(ratio, lo, hi) * a);
+      const bool clipped = (a >= 0.0f && ratio > hi) || (a < 0.0f && ratio < lo);
+      float gm = 0.f, c = 0.f;
+      if (!clipped) {
+        const float d = act - mu;
+        gm = -(a * ratio * d * inv_var) * p.scale;
+        const float dls = a * ratio * ((d * d) * inv_var - 1.0f);
+        c = -dls * p.scale;
+      }
+      c += -p.entropy_coef * p.scale;
+      if (on) {
+        p.delta[(long long)r * p.ldd + k] = gm;
+        gacc += c;
+      }
+      sacc += surr * p.scale;
+      if (p.mean_old) {  // ActorCritic::kl, ppo.rs:327-334
+        const float y = (mu - cur.mo) * inv_sd;
+        kacc += lanes_sum_ordered<G>(on ? 0.5f * (y * y) : 0.f, base, A) * p.scale;
+      }
     }
-    sacc += surr * p.scale;
-    if (p.mean_old) {  // ActorCritic::kl, ppo.rs:327-334
-      const float y = (mu - cur.mo) * inv_sd;
-      kacc += lanes_sum_ordered<G>(on ? 0.5f * (y * y) : 0.f, base, A) * p.scale;
-    }
-    cur = nxt;
   }
   sh_g[grp][k] = gacc;
   if (k == 0) {
@@ -112,15 +126,17 @@ __device__ void actor_loss_body(const ActorLossArgs& p) {
     sh_s[grp][1] = kacc;
   }
   __syncthreads();
+  // Partials component-major ([A][blocks], [2][blocks]) so that each
+  // quantity's partials are contiguous for the reductions that follow.
   if (t < A) {
     float g = 0.f;
     for (int j = 0; j < ng; ++j) g += sh_g[j][t];
-    p.gls_part[(long long)blockIdx.x * A + t] = g;
+    p.gls_part[(long long)t * gridDim.x + blockIdx.x] = g;
   } else if (t == 64 || t == 65) {
     const int q = t - 64;
     float v = 0.f;
     for (int j = 0; j < ng; ++j) v += sh_s[j][q];
-    p.stat_part[blockIdx.x * 2 + q] = v;
+    p.stat_part[(long long)q * gridDim.x + blockIdx.x] = v;
   }
 }
 
@@ -202,33 +218,101 @@ __device__ void sumsq_body(const SumsqArgs& p) {
 // with every scalar kept on the device.
 __device__ void finalize_body(const FinalizeArgs& p) {
   // Quantities 0..4: surrogate, kl, value loss, actor and critic squared
-  // norms; 5..5+A-1: the log_std gradient. Each is one wavefront's
-  // fixed-order sum over its per-block partials.
+  // norms; 5..5+A-1: the log_std gradient, each a sum over per-block
+  // partials. Every quantity's partials are cut into chunks of kChunk terms;
+  // chunk i is summed by wavefront i % 16 (lane-strided, fixed order), and
+  // each quantity then adds its chunk sums in chunk order: a fixed grouping,
+  // so the result is deterministic.
   constexpr int kMaxA = 256;
+  constexpr int kChunk = kFinalizeChunk;
+  constexpr int kMaxChunks = kFinalizeMaxChunks;
   __shared__ float q[5 + kMaxA];
+  __shared__ float cs[kMaxChunks];
   if (p.guard && *p.guard == 0) return;
   const int t = threadIdx.x;
   const int wave = t >> 6, lane = t & 63;
   const int A = p.pp.A;
   const int nq = 5 + A;
-  for (int j = wave; j < nq; j += kFinalizeThreads / 64) {
-    float v;
-    if (j == 0)
-      v = wave_sum_strided(p.astat_part, p.nb_a, 2);
-    else if (j == 1)
-      v = wave_sum_strided(p.astat_part + 1, p.nb_a, 2);
-    else if (j == 2)
-      v = wave_sum_strided(p.vstat_part, p.nb_v, 1);
-    else if (j == 3)
-      v = wave_sum_strided(p.sq_part, p.nsq_a, 1);
-    else if (j == 4)
-      v = wave_sum_strided(p.sq_part + p.nsq_a, p.nsq - p.nsq_a, 1);
-    else
-      v = wave_sum_strided(p.gls_part + (j - 5), p.nb_a, A);
-    if (lane == 0) {
-      q[j] = v;
-      if (j >= 5) p.g_logstd[j - 5] = v;
+  auto range = [&](int j, const float*& ptr, int& n, int& stride) {
+    if (j == 0) {
+      ptr = p.astat_part, n = p.nb_a, stride = 1;
+    } else if (j == 1) {
+      ptr = p.astat_part + p.nb_a, n = p.nb_a, stride = 1;
+    } else if (j == 2) {
+      ptr = p.vstat_part, n = p.nb_v, stride = 1;
+    } else if (j == 3) {
+      ptr = p.sq_part, n = p.nsq_a, stride = 1;
+    } else if (j == 4) {
+      ptr = p.sq_part + p.nsq_a, n = p.nsq - p.nsq_a, stride = 1;
+    } else {
+      ptr = p.gls_part + (long long)(j - 5) * p.nb_a, n = p.nb_a, stride = 1;
     }
+  };
+  int total = 0;
+  for (int j = 0; j < nq; ++j) {
+    const float* ptr;
+    int n, stride;
+    range(j, ptr, n, stride);
+    total += (n + kChunk - 1) / kChunk;
+  }
+  // A wavefront takes its chunks (wave, wave + 16, ...) four at a time and
+  // issues all their loads before adding: one memory latency per four chunks.
+  // Within a chunk lane l adds terms l, l + 64, ... in order.
+  constexpr int kW = kFinalizeThreads / 64, kB = 4, kPer = kChunk / 64;
+  for (int cb = wave; cb < total; cb += kW * kB) {
+    float tv[kB][kPer];
+    int len[kB];
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int ci = cb + kW * b;
+      len[b] = 0;
+      if (ci >= total) continue;
+      int j = 0, first = 0, nch = 0;
+      const float* ptr = nullptr;
+      int n = 0, stride = 1;
+      for (;; ++j) {  // the quantity owning chunk ci (uniform over the wave)
+        range(j, ptr, n, stride);
+        nch = (n + kChunk - 1) / kChunk;
+        if (ci < first + nch) break;
+        first += nch;
+      }
+      const int c0 = (ci - first) * kChunk;
+      len[b] = min(kChunk, n - c0);
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = lane + 64 * u;
+        tv[b][u] = i < len[b] ? ptr[(long long)(c0 + i) * stride] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+      const int ci = cb + kW * b;
+      if (ci >= total) continue;
+      float v = 0.f;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u)
+        if (lane + 64 * u < len[b]) v += tv[b][u];
+      v = wave_sum(v);
+      if (lane == 0) cs[ci] = v;
+    }
+  }
+  __syncthreads();
+  if (t < nq) {
+    int first = 0;
+    for (int j = 0; j < t; ++j) {
+      const float* ptr;
+      int n, stride;
+      range(j, ptr, n, stride);
+      first += (n + kChunk - 1) / kChunk;
+    }
+    const float* ptr;
+    int n, stride;
+    range(t, ptr, n, stride);
+    const int nch = (n + kChunk - 1) / kChunk;
+    float v = 0.f;
+    for (int i = 0; i < nch; ++i) v += cs[first + i];
+    q[t] = v;
+    if (t >= 5) p.g_logstd[t - 5] = v;
   }
   __syncthreads();
   if (wave != 0) return;
@@ -561,12 +645,13 @@ __device__ void clamp_body(const ClampArgs& p) {
 #define ZK_KERNEL(NAME, ARGS, BODY) \
   extern "C" __global__ __launch_bounds__(256) void NAME(zk::ARGS p) { zk::BODY(p); }
 
-// One lane group of 32 (A <= 32) or 64 (A <= 64) lanes per sample.
-extern "C" __global__ __launch_bounds__(256) void zk_actor_loss(zk::ActorLossArgs p) {
-  if (p.group == 32)
-    zk::actor_loss_body<32>(p);
-  else
-    zk::actor_loss_body<64>(p);
+// One lane group of 32 (A <= 32) or 64 (A <= 64) lanes per sample; separate
+// kernels so that the narrow case is not sized for the wide one's registers.
+extern "C" __global__ __launch_bounds__(zk::kLossThreads) void zk_actor_loss(zk::ActorLossArgs p) {
+  zk::actor_loss_body<32>(p);
+}
+extern "C" __global__ __launch_bounds__(zk::kLossThreads) void zk_actor_loss_g64(zk::ActorLossArgs p) {
+  zk::actor_loss_body<64>(p);
 }
 ZK_KERNEL(zk_value_loss, ValueLossArgs, value_loss_body)
 ZK_KERNEL(zk_sumsq, SumsqArgs, sumsq_body)

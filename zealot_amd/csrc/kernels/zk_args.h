@@ -7,8 +7,14 @@
 
 namespace zk {
 
-// Block size of zk_finalize (one wavefront per fixed-order sum, 16 in flight).
+// zk_finalize: one block of 16 wavefronts; every per-block partial sum is cut
+// into chunks of kFinalizeChunk terms, at most kFinalizeMaxChunks in total.
 constexpr int kFinalizeThreads = 1024;
+// Block sizes of zk_actor_loss (32 lane groups) and zk_reduce_all.
+constexpr int kLossThreads = 1024;
+constexpr int kReduceAllThreads = 1024;
+constexpr int kFinalizeChunk = 512;
+constexpr int kFinalizeMaxChunks = 1024;
 
 enum EpiMode : int {
   kEpiStore = 0,    // C = acc
@@ -34,7 +40,19 @@ struct GemmArgs {
   int epi;
   int act;                 // ELU in the bias epilogues
   int vecA, vecB;          // float4 global loads are aligned and in bounds
-  int kt_per_split;        // k-tiles per grid.z slice
+  int kt_per_split;        // k-tiles per split-K slice (narrow weight gradient: rows)
+  int nsplit;              // split-K slices of this problem
+};
+
+// Up to two GEMMs of one kernel variant in one launch (the actor's and the
+// critic's layer of the same shape class). grid.z = count * zper: problem
+// blockIdx.z / zper, split-K slice blockIdx.z % zper; blocks outside a
+// problem's tile grid or slice count return at once.
+constexpr int kMaxGemmBatch = 2;
+struct GemmBatch {
+  GemmArgs g[kMaxGemmBatch];
+  int count;
+  int zper;
 };
 
 struct SplitReduceArgs {
@@ -48,6 +66,30 @@ struct SplitReduceArgs {
   int rows;
   int splits;
   int lanes;  // split lanes per output element: a power of two in [1, 256]
+};
+
+// One output tensor of the all-layer reduction (zk_reduce_all): the fixed-
+// order sum over `splits` dense partial slices (part, rowpart), or, with
+// part == nullptr, a tensor already final in `out` / `rowout` that only
+// contributes its sum of squares. Blocks [blk0, blk0 + nqb) cover the matrix
+// in float4 quads, the next nrb blocks the row sums; `lanes` split lanes per
+// output element (a power of two, 256 / lanes outputs per block).
+struct ReduceSeg {
+  const float* part;
+  const float* rowpart;
+  float* out;
+  float* rowout;
+  long long mn;
+  int cols, ldo, rows, splits, lanes;
+  int blk0, nqb, nrb;
+};
+
+constexpr int kMaxReduceSegs = 16;
+struct ReduceAllArgs {
+  ReduceSeg seg[kMaxReduceSegs];
+  int nseg;
+  float* sq_part;  // per-block sum of squares of the block's final values
+  const int* guard;
 };
 
 // Scalars that live on the device for a whole update so that no kernel needs
@@ -90,8 +132,8 @@ struct ActorLossArgs {
   const float* log_std;   // [A]
   const int* perm;        // sample = perm ? perm[row0 + r] : row0 + r
   float* delta;           // [rows x ldd] dL/dmean
-  float* gls_part;        // [blocks x A] log_std gradient partials
-  float* stat_part;       // [blocks x 2] surrogate, kl partials
+  float* gls_part;        // [A x blocks] log_std gradient partials (component-major)
+  float* stat_part;       // [2 x blocks] surrogate, kl partials
   const int* guard;
   int ldm, ldact, ldmo, ldd;
   int row0, rows, A;
@@ -124,8 +166,8 @@ struct SumsqArgs {
 
 struct FinalizeArgs {
   DevState* st;
-  const float* gls_part;    // [nb_a x A]
-  const float* astat_part;  // [nb_a x 2]
+  const float* gls_part;    // [A x nb_a]
+  const float* astat_part;  // [2 x nb_a]
   const float* vstat_part;  // [nb_v]
   const float* sq_part;     // [nsq]
   const float* log_std;     // [A] (pre-step values)

@@ -32,6 +32,8 @@ enum KernelId : int {
   K_COPY_ROWS,
   K_SAMPLE,
   K_CLAMP,
+  K_REDUCE_ALL,
+  K_ACTOR_LOSS_G64,
   K_GEMM_BASE
 };
 
@@ -71,16 +73,18 @@ inline long long round_up(long long x, long long m) { return (x + m - 1) / m * m
 inline long long cdiv(long long a, long long b) { return (a + b - 1) / b; }
 
 // Launch shape of zk_actor_loss: one lane group (32 lanes for A <= 32, else
-// 64) per sample, kThreads / group samples in flight per block, and at most
+// 64) per sample, kLossThreads / group samples in flight per block, and at most
 // kLossMaxBlocks blocks over the rows (one partial row each).
-constexpr int kLossMaxBlocks = 512;
+constexpr int kLossMaxBlocks = 256;
 struct LossShape {
   int group, rows_per_block, blocks;
+  int kernel;  // K_ACTOR_LOSS (32-lane groups) or K_ACTOR_LOSS_G64
 };
 inline LossShape actor_loss_shape(int rows, int A) {
   LossShape s;
   s.group = A <= 32 ? 32 : 64;
-  const int ng = 256 / s.group;
+  s.kernel = s.group == 32 ? K_ACTOR_LOSS : K_ACTOR_LOSS_G64;
+  const int ng = zk::kLossThreads / s.group;
   s.rows_per_block = (int)std::max<long long>(ng, cdiv(rows, kLossMaxBlocks));
   s.blocks = rows > 0 ? (int)cdiv(rows, s.rows_per_block) : 0;
   return s;
@@ -195,6 +199,7 @@ struct GemmDesc {
   const int* guard = nullptr;
   float* ws = nullptr;          // split-K scratch (floats); nullptr: context scratch
   size_t ws_floats = 0;
+  zk::ReduceSeg* seg_out = nullptr;  // set: no reduce launch, describe it here instead
 };
 
 // Variant choice and split-K decision shared by run_gemm and the scratch
@@ -205,9 +210,19 @@ int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int 
                 bool vec = true);
 size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d);
+// One launch for n (1 or 2) problems that pick the same variant (else n
+// launches); problems that split K over slices need caller scratch when n > 1.
+zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n);
+// Block layout of zk_reduce_all over `segs` (fills lanes / blk0 / nqb / nrb);
+// returns the block count (= number of sum-of-squares partials).
+int reduce_all_layout(zk::ReduceSeg* segs, int nseg);
+zl_status launch_reduce_all(zl_ctx* c, const zk::ReduceSeg* segs, int nseg, float* sq_part,
+                            const int* guard);
 // Fixed-order sum over the split slices (zk_splitk_reduce); picks the split
 // lanes and grid from the shape. `r.lanes` is set here.
 zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r);
 zl_status ensure_ws(zl_ctx* c, size_t floats);
+// out[k] = sum over b of part[k * blocks + b], k < width (zk_row_sum).
+zl_status reduce_rows(zl_ctx* c, const float* part, int width, int blocks, float* out);
 
 }  // namespace zl

@@ -115,41 +115,92 @@ static size_t net_ws_floats(const zl_ctx* c, const NetLayout& nl, int rows) {
   return w;
 }
 
-// Forward of GpuMlp::forward (src/bin/biped_train_gpu.rs:364-422): one fused
-// GEMM + bias + ELU launch per layer, linear last layer (zealot-rl/src/net.rs:88-108).
+// Layer l of GpuMlp::forward (src/bin/biped_train_gpu.rs:364-422): one fused
+// GEMM + bias + ELU, linear last layer (zealot-rl/src/net.rs:88-108).
+static GemmDesc fwd_desc(const NetLayout& nl, const NetBuffers& nb, const float* params,
+                         const float* x, int ldx, const int* permx, int rows, const int* guard,
+                         int l) {
+  GemmDesc d;
+  d.A = l == 0 ? x : nb.act[l];
+  d.lda = l == 0 ? ldx : nb.ld[l];
+  d.a_kc = true;
+  d.permA = l == 0 ? permx : nullptr;
+  d.B = params + nl.w_off[l];
+  d.ldb = nl.ldw[l];
+  d.b_kc = true;
+  d.C = nb.act[l + 1];
+  d.ldc = nb.ld[l + 1];
+  d.M = rows;
+  d.N = nl.dims[l + 1];
+  d.K = nl.dims[l];
+  d.epi = zk::kEpiBiasN;
+  d.bias = params + nl.b_off[l];
+  d.act = l < nl.L - 1 ? 1 : 0;
+  d.guard = guard;
+  return d;
+}
+
+// Weight gradient of layer l (GpuMlp::backward, src/bin/biped_train_gpu.rs:423-500,
+// math of zealot-rl/src/net.rs:113-140): dW = delta^T . a, split-K over the
+// rows with a fixed-order reduction, and the bias gradient as the row sums
+// of delta^T fused in. `dl` is dL/dz of the layer.
+static GemmDesc wgrad_desc(const NetLayout& nl, const NetBuffers& nb, float* grads, const float* x,
+                           int ldx, const int* permx, int rows, const float* dl, int ldd,
+                           const int* guard, int l) {
+  GemmDesc w;
+  w.A = dl;
+  w.lda = ldd;
+  w.a_kc = false;
+  w.B = l == 0 ? x : nb.act[l];
+  w.ldb = l == 0 ? ldx : nb.ld[l];
+  w.b_kc = false;
+  w.permB = l == 0 ? permx : nullptr;
+  w.C = grads + nl.w_off[l];
+  w.ldc = nl.ldw[l];
+  w.M = nl.dims[l + 1];
+  w.N = nl.dims[l];
+  w.K = rows;
+  w.rowsum_out = grads + nl.b_off[l];
+  w.guard = guard;
+  return w;
+}
+
+// Data gradient into layer l-1: delta_{l-1} = (delta_l . W_l) * elu'(a_l),
+// ELU' fused into the GEMM epilogue.
+static GemmDesc dgrad_desc(const NetLayout& nl, const NetBuffers& nb, const float* params, int rows,
+                           const float* dl, int ldd, const int* guard, int l) {
+  GemmDesc d;
+  d.A = dl;
+  d.lda = ldd;
+  d.a_kc = true;
+  d.B = params + nl.w_off[l];
+  d.ldb = nl.ldw[l];
+  d.b_kc = false;
+  d.C = nb.delta[l - 1];
+  d.ldc = nb.ld[l];
+  d.M = rows;
+  d.N = nl.dims[l];
+  d.K = nl.dims[l + 1];
+  d.epi = zk::kEpiEluGrad;
+  d.Y = nb.act[l];
+  d.ldy = nb.ld[l];
+  d.guard = guard;
+  return d;
+}
+
 static zl_status net_forward(zl_ctx* c, const NetLayout& nl, const NetBuffers& nb,
                              const float* params, const float* x, int ldx, const int* permx,
                              int rows, const int* guard) {
   for (int l = 0; l < nl.L; ++l) {
-    GemmDesc d;
-    d.A = l == 0 ? x : nb.act[l];
-    d.lda = l == 0 ? ldx : nb.ld[l];
-    d.a_kc = true;
-    d.permA = l == 0 ? permx : nullptr;
-    d.B = params + nl.w_off[l];
-    d.ldb = nl.ldw[l];
-    d.b_kc = true;
-    d.C = nb.act[l + 1];
-    d.ldc = nb.ld[l + 1];
-    d.M = rows;
-    d.N = nl.dims[l + 1];
-    d.K = nl.dims[l];
-    d.epi = zk::kEpiBiasN;
-    d.bias = params + nl.b_off[l];
-    d.act = l < nl.L - 1 ? 1 : 0;
-    d.guard = guard;
+    const GemmDesc d = fwd_desc(nl, nb, params, x, ldx, permx, rows, guard, l);
     zl_status s = run_gemm(c, d);
     if (s) return s;
   }
   return ZL_OK;
 }
 
-// Backward of GpuMlp::backward (src/bin/biped_train_gpu.rs:423-500) with the
-// math of zealot-rl/src/net.rs:113-140: per layer the weight gradient
-// dW = delta^T . a (split-K over the rows, fixed-order reduction) with the
-// bias gradient as the row sums of delta^T fused in, then (l > 0) the data
-// gradient delta_{l-1} = (delta_l . W_l) * elu'(a_l) with ELU' fused into the
-// GEMM epilogue. `top` is dL/dz of the output layer.
+// Backward with each weight gradient reduced right after its GEMM. `top` is
+// dL/dz of the output layer.
 static zl_status net_backward(zl_ctx* c, const NetLayout& nl, const NetBuffers& nb,
                               const float* params, float* grads, const float* x, int ldx,
                               const int* permx, int rows, const float* top, int ld_top,
@@ -157,45 +208,105 @@ static zl_status net_backward(zl_ctx* c, const NetLayout& nl, const NetBuffers& 
   for (int l = nl.L - 1; l >= 0; --l) {
     const float* dl = l == nl.L - 1 ? top : nb.delta[l];
     const int ldd = l == nl.L - 1 ? ld_top : nb.ld[l + 1];
-    GemmDesc w;
-    w.A = dl;
-    w.lda = ldd;
-    w.a_kc = false;
-    w.B = l == 0 ? x : nb.act[l];
-    w.ldb = l == 0 ? ldx : nb.ld[l];
-    w.b_kc = false;
-    w.permB = l == 0 ? permx : nullptr;
-    w.C = grads + nl.w_off[l];
-    w.ldc = nl.ldw[l];
-    w.M = nl.dims[l + 1];
-    w.N = nl.dims[l];
-    w.K = rows;
-    w.rowsum_out = grads + nl.b_off[l];
-    w.guard = guard;
+    GemmDesc w = wgrad_desc(nl, nb, grads, x, ldx, permx, rows, dl, ldd, guard, l);
     w.ws = ws;
     w.ws_floats = ws_floats;
     zl_status s = run_gemm(c, w);
     if (s) return s;
     if (l > 0) {
-      GemmDesc d;
-      d.A = dl;
-      d.lda = ldd;
-      d.a_kc = true;
-      d.B = params + nl.w_off[l];
-      d.ldb = nl.ldw[l];
-      d.b_kc = false;
-      d.C = nb.delta[l - 1];
-      d.ldc = nb.ld[l];
-      d.M = rows;
-      d.N = nl.dims[l];
-      d.K = nl.dims[l + 1];
-      d.epi = zk::kEpiEluGrad;
-      d.Y = nb.act[l];
-      d.ldy = nb.ld[l];
-      d.guard = guard;
-      s = run_gemm(c, d);
+      s = run_gemm(c, dgrad_desc(nl, nb, params, rows, dl, ldd, guard, l));
       if (s) return s;
     }
+  }
+  return ZL_OK;
+}
+
+// One net's operands in a paired actor + critic pass.
+struct NetView {
+  const NetLayout* nl;
+  const NetBuffers* nb;
+  const float* x;  // layer-0 input rows
+  int ldx;
+};
+
+// Forward of both nets, layer by layer, each layer's two GEMMs in one launch
+// when the nets have the same depth (otherwise one after the other).
+static zl_status pair_forward(zl_ctx* c, const NetView v[2], const float* params,
+                              const int* permx, int rows, const int* guard) {
+  if (v[0].nl->L != v[1].nl->L) {
+    for (int i = 0; i < 2; ++i) {
+      zl_status s = net_forward(c, *v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard);
+      if (s) return s;
+    }
+    return ZL_OK;
+  }
+  for (int l = 0; l < v[0].nl->L; ++l) {
+    GemmDesc d[2];
+    for (int i = 0; i < 2; ++i)
+      d[i] = fwd_desc(*v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard, l);
+    zl_status s = run_gemm_batch(c, d, 2);
+    if (s) return s;
+  }
+  return ZL_OK;
+}
+
+// Split-K partial regions of every weight gradient of a paired backward
+// (they stay alive until the all-layer reduction): region [net][layer] at
+// base + off, `size` floats.
+struct PartialPlan {
+  std::vector<size_t> off[2], size[2];
+  size_t total = 0;
+  void build(const zl_ctx* c, const NetLayout* nl[2], int rows) {
+    total = 0;
+    for (int i = 0; i < 2; ++i) {
+      off[i].assign(nl[i]->L, 0);
+      size[i].assign(nl[i]->L, 0);
+      for (int l = 0; l < nl[i]->L; ++l) {
+        off[i][l] = total;
+        size[i][l] = gemm_ws_floats(c, nl[i]->dims[l + 1], nl[i]->dims[l], rows, false, false,
+                                    zk::kEpiStore);
+        total += round_up((long long)size[i][l], 64);
+      }
+    }
+  }
+};
+
+// Backward of both nets with deferred reductions: each layer's weight-gradient
+// GEMMs (and data-gradient GEMMs) of the two nets in one launch; the split-K
+// reduction of every weight gradient is described in segs[net * L_actor +
+// layer] (actor first) for one zk_reduce_all launch afterwards.
+static zl_status pair_backward(zl_ctx* c, const NetView v[2], const float* params, float* grads,
+                               const int* permx, int rows, const float* const top[2],
+                               const int ld_top[2], const int* guard, float* pws,
+                               const PartialPlan& pp, zk::ReduceSeg* segs) {
+  const int L[2] = {v[0].nl->L, v[1].nl->L};
+  const bool paired = L[0] == L[1];
+  for (int depth = 0; depth < std::max(L[0], L[1]); ++depth) {
+    GemmDesc w[2], d[2];
+    int nw = 0, nd = 0;
+    for (int i = 0; i < 2; ++i) {
+      const int l = L[i] - 1 - depth;
+      if (l < 0) continue;
+      const NetLayout& nl = *v[i].nl;
+      const NetBuffers& nb = *v[i].nb;
+      const float* dl = l == nl.L - 1 ? top[i] : nb.delta[l];
+      const int ldd = l == nl.L - 1 ? ld_top[i] : nb.ld[l + 1];
+      GemmDesc& q = w[nw++];
+      q = wgrad_desc(nl, nb, grads, v[i].x, v[i].ldx, permx, rows, dl, ldd, guard, l);
+      q.ws = pws + pp.off[i][l];
+      q.ws_floats = pp.size[i][l];
+      q.seg_out = &segs[i * L[0] + l];
+      if (l > 0) d[nd++] = dgrad_desc(nl, nb, params, rows, dl, ldd, guard, l);
+    }
+    zl_status s = ZL_OK;
+    if (paired) {
+      s = run_gemm_batch(c, w, nw);
+      if (!s && nd) s = run_gemm_batch(c, d, nd);
+    } else {
+      for (int j = 0; j < nw && !s; ++j) s = run_gemm_batch(c, &w[j], 1);
+      for (int j = 0; j < nd && !s; ++j) s = run_gemm_batch(c, &d[j], 1);
+    }
+    if (s) return s;
   }
   return ZL_OK;
 }
@@ -382,18 +493,21 @@ struct zl_ppo {
   float *params = nullptr, *grads = nullptr, *m = nullptr, *v = nullptr;
   NetBuffers ab, cb;
   int mb_cap = 0;
-  float* ws = nullptr;
-  size_t ws_floats = 0;
   // Reduction partials.
   float* gls_part = nullptr;  // [nb x A]
   float* astat_part = nullptr;
   float* vstat_part = nullptr;
-  float* sq_part = nullptr;
+  float* sq_part = nullptr;  // grad-norm partials, one per zk_reduce_all block
+  int sq_cap = 0;
   float* kl_part = nullptr;
   float* adv_part = nullptr;
-  int nb_cap = 0, nsq_a = 0, nsq = 0;
-  static constexpr int kSqChunk = 1024;  // one float4 per thread
+  int nb_cap = 0;
   static constexpr int kAdvChunk = 4096;
+  // Split-K partials of every weight gradient of a minibatch step, alive
+  // until the all-layer reduction (regions laid out for `pplan_rows` rows).
+  float* pws = nullptr;
+  size_t pws_cap = 0;
+  PartialPlan pplan;
   size_t adv_part_cap = 0;
   zk::DevState* dstate = nullptr;
   float* ls_old = nullptr;
@@ -423,6 +537,39 @@ zl_status grow(zl_ctx* c, void** p, size_t* cap, size_t bytes) {
   ZL_HIP(c, hipMalloc(p, bytes));
   *cap = bytes;
   return ZL_OK;
+}
+
+// Lay out the weight-gradient partial regions for minibatches of `rows` rows
+// and grow their buffer (outside graph capture: may synchronize).
+zl_status ensure_partials(zl_ppo* p, int rows) {
+  const NetLayout* nls[2] = {&p->actor, &p->critic};
+  p->pplan.build(p->c, nls, rows);
+  size_t cap = p->pws_cap * 4;
+  zl_status s = grow(p->c, (void**)&p->pws, &cap, p->pplan.total * 4 + 4);
+  p->pws_cap = cap / 4;
+  return s;
+}
+
+// Backward of both nets for one minibatch plus the all-layer reduction with
+// the grad-norm partials; nsq / nsq_a receive the partial counts (all, actor).
+zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, int rows,
+                              const int* guard, int* nsq, int* nsq_a) {
+  zl_ctx* c = p->c;
+  const int La = p->actor.L, Lc = p->critic.L;
+  const float* top[2] = {p->ab.delta[La - 1], p->cb.delta[Lc - 1]};
+  const int ldt[2] = {p->ab.ld[La], p->cb.ld[Lc]};
+  zk::ReduceSeg segs[zk::kMaxReduceSegs];
+  zl_status s = pair_backward(c, v, p->params, p->grads, permx, rows, top, ldt, guard, p->pws,
+                              p->pplan, segs);
+  if (s) return s;
+  zk::ReduceSeg lay[zk::kMaxReduceSegs];
+  std::copy(segs, segs + La + Lc, lay);
+  const int blocks = reduce_all_layout(lay, La + Lc);
+  if (blocks > p->sq_cap)
+    return fail(c, ZL_ERR_INVALID, "grad-norm partials: %d blocks > capacity %d", blocks, p->sq_cap);
+  *nsq = blocks;
+  *nsq_a = lay[La].blk0;
+  return launch_reduce_all(c, segs, La + Lc, p->sq_part, guard);
 }
 
 struct Plan {
@@ -472,9 +619,8 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       const int* px = perm_e ? perm_e + row0 : nullptr;
       const float* xa = perm_e ? pl.X : pl.X + (size_t)row0 * pl.ldx;
       const float* xc = perm_e ? pl.XC : pl.XC + (size_t)row0 * pl.ldxc;
-      if ((s = net_forward(c, p->actor, p->ab, p->params, xa, pl.ldx, px, pl.mb, guard))) return s;
-      if ((s = net_forward(c, p->critic, p->cb, p->params, xc, pl.ldxc, px, pl.mb, guard)))
-        return s;
+      const NetView v[2] = {{&p->actor, &p->ab, xa, pl.ldx}, {&p->critic, &p->cb, xc, pl.ldxc}};
+      if ((s = pair_forward(c, v, p->params, px, pl.mb, guard))) return s;
       zk::ActorLossArgs al{};
       al.mean = p->ab.act[La];
       al.ldm = p->ab.ld[La];
@@ -499,7 +645,8 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       al.scale = pl.pp.scale;
       al.rows_per_block = ls_shape.rows_per_block;
       al.group = ls_shape.group;
-      if ((s = launch(c, K_ACTOR_LOSS, (unsigned)ls_shape.blocks, 1, 1, al))) return s;
+      if ((s = launch(c, ls_shape.kernel, (unsigned)ls_shape.blocks, 1, 1, al, 0, zk::kLossThreads)))
+        return s;
       zk::ValueLossArgs vl{};
       vl.v = p->cb.act[Lc];
       vl.ldv = p->cb.ld[Lc];
@@ -516,23 +663,15 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       vl.value_coef = cfg->value_coef;
       vl.scale = pl.pp.scale;
       if ((s = launch(c, K_VALUE_LOSS, (unsigned)nb, 1, 1, vl))) return s;
-      if ((s = net_backward(c, p->actor, p->ab, p->params, p->grads, xa, pl.ldx, px, pl.mb,
-                            p->ab.delta[La - 1], p->ab.ld[La], guard, p->ws, p->ws_floats)))
-        return s;
-      if ((s = net_backward(c, p->critic, p->cb, p->params, p->grads, xc, pl.ldxc, px, pl.mb,
-                            p->cb.delta[Lc - 1], p->cb.ld[Lc], guard, p->ws, p->ws_floats)))
-        return s;
-      zk::SumsqArgs sq{};
-      sq.x = p->grads;
-      sq.part = p->sq_part;
-      sq.guard = guard;
-      sq.off0 = p->actor.begin;
-      sq.len0 = p->actor.end - p->actor.begin;
-      sq.off1 = p->critic.begin;
-      sq.len1 = p->critic.end - p->critic.begin;
-      sq.blocks0 = p->nsq_a;
-      sq.chunk = zl_ppo::kSqChunk;
-      if ((s = launch(c, K_SUMSQ, (unsigned)p->nsq, 1, 1, sq))) return s;
+      int nsq = 0, nsq_a = 0;
+      if ((s = backward_and_reduce(p, v, px, pl.mb, guard, &nsq, &nsq_a))) return s;
+      {
+        auto ch = [](long long n) { return cdiv(n, zk::kFinalizeChunk); };
+        const long long chunks = (2 + A) * ch(ls_shape.blocks) + ch(nb) + ch(nsq_a) + ch(nsq - nsq_a);
+        if (chunks > zk::kFinalizeMaxChunks)
+          return fail(c, ZL_ERR_INVALID, "finalize: %lld partial chunks > %d", chunks,
+                      zk::kFinalizeMaxChunks);
+      }
       zk::FinalizeArgs fz{};
       fz.st = p->dstate;
       fz.gls_part = p->gls_part;
@@ -545,8 +684,8 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       fz.pp = pl.pp;
       fz.nb_a = ls_shape.blocks;
       fz.nb_v = nb;
-      fz.nsq = p->nsq;
-      fz.nsq_a = p->nsq_a;
+      fz.nsq = nsq;
+      fz.nsq_a = nsq_a;
       if ((s = launch(c, K_FINALIZE, 1, 1, 1, fz, 0, zk::kFinalizeThreads))) return s;
       zk::AdamArgs ad{};
       ad.p = p->params;
@@ -617,6 +756,9 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
     return fail(c, ZL_ERR_INVALID, "zl_ppo_create: critic must output a scalar");  // ppo.rs:242-246
   if (adims[na - 1] > 48)
     return fail(c, ZL_ERR_INVALID, "zl_ppo_create: action dim %d > 48", adims[na - 1]);
+  if ((na - 1) + (nc - 1) > zk::kMaxReduceSegs)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_create: more than %d layers in actor + critic",
+                zk::kMaxReduceSegs);
   zl_ppo* p = new zl_ppo();
   p->c = c;
   p->actor.build(adims, na, 0);
@@ -639,16 +781,20 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
   dalloc((void**)&p->v, bytes);
   if (!s) s = p->ab.alloc(c, p->actor, mb);
   if (!s) s = p->cb.alloc(c, p->critic, mb);
-  p->ws_floats = std::max<size_t>(std::max(net_ws_floats(c, p->actor, mb), net_ws_floats(c, p->critic, mb)), 1);
-  dalloc((void**)&p->ws, p->ws_floats * 4);
   p->nb_cap = (int)std::max<long long>(cdiv(mb, kThreads), kLossMaxBlocks);
   dalloc((void**)&p->gls_part, (size_t)p->nb_cap * p->A * 4);
   dalloc((void**)&p->astat_part, (size_t)p->nb_cap * 2 * 4);
   dalloc((void**)&p->vstat_part, (size_t)p->nb_cap * 4);
   dalloc((void**)&p->kl_part, (size_t)p->nb_cap * 4);
-  p->nsq_a = (int)cdiv(p->actor.end - p->actor.begin, zl_ppo::kSqChunk);
-  p->nsq = p->nsq_a + (int)cdiv(p->critic.end - p->critic.begin, zl_ppo::kSqChunk);
-  dalloc((void**)&p->sq_part, (size_t)p->nsq * 4);
+  // zk_reduce_all takes at least kReduceAllThreads / 64 outputs per block
+  // (at most 64 split lanes).
+  p->sq_cap = 0;
+  const int min_per_block = zk::kReduceAllThreads / 64;
+  for (const NetLayout* nl : {&p->actor, &p->critic})
+    for (int l = 0; l < nl->L; ++l)
+      p->sq_cap += (int)(cdiv(cdiv((long long)nl->dims[l + 1] * nl->dims[l], 4), min_per_block) +
+                         cdiv(nl->dims[l + 1], min_per_block));
+  dalloc((void**)&p->sq_part, (size_t)p->sq_cap * 4);
   dalloc((void**)&p->dstate, sizeof(zk::DevState));
   dalloc((void**)&p->ls_old, (size_t)p->A * 4);
   dalloc((void**)&p->stat_out, 8 * 4);
@@ -670,11 +816,11 @@ void zl_ppo_destroy(zl_ppo* p) {
   if (p->gexec) hipGraphExecDestroy(p->gexec);
   p->ab.release();
   p->cb.release();
-  for (void* b : {(void*)p->params, (void*)p->grads, (void*)p->m, (void*)p->v, (void*)p->ws,
+  for (void* b : {(void*)p->params, (void*)p->grads, (void*)p->m, (void*)p->v,
                   (void*)p->gls_part, (void*)p->astat_part, (void*)p->vstat_part,
                   (void*)p->kl_part, (void*)p->sq_part, (void*)p->adv_part, (void*)p->dstate,
                   (void*)p->ls_old, (void*)p->obs_pad, (void*)p->cobs_pad, (void*)p->perm,
-                  (void*)p->stat_out})
+                  (void*)p->stat_out, (void*)p->pws})
     if (b) hipFree(b);
   delete p;
 }
@@ -807,6 +953,7 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
     size_t need = (size_t)2 * cdiv(pl.n, zl_ppo::kAdvChunk) * 4;
     if ((s = grow(c, (void**)&p->adv_part, &p->adv_part_cap, need))) return s;
   }
+  if ((s = ensure_partials(p, pl.mb))) return s;
   if (pl.shuffle) {
     size_t cap = p->perm_cap * 4;
     if ((s = grow(c, (void**)&p->perm, &cap, (size_t)pl.epochs * pl.n * 4 + 4))) return s;
@@ -849,7 +996,7 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
   char key[1024];
   snprintf(key, sizeof(key),
            "%d|%lld|%d|%d|%d|%p|%d|%p|%d|%p|%d|%p|%d|%p|%p|%p|%p|%d%d%d|%a|%a|%a|%a|%a|%a|%a|%d|%d|"
-           "%d|%d|%d|%p|%p",
+           "%d|%d|%d|%p|%p|%p",
            mode, pl.n, pl.mb, pl.n_mb, pl.epochs, (const void*)b->obs, b->ld_obs,
            (const void*)b->critic_obs, b->ld_critic_obs, (const void*)b->action, b->ld_action,
            (const void*)b->mean_old, b->ld_mean_old, (const void*)b->logp_old,
@@ -858,7 +1005,7 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
            (double)cfg->value_coef, (double)cfg->max_grad_norm, (double)cfg->desired_kl,
            (double)cfg->lr_min, (double)cfg->lr_max, cfg->adaptive_lr, cfg->early_stop,
            cfg->normalize_adv, cfg->clamp_log_std, cfg->shuffle, (void*)p->obs_pad,
-           (void*)p->perm);
+           (void*)p->perm, (void*)p->pws);
   const bool eager = c->timing_kernel != -1;
   if (!eager && (!p->gexec || p->gkey != key)) {
     if (p->gexec) {
@@ -970,10 +1117,9 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
     return s;
   const int La = p->actor.L, Lc = p->critic.L, A = p->A;
   const int nb = (int)cdiv(rows, kThreads);
-  if ((s = net_forward(c, p->actor, p->ab, p->params, p->obs_pad, odp, nullptr, rows, nullptr)))
-    return s;
-  if ((s = net_forward(c, p->critic, p->cb, p->params, p->cobs_pad, cdp, nullptr, rows, nullptr)))
-    return s;
+  if ((s = ensure_partials(p, rows))) return s;
+  const NetView v[2] = {{&p->actor, &p->ab, p->obs_pad, odp}, {&p->critic, &p->cb, p->cobs_pad, cdp}};
+  if ((s = pair_forward(c, v, p->params, nullptr, rows, nullptr))) return s;
   const float scale = 1.0f / (float)rows;
   zk::ActorLossArgs al{};
   al.mean = p->ab.act[La];
@@ -999,7 +1145,7 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
   const LossShape lsh = actor_loss_shape(rows, A);
   al.rows_per_block = lsh.rows_per_block;
   al.group = lsh.group;
-  if ((s = launch(c, K_ACTOR_LOSS, (unsigned)lsh.blocks, 1, 1, al))) return s;
+  if ((s = launch(c, lsh.kernel, (unsigned)lsh.blocks, 1, 1, al, 0, zk::kLossThreads))) return s;
   zk::ValueLossArgs vl{};
   vl.v = p->cb.act[Lc];
   vl.ldv = p->cb.ld[Lc];
@@ -1015,12 +1161,8 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
   vl.value_coef = cfg->value_coef;
   vl.scale = scale;
   if ((s = launch(c, K_VALUE_LOSS, (unsigned)nb, 1, 1, vl))) return s;
-  if ((s = net_backward(c, p->actor, p->ab, p->params, p->grads, p->obs_pad, odp, nullptr, rows,
-                        p->ab.delta[La - 1], p->ab.ld[La], nullptr, p->ws, p->ws_floats)))
-    return s;
-  if ((s = net_backward(c, p->critic, p->cb, p->params, p->grads, p->cobs_pad, cdp, nullptr, rows,
-                        p->cb.delta[Lc - 1], p->cb.ld[Lc], nullptr, p->ws, p->ws_floats)))
-    return s;
+  int nsq = 0, nsq_a = 0;
+  if ((s = backward_and_reduce(p, v, nullptr, rows, nullptr, &nsq, &nsq_a))) return s;
   // Fixed-order sums of the per-block partials.
   auto reduce = [&](const float* part, int width, int parts, float* out) {
     zk::SplitReduceArgs r{};
@@ -1032,8 +1174,8 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
     r.splits = parts;
     return launch_splitk_reduce(c, r);
   };
-  if ((s = reduce(p->gls_part, A, lsh.blocks, p->grads + p->ls_off))) return s;
-  if ((s = reduce(p->astat_part, 2, lsh.blocks, p->stat_out))) return s;
+  if ((s = reduce_rows(c, p->gls_part, A, lsh.blocks, p->grads + p->ls_off))) return s;
+  if ((s = reduce_rows(c, p->astat_part, 2, lsh.blocks, p->stat_out))) return s;
   if ((s = reduce(p->vstat_part, 1, nb, p->stat_out + 2))) return s;
   float h[3];
   ZL_HIP(c, hipMemcpyAsync(h, p->stat_out, sizeof(h), hipMemcpyDeviceToHost, c->stream));

@@ -18,7 +18,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_splitk_reduce", "zk_actor_loss",  "zk_value_loss", "zk_sumsq",       "zk_finalize",
     "zk_adam",          "zk_epoch_begin", "zk_kl",         "zk_epoch_end",   "zk_gae",
     "zk_adv_norm",      "zk_elu_backward", "zk_row_sum",   "zk_copy_rows",   "zk_sample",
-    "zk_clamp",
+    "zk_clamp",         "zk_reduce_all",  "zk_actor_loss_g64",
 };
 
 // {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
@@ -27,6 +27,9 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bk_96x128x32_w24", true, true, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bk_96x128x16_w24", true, true, 96, 128, 16, 512, true},
     {"zk_gemm_ak_bk_96x128x32_w22k2", true, true, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bk_128x128x32_w24", true, true, 128, 128, 32, 512, true},
+    {"zk_gemm_ak_bk_128x128x32_w22", true, true, 128, 128, 32, 256, true},
+    {"zk_gemm_ak_bk_128x128x16_w22", true, true, 128, 128, 16, 256, true},
     {"zk_gemm_ak_bk_128x32x16_w41", true, true, 128, 32, 16, 256, true},
     {"zk_gemm_ak_bk_96x32x32_w21", true, true, 96, 32, 32, 128, true},
     {"zk_gemm_ak_bk_256x16x16_w41", true, true, 256, 16, 16, 256, true},
@@ -34,6 +37,9 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x16_w24", true, false, 96, 128, 16, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w22k2", true, false, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bn_128x128x32_w24", true, false, 128, 128, 32, 512, true},
+    {"zk_gemm_ak_bn_128x128x32_w22", true, false, 128, 128, 32, 256, true},
+    {"zk_gemm_ak_bn_128x128x16_w22", true, false, 128, 128, 16, 256, true},
     {"zk_gemm_am_bn_64x128x16_w22", false, false, 64, 128, 16, 256, true},
     {"zk_gemm_am_bn_64x128x16_w24", false, false, 64, 128, 16, 512, true},
     {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512, true},
@@ -222,10 +228,10 @@ size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc
   return (size_t)s * M * N + (size_t)s * M;
 }
 
+static int reduce_lanes(int splits);
+
 zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r) {
-  // Enough split lanes that each thread adds at most ~8 slices.
-  int sl = 1;
-  while (sl < 64 && sl * 8 < r.splits) sl <<= 1;
+  const int sl = reduce_lanes(r.splits);
   r.lanes = sl;
   const int per_block = kThreads / sl;
   const long long nqb = cdiv(cdiv(r.mn, 4), per_block);
@@ -233,103 +239,229 @@ zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r) {
   return launch(c, K_SPLITK_REDUCE, (unsigned)(nqb + nrb), 1, 1, r);
 }
 
-zl_status run_gemm(zl_ctx* c, const GemmDesc& d) {
-  if (d.M <= 0 || d.N <= 0) return ZL_OK;
+// Variant, split-K slicing and tile grid of one GEMM problem.
+struct GemmPlan {
+  int kid = -1;
+  bool vec = false;
+  int splits = 1, per = 0;
+  unsigned gx = 0, gy = 0;
+};
+
+static zl_status plan_gemm(zl_ctx* c, const GemmDesc& d, GemmPlan& P) {
   // float4 row loads need 16-byte aligned rows that cover the padded extent.
   const int a_ext = d.a_kc ? d.K : d.M;
   const int b_ext = d.b_kc ? d.K : d.N;
-  const bool vec = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4) &&
-                   aligned16(d.B) && d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
-  const int kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc, vec);
-  if (kid < 0) return fail(c, ZL_ERR_INVALID, "no GEMM variant for this layout");
-  const GemmKernel& g = kGemmTable[kid - K_GEMM_BASE];
-  if (g.a_kc != d.a_kc || g.b_kc != d.b_kc || (g.vec && !vec))
+  P.vec = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4) && aligned16(d.B) &&
+          d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
+  P.kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc, P.vec);
+  if (P.kid < 0) return fail(c, ZL_ERR_INVALID, "no GEMM variant for this layout");
+  const GemmKernel& g = kGemmTable[P.kid - K_GEMM_BASE];
+  if (g.a_kc != d.a_kc || g.b_kc != d.b_kc || (g.vec && !P.vec))
     return fail(c, ZL_ERR_INVALID, "GEMM variant %s does not match the operand layout", g.name);
-  int splits, per;
-  unsigned gx, gy;
   if (g.kind == G_NARROW_N || g.kind == G_NARROW_K) {
-    splits = 1;
-    per = 0;
-    gx = (unsigned)cdiv(d.M, kNarrowRows);
-    gy = g.kind == G_NARROW_K ? (unsigned)cdiv(d.N, kNarrowKCols) : 1u;
+    P.splits = 1;
+    P.per = 0;
+    P.gx = (unsigned)cdiv(d.M, kNarrowRows);
+    P.gy = g.kind == G_NARROW_K ? (unsigned)cdiv(d.N, kNarrowKCols) : 1u;
   } else if (g.kind == G_NARROW_M) {
-    per = narrow_rows_per_slice(c, d.N, d.K, d.epi);
-    splits = (int)cdiv(std::max(d.K, 1), per);
-    gx = (unsigned)splits;
-    gy = (unsigned)cdiv(d.N, kNarrowCols);
+    P.per = narrow_rows_per_slice(c, d.N, d.K, d.epi);
+    P.splits = (int)cdiv(std::max(d.K, 1), P.per);
+    P.gx = (unsigned)P.splits;
+    P.gy = (unsigned)cdiv(d.N, kNarrowCols);
   } else {
-    splits = d.splits > 0 ? d.splits : gemm_splits(c, d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi, vec);
+    int splits = d.splits > 0 ? d.splits : gemm_splits(c, d.M, d.N, d.K, d.a_kc, d.b_kc, d.epi, P.vec);
     if (d.epi != zk::kEpiStore) splits = 1;
     const long long kt = cdiv(std::max(d.K, 0), g.bk);
-    per = (int)std::max<long long>(1, cdiv(kt, splits));
-    splits = (int)std::max<long long>(1, cdiv(kt, per));
-    gx = (unsigned)cdiv(d.M, g.bm);
-    gy = (unsigned)cdiv(d.N, g.bn);
+    P.per = (int)std::max<long long>(1, cdiv(kt, splits));
+    P.splits = (int)std::max<long long>(1, cdiv(kt, P.per));
+    P.gx = (unsigned)cdiv(d.M, g.bm);
+    P.gy = (unsigned)cdiv(d.N, g.bn);
   }
+  return ZL_OK;
+}
 
-  zk::GemmArgs a{};
-  a.A = d.A;
-  a.B = d.B;
-  a.bias = d.bias;
-  a.Y = d.Y;
-  a.permA = d.permA;
-  a.permB = d.permB;
-  a.guard = d.guard;
-  a.M = d.M;
-  a.N = d.N;
-  a.K = d.K;
-  a.lda = d.lda;
-  a.ldb = d.ldb;
-  a.ldy = d.ldy;
-  a.bias_stride = d.bias_stride;
-  a.epi = d.epi;
-  a.act = d.act;
-  a.kt_per_split = per;
-  a.vecA = vec;
-  a.vecB = vec;
-
-  const double flops = 2.0 * d.M * d.N * (double)d.K;
-  if (splits == 1) {
-    a.C = d.C;
-    a.ldc = d.ldc;
-    a.split_stride = 0;
-    a.rowsumA = d.rowsum_out;
-    c->pending_flops = flops;
-    c->pending_shape = {d.M, d.N, d.K, 1};
-    return launch(c, kid, gx, gy, 1, a, 0, (unsigned)g.threads);
-  }
-  const size_t mn = (size_t)d.M * d.N;
-  const size_t need = (size_t)splits * mn + (d.rowsum_out ? (size_t)splits * d.M : 0);
-  float* ws = d.ws;
-  if (!ws) {
-    zl_status s = ensure_ws(c, need);
+zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
+  // Problems with an empty output do nothing; a pair whose members pick
+  // different variants runs as two launches.
+  const GemmDesc* live[zk::kMaxGemmBatch];
+  int nl = 0;
+  for (int i = 0; i < n; ++i)
+    if (d[i].M > 0 && d[i].N > 0) live[nl++] = &d[i];
+  if (nl == 0) return ZL_OK;
+  if (nl > zk::kMaxGemmBatch) return fail(c, ZL_ERR_INVALID, "GEMM batch of %d problems", nl);
+  GemmPlan P[zk::kMaxGemmBatch];
+  for (int i = 0; i < nl; ++i) {
+    zl_status s = plan_gemm(c, *live[i], P[i]);
     if (s) return s;
-    ws = c->ws;
-  } else if (need > d.ws_floats) {
-    return fail(c, ZL_ERR_INVALID, "split-K scratch too small (%zu < %zu floats)", d.ws_floats,
-                need);
   }
-  a.C = ws;
-  a.ldc = d.N;
-  a.split_stride = (long long)mn;
-  a.rowsumA = d.rowsum_out ? ws + (size_t)splits * mn : nullptr;
+  if (nl == 2 && P[0].kid != P[1].kid) {
+    // Two narrow problems of one family that differ only in the template
+    // width (16 vs 32 columns / rows, float4 vs element loads) share the
+    // variant that serves both: the wider, element loads unless both can
+    // use float4.
+    const GemmKernel& g0 = kGemmTable[P[0].kid - K_GEMM_BASE];
+    const GemmKernel& g1 = kGemmTable[P[1].kid - K_GEMM_BASE];
+    int shared = -1;
+    if (g0.kind == G_NARROW_N && g1.kind == G_NARROW_N) {
+      const bool wide = live[0]->N > 16 || live[1]->N > 16;
+      const bool v = g0.vec && g1.vec;
+      shared = gemm_id(wide ? (v ? "zk_narrow_n2_v" : "zk_narrow_n2_s") : (v ? "zk_narrow_n1_v" : "zk_narrow_n1_s"));
+    } else if (g0.kind == G_NARROW_M && g1.kind == G_NARROW_M) {
+      shared = gemm_id(live[0]->M > 16 || live[1]->M > 16 ? "zk_narrow_m2" : "zk_narrow_m1");
+    }
+    if (shared >= 0) {
+      P[0].kid = P[1].kid = shared;
+    } else {
+      zl_status s = run_gemm_batch(c, live[0], 1);
+      return s ? s : run_gemm_batch(c, live[1], 1);
+    }
+  }
+  const GemmKernel& g = kGemmTable[P[0].kid - K_GEMM_BASE];
+  zk::GemmBatch B{};
+  B.count = nl;
+  B.zper = 1;
+  unsigned gx = 0, gy = 0;
+  double flops = 0.0;
+  float* part[zk::kMaxGemmBatch] = {nullptr, nullptr};
+  for (int i = 0; i < nl; ++i) {
+    const GemmDesc& q = *live[i];
+    zk::GemmArgs& a = B.g[i];
+    a.A = q.A;
+    a.B = q.B;
+    a.bias = q.bias;
+    a.Y = q.Y;
+    a.permA = q.permA;
+    a.permB = q.permB;
+    a.guard = q.guard;
+    a.M = q.M;
+    a.N = q.N;
+    a.K = q.K;
+    a.lda = q.lda;
+    a.ldb = q.ldb;
+    a.ldy = q.ldy;
+    a.bias_stride = q.bias_stride;
+    a.epi = q.epi;
+    a.act = q.act;
+    a.kt_per_split = P[i].per;
+    a.nsplit = P[i].splits;
+    a.vecA = P[i].vec;
+    a.vecB = P[i].vec;
+    if (P[i].splits == 1) {
+      a.C = q.C;
+      a.ldc = q.ldc;
+      a.split_stride = 0;
+      a.rowsumA = q.rowsum_out;
+    } else {
+      const size_t mn = (size_t)q.M * q.N;
+      const size_t need = (size_t)P[i].splits * mn + (q.rowsum_out ? (size_t)P[i].splits * q.M : 0);
+      float* ws = q.ws;
+      if (!ws) {
+        if (nl > 1) return fail(c, ZL_ERR_INVALID, "batched split-K needs caller scratch");
+        zl_status s = ensure_ws(c, need);
+        if (s) return s;
+        ws = c->ws;
+      } else if (need > q.ws_floats) {
+        return fail(c, ZL_ERR_INVALID, "split-K scratch too small (%zu < %zu floats)", q.ws_floats,
+                    need);
+      }
+      part[i] = ws;
+      a.C = ws;
+      a.ldc = q.N;
+      a.split_stride = (long long)mn;
+      a.rowsumA = q.rowsum_out ? ws + (size_t)P[i].splits * mn : nullptr;
+    }
+    gx = std::max(gx, P[i].gx);
+    gy = std::max(gy, P[i].gy);
+    if (g.kind == G_TILED) B.zper = std::max(B.zper, P[i].splits);
+    flops += 2.0 * q.M * q.N * (double)q.K;
+  }
   c->pending_flops = flops;
-  c->pending_shape = {d.M, d.N, d.K, splits};
-  zl_status s = launch(c, kid, gx, gy, g.kind == G_NARROW_M ? 1u : (unsigned)splits, a, 0,
-                       (unsigned)g.threads);
+  c->pending_shape = {live[0]->M, live[0]->N, live[0]->K, P[0].splits};
+  zl_status s = launch(c, P[0].kid, gx, gy, (unsigned)(nl * B.zper), B, 0, (unsigned)g.threads);
   if (s) return s;
-  zk::SplitReduceArgs r{};
-  r.part = ws;
-  r.out = d.C;
-  r.rowpart = a.rowsumA;
-  r.rowout = d.rowsum_out;
-  r.guard = d.guard;
-  r.mn = (long long)mn;
-  r.cols = d.N;
-  r.ldo = d.ldc;
-  r.rows = d.rowsum_out ? d.M : 0;
-  r.splits = splits;
-  return launch_splitk_reduce(c, r);
+  // Split-K partials: reduced now, or handed to the caller's all-layer
+  // reduction (seg_out), which also takes tensors written directly.
+  for (int i = 0; i < nl; ++i) {
+    const GemmDesc& q = *live[i];
+    const zk::GemmArgs& a = B.g[i];
+    if (q.seg_out) {
+      zk::ReduceSeg& r = *q.seg_out;
+      r = zk::ReduceSeg{};
+      r.part = part[i];
+      r.rowpart = part[i] ? a.rowsumA : nullptr;
+      r.out = q.C;
+      r.rowout = q.rowsum_out;
+      r.mn = (long long)q.M * q.N;
+      r.cols = q.N;
+      r.ldo = q.ldc;
+      r.rows = q.rowsum_out ? q.M : 0;
+      r.splits = P[i].splits;
+      continue;
+    }
+    if (!part[i]) continue;
+    zk::SplitReduceArgs r{};
+    r.part = part[i];
+    r.out = q.C;
+    r.rowpart = a.rowsumA;
+    r.rowout = q.rowsum_out;
+    r.guard = q.guard;
+    r.mn = (long long)q.M * q.N;
+    r.cols = q.N;
+    r.ldo = q.ldc;
+    r.rows = q.rowsum_out ? q.M : 0;
+    r.splits = P[i].splits;
+    if ((s = launch_splitk_reduce(c, r))) return s;
+  }
+  return ZL_OK;
+}
+
+zl_status run_gemm(zl_ctx* c, const GemmDesc& d) { return run_gemm_batch(c, &d, 1); }
+
+// Sum the component-major [width x blocks] partials of zk_actor_loss over
+// blocks into out[width] (zk_row_sum, fixed order).
+zl_status reduce_rows(zl_ctx* c, const float* part, int width, int blocks, float* out) {
+  zk::RowSumArgs a{};
+  a.out = out;
+  a.x = part;
+  a.rows = width;
+  a.cols = blocks;
+  a.ldx = blocks;
+  return launch(c, K_ROW_SUM, (unsigned)width, 1, 1, a);
+}
+
+
+// Split lanes for `splits` slices: enough that each thread adds at most ~8.
+static int reduce_lanes(int splits) {
+  int sl = 1;
+  while (sl < 64 && sl * 8 < splits) sl <<= 1;
+  return sl;
+}
+
+int reduce_all_layout(zk::ReduceSeg* segs, int nseg) {
+  int blk = 0;
+  for (int i = 0; i < nseg; ++i) {
+    zk::ReduceSeg& r = segs[i];
+    r.lanes = r.part ? reduce_lanes(r.splits) : 1;
+    const int per_block = zk::kReduceAllThreads / r.lanes;
+    r.blk0 = blk;
+    r.nqb = (int)cdiv(cdiv(r.mn, 4), per_block);
+    r.nrb = r.rows > 0 ? (int)cdiv(r.rows, per_block) : 0;
+    blk += r.nqb + r.nrb;
+  }
+  return blk;
+}
+
+zl_status launch_reduce_all(zl_ctx* c, const zk::ReduceSeg* segs, int nseg, float* sq_part,
+                            const int* guard) {
+  if (nseg < 1 || nseg > zk::kMaxReduceSegs)
+    return fail(c, ZL_ERR_INVALID, "reduce_all: %d segments", nseg);
+  zk::ReduceAllArgs a{};
+  for (int i = 0; i < nseg; ++i) a.seg[i] = segs[i];
+  a.nseg = nseg;
+  a.sq_part = sq_part;
+  a.guard = guard;
+  const int blocks = reduce_all_layout(a.seg, nseg);
+  return launch(c, K_REDUCE_ALL, (unsigned)blocks, 1, 1, a, 0, zk::kReduceAllThreads);
 }
 
 static std::string code_object_path() {
@@ -837,11 +969,11 @@ zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const flo
   a.rows_per_block = sh.rows_per_block;
   a.group = sh.group;
   if (nb == 0) return ZL_OK;
-  s = launch(c, K_ACTOR_LOSS, (unsigned)nb, 1, 1, a);
+  s = launch(c, sh.kernel, (unsigned)nb, 1, 1, a, 0, zk::kLossThreads);
   if (s) return s;
-  s = reduce_partials(c, a.gls_part, nb, A, d_log_std);
+  s = reduce_rows(c, a.gls_part, A, nb, d_log_std);
   if (s) return s;
-  return reduce_partials(c, a.stat_part, nb, 2, stats_dev);
+  return reduce_rows(c, a.stat_part, 2, nb, stats_dev);
 }
 
 zl_status zl_ppo_value_grad(zl_ctx* c, const float* v, const float* value_old, const float* ret,
