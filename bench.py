@@ -31,6 +31,12 @@ N_ENVS, T_STEPS = 4096, 24
 EPOCHS, MINIBATCHES = 5, 4
 FP32_MFMA_PEAK = 157.3e12  # MI355X dense fp32 matrix, FLOP/s
 HBM_PEAK = 8.0e12  # bytes/s
+# HBM bytes per launch of a kernel, measured with rocprofv3 --pmc FETCH_SIZE
+# and WRITE_SIZE on this workload (one counter per run), scaled by the
+# readings of a 256 MiB copy kernel (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0) and
+# averaged over an update's launch mix; reported as roofline.traffic for the
+# dominant kernel when it is one of these.
+MEASURED_TRAFFIC = {"zk_gemm_ak_bk_96x128x32_w24": 116.7e6}
 
 
 def cpu_baseline(ro, actor, critic, log_std, mean_old, action, logp_old, values, adv):
@@ -135,7 +141,7 @@ def main():
                                            C.byref(fl)), "timing_kernel")
         if cnt.value:
             ktime[name.value.decode()] = (ms.value, cnt.value, fl.value)
-    gemm = {k: v for k, v in ktime.items() if k.startswith("zk_gemm")}
+    gemm = {k: v for k, v in ktime.items() if k.startswith(("zk_gemm", "zk_narrow"))}
     gemm_ms = sum(v[0] for v in gemm.values())
     gemm_flops = sum(v[2] for v in gemm.values())
     dom = max(gemm, key=lambda k: gemm[k][0])
@@ -201,7 +207,7 @@ def main():
             "peak": FP32_MFMA_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved / FP32_MFMA_PEAK,
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC.get(dom),
             "flop_per_launch": dom_flop_per_launch,
             "avg_launch_us": dom_avg_s * 1e6,
             "launches_per_step": dom_cnt,

@@ -236,7 +236,8 @@ struct Tile {
 // g runs the 16-wide chunks [g, g+1) * BK/16/KG); the groups' accumulators are
 // added in LDS in group order before the epilogue, so a tile gets KG times
 // the waves without any global split-K partials.
-template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, int KG, bool VEC>
+template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, int KG, bool VEC,
+          bool YPRE = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
   constexpr int NT = 64 * WM * WN * KG;
   constexpr int TM = BM / (WM * 16);
@@ -296,9 +297,30 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
   }
   __syncthreads();
 
+  // YPRE variants (data gradients): the ELU' operand is read into registers
+  // two k-tiles before the end, so its latency overlaps the last MFMAs
+  // instead of the epilogue waiting for it.
+  const bool elu_grad = YPRE && p.epi == kEpiEluGrad && kg == 0;
+  float ypre[YPRE ? TM : 1][YPRE ? TN : 1][4];
+  auto prefetch_y = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + (wn * TN + j) * 16 + lr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + (wm * TM + i) * 16 + lg * 4 + r;
+          if constexpr (YPRE) ypre[i][j][r] = (m < p.M && n < p.N) ? p.Y[(long long)m * p.ldy + n] : 0.f;
+        }
+      }
+  };
+  if (elu_grad && kt1 - kt0 <= 2) prefetch_y();
+
   for (int kt = kt0; kt < kt1; ++kt) {
     const int cur = (kt - kt0) & 1;
     const bool more = kt + 1 < kt1;
+    if (elu_grad && kt1 - kt0 > 2 && kt == kt1 - 2) prefetch_y();
     if (more) {
       ta.load((kt + 1) * BK);
       tb.load((kt + 1) * BK);
@@ -389,7 +411,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
             v = v + p.bias[(long long)m * p.bias_stride];
             if (p.act) v = elu(v);
           } else if (p.epi == kEpiEluGrad) {
-            v = v * elu_grad_from_act(p.Y[(long long)m * p.ldy + n]);
+            if constexpr (YPRE)
+              v = v * elu_grad_from_act(ypre[i][j][r]);
+            else
+              v = v * elu_grad_from_act(p.Y[(long long)m * p.ldy + n]);
           }
           C[(long long)m * p.ldc + n] = v;
         }
@@ -604,6 +629,14 @@ ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_96x128x16_w24, true, false, 96, 128, 16, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_96x128x32_w22k2, true, false, 96, 128, 32, 2, 2, 2, true)
+// Data-gradient variant (ELU' operand prefetched), held to 4 waves per SIMD
+// so that two 8-wave blocks stay resident per CU.
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+void zk_gemm_ak_bn_96x128x32_w24_dg(zk::GemmBatch b) {
+  const int prob = blockIdx.z / b.zper;
+  if (prob >= b.count) return;
+  zk::gemm_body<true, false, 96, 128, 32, 2, 4, 1, true, true>(b.g[prob], blockIdx.z % b.zper);
+}
 ZK_GEMM(zk_gemm_ak_bn_128x128x32_w24, true, false, 128, 128, 32, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_128x128x32_w22, true, false, 128, 128, 32, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_ak_bn_128x128x16_w22, true, false, 128, 128, 16, 2, 2, 1, true)

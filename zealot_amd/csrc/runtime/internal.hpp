@@ -205,7 +205,8 @@ struct GemmDesc {
 // Variant choice and split-K decision shared by run_gemm and the scratch
 // sizing of composites.
 // vec: both operands can be read as aligned float4 rows (see run_gemm).
-int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec = true);
+int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec = true,
+              int epi = zk::kEpiStore);
 int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi,
                 bool vec = true);
 size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);

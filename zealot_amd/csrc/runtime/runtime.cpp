@@ -37,6 +37,7 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x16_w24", true, false, 96, 128, 16, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w22k2", true, false, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bn_96x128x32_w24_dg", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bn_128x128x32_w24", true, false, 128, 128, 32, 512, true},
     {"zk_gemm_ak_bn_128x128x32_w22", true, false, 128, 128, 32, 256, true},
     {"zk_gemm_ak_bn_128x128x16_w22", true, false, 128, 128, 16, 256, true},
@@ -137,7 +138,7 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
 // 512- and 256-wide layers, 64 x 128 for the 128-wide one and 32 x 128 for
 // the narrow heads (measured on gfx950 at 24,576 rows).
-int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec) {
+int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec, int epi) {
   const int lay = layout_of(a_kc, b_kc);
   const bool forced = c && c->force_gemm[lay] >= 0;
   if (!forced && (!c || c->narrow)) {
@@ -167,7 +168,11 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
         name = M >= 4096 ? "zk_gemm_ak_bk_96x128x32_w24" : "zk_gemm_ak_bk_64x128x16_w22";
       break;
     case L_AK_BN:
-      name = M >= 4096 ? "zk_gemm_ak_bn_96x128x32_w24" : "zk_gemm_ak_bn_64x128x16_w22";
+      // Data gradients (ELU' epilogue) take the variant that prefetches the
+      // activation operand.
+      name = M >= 4096 ? (epi == zk::kEpiEluGrad ? "zk_gemm_ak_bn_96x128x32_w24_dg"
+                                                 : "zk_gemm_ak_bn_96x128x32_w24")
+                       : "zk_gemm_ak_bn_64x128x16_w22";
       break;
     case L_AM_BN:
       if (M >= 256)
@@ -253,7 +258,7 @@ static zl_status plan_gemm(zl_ctx* c, const GemmDesc& d, GemmPlan& P) {
   const int b_ext = d.b_kc ? d.K : d.N;
   P.vec = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4) && aligned16(d.B) &&
           d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
-  P.kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc, P.vec);
+  P.kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc, P.vec, d.epi);
   if (P.kid < 0) return fail(c, ZL_ERR_INVALID, "no GEMM variant for this layout");
   const GemmKernel& g = kGemmTable[P.kid - K_GEMM_BASE];
   if (g.a_kc != d.a_kc || g.b_kc != d.b_kc || (g.vec && !P.vec))
