@@ -132,7 +132,7 @@ struct zl_ctx {
   // (ZL_SPLITK) and the split-K target grid size (ZL_SPLITK_TARGET).
   int force_gemm[4] = {-1, -1, -1, -1};
   int force_splits = 0;
-  int splitk_target = 512;
+  int splitk_target = 256;
   // Narrow kernels for shapes with a dimension <= 32 (ZL_NARROW=0 turns them
   // off) and the block count their row slices aim at (ZL_NARROW_TARGET).
   bool narrow = true;

@@ -215,8 +215,10 @@ int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int 
   } else {
     // Deep-K, few-tile shapes (the weight gradients, K = batch rows) would
     // leave most CUs idle: slice K so the grid reaches the split-K target
-    // (512 = two workgroups per CU), keeping at least 8 k-tiles per slice.
-    const int target = c ? c->splitk_target : 512;
+    // (256 = one workgroup per CU: more slices buy no speed in the GEMM at
+    // 24,576 rows and cost reduction traffic), keeping at least 8 k-tiles
+    // per slice.
+    const int target = c ? c->splitk_target : 256;
     if (tiles >= target || kt < 16) return 1;
     s = std::min<long long>(cdiv(target, tiles), std::max<long long>(1, kt / 8));
   }
