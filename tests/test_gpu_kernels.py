@@ -72,6 +72,34 @@ def test_gemm_layouts_ragged(ctx, lt, rt, shape):
     assert err <= FWD_BWD_TOL, (shape, lt, rt, err)
 
 
+# Shapes with several 96x128 output tiles per resident workgroup and no
+# split-K (the row-major forward ak_bk and data-gradient ak_bn tiles), ragged
+# in every dimension, with K tails of 12 and 4 and a single k-tile.
+LARGE_CASES = [
+    (50000, 300, 76, False, True),
+    (50000, 300, 76, False, False),
+    (13001, 1000, 132, False, True),
+    (13001, 1000, 132, False, False),
+    (70001, 130, 20, False, True),
+]
+
+
+@pytest.mark.parametrize("case", LARGE_CASES)
+def test_gemm_large_ragged(ctx, case):
+    m, n, k, lt, rt = case
+    g = np.random.default_rng(m + 3 * n + 5 * k + rt)
+    L = g.standard_normal((m, k)).astype(np.float32)
+    R = g.standard_normal((k, n)).astype(np.float32)
+    ref = L.astype(np.float64) @ R.astype(np.float64)
+    dl = ctx.to_device(L)
+    dr = ctx.to_device(R.T.copy() if rt else R)
+    out = ctx.alloc((m, n))
+    ops.gemm(ctx, out, dl, lt, dr, rt, m, n, k)
+    err = rel_amax(out.numpy(), ref)
+    print(f"[gpu] large gemm {case}: rel err {err:.2e}", flush=True)
+    assert err <= FWD_BWD_TOL, (case, err)
+
+
 # Shapes routed to the register-resident narrow kernels (one dimension <= 32):
 # (m, n, k, lhs_t, rhs_t) and the family each exercises.
 NARROW_CASES = [
@@ -174,7 +202,8 @@ def _mlp_case(ctx, dims, rows, seed, bias_bound=0.1):
 
 
 @pytest.mark.parametrize("dims,rows", [([4, 6, 5, 3], 7), ([123, 512, 256, 128, 29], 4096),
-                                       ([123, 512, 256, 128, 1], 1000), ([17, 33, 2], 300)])
+                                       ([123, 512, 256, 128, 1], 1000), ([17, 33, 2], 300),
+                                       ([123, 512, 256, 128, 29], 13001)])
 def test_mlp_forward_vs_oracle(ctx, dims, rows):
     g, params, x, dx, mlp = _mlp_case(ctx, dims, rows, seed=rows)
     got = mlp.output(rows)
@@ -185,7 +214,8 @@ def test_mlp_forward_vs_oracle(ctx, dims, rows):
 
 
 @pytest.mark.parametrize("dims,rows", [([4, 6, 5, 3], 7), ([123, 512, 256, 128, 29], 4096),
-                                       ([123, 512, 256, 128, 1], 2048), ([17, 33, 2], 300)])
+                                       ([123, 512, 256, 128, 1], 2048), ([17, 33, 2], 300),
+                                       ([123, 512, 256, 128, 29], 13001)])
 def test_mlp_backward_vs_oracle(ctx, dims, rows):
     g, params, x, dx, mlp = _mlp_case(ctx, dims, rows, seed=rows + 1)
     gout = (g.standard_normal((rows, dims[-1])) / rows).astype(np.float32)

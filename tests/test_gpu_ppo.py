@@ -123,28 +123,36 @@ def test_minibatch_grads_config4(ctx):
     gac.close()
 
 
-@pytest.mark.parametrize("hidden", [64, 24])
-def test_minibatch_grads_with_perm(ctx, hidden):
+@pytest.mark.parametrize("hidden,n,start,mb", [(64, 5000, 1000, 1500), (24, 5000, 1000, 1500),
+                                                (512, 20000, 3000, 13001)])
+def test_minibatch_grads_with_perm(ctx, hidden, n, start, mb):
     """Row gather through a device permutation (the shuffled minibatch); a
-    24-wide first layer sends the gathered rows through the narrow kernels."""
+    24-wide first layer sends the gathered rows through the narrow kernels,
+    a 512-wide one over 13,001 rows through ragged multi-wave tile grids."""
     ad, cd = [37, hidden, 48, 7], [37, hidden, 48, 1]
     g = np.random.default_rng(8)
     actor = synth.kaiming_uniform_net(g, ad, 0.1)
     critic = synth.kaiming_uniform_net(g, cd, 0.1)
-    n = 5000
     batch, log_std = make_batch(n, ad, cd, actor, critic, seed=99)
     move_off_branch_boundaries(batch, ad, cd, actor, critic, log_std)
     perm = g.permutation(n).astype(np.int32)
-    gac = GpuActorCritic(ctx, ad, cd, 1500)
+    gac = GpuActorCritic(ctx, ad, cd, mb)
     gac.set_params(actor, critic, log_std, 1e-3)
     db = DeviceBatch(ctx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
                      batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
-    ga, gc, gl, st = gac.minibatch_grads(db, PpoConfig(entropy_coef=0.01), 1000, 1500,
+    ga, gc, gl, st = gac.minibatch_grads(db, PpoConfig(entropy_coef=0.01), start, mb,
                                          perm=ctx.to_device(perm))
-    idx = perm[1000:2500]
+    idx = perm[start:start + mb]
     ra, rc, rl, rst = zo.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
     assert per_tensor_err(ad, ga, ra) <= TOL and per_tensor_err(cd, gc, rc) <= TOL
-    assert rel_amax(gl, rl) <= TOL
+    # The log_std gradient is a sum over rows with cancellation: over 13,001
+    # rows the oracle's sequential fp32 sum is itself 1.6e-4 off the float64
+    # truth (the GPU 1.8e-5), so that leg is judged against the truth.
+    _, _, tl, _ = np_ref.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
+    e_gpu, e_cpu = rel_amax(gl, tl), rel_amax(rl, tl)
+    print(f"[gpu] perm grads hidden {hidden} x {mb}: log_std gpu vs f64 {e_gpu:.2e}, oracle vs f64 {e_cpu:.2e}",
+          flush=True)
+    assert e_gpu <= TOL
 
 
 def _param_delta_report(p0, pg, pc, lr, steps):
