@@ -173,6 +173,33 @@ zl_status zl_sample_actions(zl_ctx* ctx, const float* mean, int ld_mean, const f
                             const float* eps, int rows, int action_dim, float* action,
                             float* logp);
 
+/* ----------------------------------------- observation normalisation ---- */
+
+/* A running normaliser lives in device memory as float[2 * dim + 1]:
+ * mean[dim], m2[dim], count (Normalizer, zealot-rl/src/ppo.rs:104-113). A
+ * pending state (PendingNorm, :115-122) has the same layout; count 0 means
+ * empty. dim <= 4096. All calls are enqueued on the context's stream. */
+
+/* unit_prior != 0: Normalizer::new (ppo.rs:141-148: mean 0, m2 1, count 1);
+ * unit_prior == 0: an empty PendingNorm (PendingNorm::default). */
+zl_status zl_norm_reset(zl_ctx* ctx, float* state, int dim, int unit_prior);
+/* Fold rows x[r * ld + i], r = 0 .. rows-1 in order, into a state:
+ * Normalizer::update (ppo.rs:161-168, ActorCritic::record_obs :276-279) on a
+ * live state, PendingNorm::push (:126-137) on a pending one. count is exact
+ * (the reference's f32 `count += 1.0`, saturating at 2^24); mean and m2 are
+ * folded in chunks of 256 rows and agree with the one-at-a-time fold to fp32
+ * rounding. */
+zl_status zl_norm_update(zl_ctx* ctx, float* state, int dim, const float* x, int ld,
+                         long long rows);
+/* Normalizer::commit (ppo.rs:179-195): merge pending into state (Chan), then
+ * empty pending; no-op when pending is empty. */
+zl_status zl_norm_commit(zl_ctx* ctx, float* state, float* pending, int dim);
+/* Normalizer::normalize (ppo.rs:198-205) of each row:
+ * out[r * ld_out + i] = clamp((x[r * ld_x + i] - mean[i]) / sqrt(max(m2[i] / count, 1e-8)), -5, 5).
+ * out may be x (in place) when ld_out == ld_x. */
+zl_status zl_norm_normalize(zl_ctx* ctx, const float* state, int dim, const float* x, int ld_x,
+                            long long rows, float* out, int ld_out);
+
 /* ------------------------------------------------ GpuMlp equivalent ---- */
 
 /* A dense ELU MLP (hidden ELU, linear output) with device-resident weights,

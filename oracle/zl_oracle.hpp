@@ -20,10 +20,10 @@
 //
 // Pinning: every function used by the tests is checked against the
 // reference's own known-answer tests, closed forms or float64 finite
-// differences (tests/test_oracle.py). PendingNorm::push / norm_commit
-// (ppo.rs:126-137,179-195) are restated but not reachable from the C API and
-// have no check: parity unpinned (they belong to the on-device observation
-// normaliser, which the HIP path does not implement yet).
+// differences (tests/test_oracle.py); the normaliser (Normalizer::update,
+// PendingNorm::push, norm_commit, normalize; ppo.rs:104-206) by the float64
+// Chan-merge closed forms, the unit-prior identity, the variance floor and
+// the f32 count saturation at 2^24.
 #pragma once
 #include <cmath>
 #include <cstddef>

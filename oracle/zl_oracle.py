@@ -92,6 +92,10 @@ def lib() -> C.CDLL:
         "zlo_tr_update": (None, [vp, C.c_longlong, C.c_int, C.c_int, vp, vp, vp, vp, vp, vp, vp,
                                  vp, C.POINTER(TrainerCfg), C.c_int, vp]),
         "zlo_adv_normalize": (None, [vp, C.c_longlong]),
+        "zlo_norm_update_rows": (None, [vp, C.c_int, vp, C.c_int, C.c_longlong]),
+        "zlo_pending_push_rows": (None, [vp, C.c_int, vp, C.c_int, C.c_longlong]),
+        "zlo_norm_commit": (None, [vp, vp, C.c_int]),
+        "zlo_norm_normalize_rows": (None, [vp, C.c_int, vp, C.c_int, C.c_longlong, vp, C.c_int]),
         "zlo_ppo_minibatch_grads": (None, [vp, C.c_int, vp, C.c_int, vp, vp, vp, C.c_longlong,
                                            vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_longlong, fl,
                                            fl, fl, C.c_int, vp, vp, vp, vp]),
@@ -196,6 +200,48 @@ def adv_normalize(adv):
     a = f32(adv).copy()
     lib().zlo_adv_normalize(_p(a), a.size)
     return a
+
+
+# Observation normaliser on flat states float[2 * dim + 1] = mean, m2, count
+# (ppo.rs:104-206).
+def norm_new(dim, unit_prior=True):
+    """Normalizer::new (unit prior) or an empty PendingNorm."""
+    st = np.zeros(2 * dim + 1, np.float32)
+    if unit_prior:
+        st[dim:] = 1.0
+    return st
+
+
+def norm_update(state, x):
+    """Normalizer::update for each row of x [rows x dim] in order; returns the new state."""
+    st, xa = f32(state).copy(), f32(x)
+    dim = st.size // 2
+    lib().zlo_norm_update_rows(_p(st), dim, _p(xa), xa.shape[1], xa.shape[0])
+    return st
+
+
+def pending_push(state, x):
+    """PendingNorm::push for each row of x in order; returns the new pending state."""
+    st, xa = f32(state).copy(), f32(x)
+    dim = st.size // 2
+    lib().zlo_pending_push_rows(_p(st), dim, _p(xa), xa.shape[1], xa.shape[0])
+    return st
+
+
+def norm_commit(state, pending):
+    """Normalizer::commit; returns (state, pending) after the merge."""
+    st, pd = f32(state).copy(), f32(pending).copy()
+    lib().zlo_norm_commit(_p(st), _p(pd), st.size // 2)
+    return st, pd
+
+
+def norm_normalize(state, x):
+    """Normalizer::normalize of each row of x [rows x dim]."""
+    st, xa = f32(state), f32(x)
+    out = np.empty_like(xa)
+    lib().zlo_norm_normalize_rows(_p(st), st.size // 2, _p(xa), xa.shape[1], xa.shape[0], _p(out),
+                                  xa.shape[1])
+    return out
 
 
 def minibatch_grads(actor_dims, critic_dims, actor, critic, log_std, batch: dict, idx, clip,

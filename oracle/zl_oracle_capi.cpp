@@ -407,6 +407,69 @@ void zlo_ppo_minibatch_grads(const int* adims, int na, const int* cdims, int nc,
   std::memcpy(gls_out, gls.data(), ad * 4);
 }
 
+// ---- observation normaliser on flat state buffers float[2 * dim + 1] =
+// mean[dim], m2[dim], count (the device normaliser's layout). A pending
+// state with count 0 is an empty PendingNorm.
+
+static Normalizer norm_from(const float* st, int dim) {
+  Normalizer n;
+  n.mean.assign(st, st + dim);
+  n.m2.assign(st + dim, st + 2 * dim);
+  n.count = st[2 * dim];
+  return n;
+}
+static void norm_to(const Normalizer& n, float* st, int dim) {
+  std::memcpy(st, n.mean.data(), dim * 4);
+  std::memcpy(st + dim, n.m2.data(), dim * 4);
+  st[2 * dim] = n.count;
+}
+static PendingNorm pending_from(const float* st, int dim) {
+  PendingNorm p;
+  p.count = st[2 * dim];
+  if (p.count != 0.0f) {  // an empty PendingNorm holds no vectors
+    p.mean.assign(st, st + dim);
+    p.m2.assign(st + dim, st + 2 * dim);
+  }
+  return p;
+}
+static void pending_to(const PendingNorm& p, float* st, int dim) {
+  for (int i = 0; i < dim; ++i) {
+    st[i] = p.mean.empty() ? 0.0f : p.mean[i];
+    st[dim + i] = p.m2.empty() ? 0.0f : p.m2[i];
+  }
+  st[2 * dim] = p.count;
+}
+
+// Normalizer::update (ppo.rs:161-168) for rows x[r * ld ..], in order.
+void zlo_norm_update_rows(float* st, int dim, const float* x, int ld, long long rows) {
+  Normalizer n = norm_from(st, dim);
+  for (long long r = 0; r < rows; ++r) n.update(x + r * ld);
+  norm_to(n, st, dim);
+}
+
+// PendingNorm::push (ppo.rs:126-137) for rows x[r * ld ..], in order.
+void zlo_pending_push_rows(float* st, int dim, const float* x, int ld, long long rows) {
+  PendingNorm p = pending_from(st, dim);
+  for (long long r = 0; r < rows; ++r) p.push(x + r * ld, (size_t)dim);
+  pending_to(p, st, dim);
+}
+
+// Normalizer::commit (ppo.rs:179-195).
+void zlo_norm_commit(float* st, float* pend, int dim) {
+  Normalizer n = norm_from(st, dim);
+  PendingNorm p = pending_from(pend, dim);
+  norm_commit(n, p);
+  norm_to(n, st, dim);
+  pending_to(p, pend, dim);
+}
+
+// Normalizer::normalize (ppo.rs:198-205) of each row.
+void zlo_norm_normalize_rows(const float* st, int dim, const float* x, int ld, long long rows,
+                             float* out, int ld_out) {
+  Normalizer n = norm_from(st, dim);
+  for (long long r = 0; r < rows; ++r) n.normalize(x + r * ld, out + r * ld_out);
+}
+
 // Advantage normalisation exactly as ppo.rs:343-348 / biped_train_gpu.rs:1010-1016.
 void zlo_adv_normalize(float* adv, long long n) {
   float mean = 0.0f;

@@ -495,3 +495,97 @@ def test_normalizer_welford_with_unit_prior():
     assert np.allclose(ac.mean(probe), np_ref.forward(ad, actor, z[None])[-1][0], rtol=1e-5, atol=1e-6)
     zc = closed(cs, probe)
     assert np.allclose(ac.value(probe), np_ref.forward(cd, critic, zc[None])[-1][0, 0], rtol=1e-5, atol=1e-6)
+
+
+# ---- observation normaliser on flat states (mean[dim], m2[dim], count), the
+# layout the device normaliser uses (ppo.rs:104-206).
+
+def _obs_rows(seed, n, dim):
+    g = np.random.default_rng(seed)
+    scale = g.uniform(0.1, 3.0, dim)
+    shift = g.uniform(-4.0, 4.0, dim)
+    return (g.standard_normal((n, dim)) * scale + shift).astype(np.float32)
+
+
+def test_norm_update_rows_closed_form():
+    """Normalizer::update from the unit prior over n rows equals the Chan
+    merge of the prior (count 1, mean 0, m2 1) with the data: count n + 1,
+    mean sum(x) / (n + 1), m2 1 + sum((x - xbar)^2) + xbar^2 n / (n + 1)."""
+    dim, n = 7, 3000
+    x = _obs_rows(1, n, dim)
+    st = zo.norm_update(zo.norm_new(dim), x)
+    d = x.astype(np.float64)
+    xbar = d.mean(0)
+    mean = d.sum(0) / (n + 1)
+    m2 = 1.0 + ((d - xbar) ** 2).sum(0) + xbar ** 2 * n / (n + 1)
+    assert st[2 * dim] == n + 1
+    assert rel_amax(st[:dim], mean) <= 1e-5
+    assert np.max(np.abs(st[dim:2 * dim] / m2 - 1.0)) <= 1e-4
+
+
+def test_pending_push_rows_closed_form():
+    """PendingNorm::push from empty: count n, mean xbar, m2 = sum((x - xbar)^2)."""
+    dim, n = 5, 2000
+    x = _obs_rows(2, n, dim)
+    pd = zo.pending_push(zo.norm_new(dim, unit_prior=False), x)
+    d = x.astype(np.float64)
+    assert pd[2 * dim] == n
+    assert rel_amax(pd[:dim], d.mean(0)) <= 1e-5
+    assert np.max(np.abs(pd[dim:2 * dim] / ((d - d.mean(0)) ** 2).sum(0) - 1.0)) <= 1e-4
+    # Pushing in two halves continues the same fold: bit-identical.
+    half = zo.pending_push(zo.pending_push(zo.norm_new(dim, False), x[:777]), x[777:])
+    assert np.array_equal(half, pd)
+
+
+def test_norm_commit_closed_form_and_empty():
+    """Normalizer::commit: the Chan merge in float64 (state then pending),
+    the pending state emptied, and a no-op for an empty pending state."""
+    dim = 6
+    base = zo.norm_update(zo.norm_new(dim), _obs_rows(3, 500, dim))
+    pend = zo.pending_push(zo.norm_new(dim, False), _obs_rows(4, 800, dim) + np.float32(1.5))
+    st, pd = zo.norm_commit(base, pend)
+    n1, n2 = float(base[2 * dim]), float(pend[2 * dim])
+    dlt = pend[:dim].astype(np.float64) - base[:dim]
+    mean = base[:dim] + dlt * n2 / (n1 + n2)
+    m2 = base[dim:2 * dim].astype(np.float64) + pend[dim:2 * dim] + dlt ** 2 * n1 * n2 / (n1 + n2)
+    assert st[2 * dim] == n1 + n2
+    assert rel_amax(st[:dim], mean) <= 1e-6
+    assert np.max(np.abs(st[dim:2 * dim] / m2 - 1.0)) <= 1e-6
+    assert not pd.any()
+    # Committing an empty pending state changes nothing.
+    st2, pd2 = zo.norm_commit(st, pd)
+    assert np.array_equal(st2, st) and not pd2.any()
+    # Commit of a pushed batch agrees with the live fold of the same rows.
+    rows = _obs_rows(5, 1000, dim)
+    live = zo.norm_update(base, rows)
+    merged, _ = zo.norm_commit(base, zo.pending_push(zo.norm_new(dim, False), rows))
+    assert merged[2 * dim] == live[2 * dim]
+    assert rel_amax(merged[:dim], live[:dim]) <= 1e-5
+    assert np.max(np.abs(merged[dim:2 * dim] / live[dim:2 * dim] - 1.0)) <= 1e-4
+
+
+def test_norm_normalize_closed_form():
+    """Normalizer::normalize: the unit prior is the identity clamped to +-5
+    (bit-exact), a zero m2 hits the 1e-8 variance floor, and a general state
+    matches clamp((x - mean) / sqrt(max(m2 / count, 1e-8)), -5, 5) in float64."""
+    dim = 9
+    x = (_obs_rows(6, 400, dim) * np.float32(2.0)).astype(np.float32)
+    ident = zo.norm_normalize(zo.norm_new(dim), x)
+    assert np.array_equal(ident, np.clip(x, -5, 5))
+    st = zo.norm_update(zo.norm_new(dim), _obs_rows(7, 300, dim))
+    st[dim + 2] = 0.0  # component 2: var floor 1e-8 -> sd 1e-4
+    got = zo.norm_normalize(st, x)
+    var = np.maximum(st[dim:2 * dim].astype(np.float64) / st[2 * dim], 1e-8)
+    ref = np.clip((x - st[:dim].astype(np.float64)) / np.sqrt(var), -5, 5)
+    assert np.max(np.abs(got - ref)) <= 5e-6
+    far = np.abs(x[:, 2].astype(np.float64) - st[2]) > 5e-4  # beyond 5 sd of 1e-4
+    assert far.sum() > 300 and np.all(np.abs(got[far, 2]) == 5.0)
+
+
+def test_norm_count_saturates_like_f32():
+    """count += 1.0 in f32 stops at 2^24 (x + 1 rounds back to x there)."""
+    dim = 2
+    st = zo.norm_new(dim)
+    st[2 * dim] = np.float32(2 ** 24 - 2)
+    out = zo.norm_update(st, _obs_rows(8, 5, dim))
+    assert out[2 * dim] == np.float32(2 ** 24)

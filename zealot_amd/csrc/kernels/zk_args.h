@@ -275,6 +275,24 @@ struct SampleArgs {
   const int* guard;
 };
 
+// Observation normaliser (Normalizer / PendingNorm, zealot-rl/src/ppo.rs:104-206).
+// A state is float[2 * dim + 1]: mean[dim], m2[dim], count; a pending state
+// with count 0 is empty (its mean and m2 are zero).
+constexpr int kNormMaxDim = 4096;
+constexpr int kNormChunkRows = 256;    // rows per partial-statistics chunk
+constexpr int kNormApplyRows = 256;    // rows per zk_norm_apply block
+constexpr int kNormFoldThreads = 1024;  // zk_norm_merge / zk_norm_commit block
+struct NormArgs {
+  const float* x;   // [rows x ldx]
+  float* out;       // zk_norm_apply: [rows x ldo]
+  float* state;     // fold / commit target, zk_norm_apply source, zk_norm_set target
+  float* pending;   // zk_norm_commit: folded into state, then emptied
+  float* part;      // [nchunks x 2 x dim]: per chunk mean[dim], then M2[dim]
+  long long rows;
+  int dim, ldx, ldo, nchunks;
+  int unit_prior;   // zk_norm_set: 1 = Normalizer::new, 0 = empty pending state
+};
+
 struct ClampArgs {
   float* x;
   int n;

@@ -34,6 +34,11 @@ enum KernelId : int {
   K_CLAMP,
   K_REDUCE_ALL,
   K_ACTOR_LOSS_G64,
+  K_NORM_SET,
+  K_NORM_APPLY,
+  K_NORM_STATS,
+  K_NORM_MERGE,
+  K_NORM_COMMIT,
   K_GEMM_BASE
 };
 

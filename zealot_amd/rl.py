@@ -175,6 +175,74 @@ class GpuMlp:
             pass
 
 
+def _dptr(x):
+    """Device pointer of a DeviceBuffer, or a raw pointer (DeviceBuffer.offset)."""
+    return x.p if isinstance(x, DeviceBuffer) else x
+
+
+class GpuNormalizer:
+    """zealot-rl's running observation Normalizer (ppo.rs:104-206) with its
+    Welford state in HBM as float[2 * dim + 1] = mean, m2, count. update /
+    commit / normalize are kernels on the context's stream."""
+
+    def __init__(self, ctx: Context, dim: int, unit_prior: bool = True):
+        self.ctx = ctx
+        self.dim = int(dim)
+        self.buf = ctx.alloc(2 * self.dim + 1)
+        ctx.check(ctx.lib.zl_norm_reset(ctx.h, self.buf.p, self.dim, int(unit_prior)), "zl_norm_reset")
+
+    @classmethod
+    def from_state(cls, ctx: Context, mean, m2, count: float) -> "GpuNormalizer":
+        """Normalizer::from_state (ppo.rs:150-153)."""
+        n = cls(ctx, len(mean))
+        st = np.concatenate([np.asarray(mean, np.float32), np.asarray(m2, np.float32),
+                             np.array([count], np.float32)])
+        n.buf.upload(st)
+        return n
+
+    def state(self):
+        """Normalizer::state (ppo.rs:156-158): host copies (mean, m2, count)."""
+        st = self.buf.numpy()
+        return st[:self.dim].copy(), st[self.dim:2 * self.dim].copy(), float(st[2 * self.dim])
+
+    def update(self, x: DeviceBuffer, rows: int, ld: int | None = None):
+        """Normalizer::update (ppo.rs:161-168) for rows of x, in order."""
+        self.ctx.check(self.ctx.lib.zl_norm_update(self.ctx.h, self.buf.p, self.dim, _dptr(x),
+                                                   int(ld or self.dim), int(rows)), "zl_norm_update")
+
+    def commit(self, pending: "GpuPendingNorm"):
+        """Normalizer::commit (ppo.rs:179-195): merge, then empty `pending`."""
+        self.ctx.check(self.ctx.lib.zl_norm_commit(self.ctx.h, self.buf.p, pending.buf.p, self.dim),
+                       "zl_norm_commit")
+
+    def normalize(self, x: DeviceBuffer, rows: int, out: DeviceBuffer, ld_x: int | None = None,
+                  ld_out: int | None = None):
+        """Normalizer::normalize (ppo.rs:198-205) of each row of x into out."""
+        self.ctx.check(self.ctx.lib.zl_norm_normalize(self.ctx.h, self.buf.p, self.dim, _dptr(x),
+                                                      int(ld_x or self.dim), int(rows), _dptr(out),
+                                                      int(ld_out or self.dim)), "zl_norm_normalize")
+
+
+class GpuPendingNorm:
+    """PendingNorm (ppo.rs:115-137): Welford statistics gathered while the
+    live transform is frozen, merged by GpuNormalizer.commit."""
+
+    def __init__(self, ctx: Context, dim: int):
+        self.ctx = ctx
+        self.dim = int(dim)
+        self.buf = ctx.alloc(2 * self.dim + 1)
+        ctx.check(ctx.lib.zl_norm_reset(ctx.h, self.buf.p, self.dim, 0), "zl_norm_reset")
+
+    def push(self, x: DeviceBuffer, rows: int, ld: int | None = None):
+        """PendingNorm::push for rows of x, in order."""
+        self.ctx.check(self.ctx.lib.zl_norm_update(self.ctx.h, self.buf.p, self.dim, _dptr(x),
+                                                   int(ld or self.dim), int(rows)), "zl_norm_update")
+
+    @property
+    def count(self) -> float:
+        return float(self.buf.numpy()[2 * self.dim])
+
+
 class GpuActorCritic:
     """The ActorCritic of zealot-rl/src/ppo.rs:208-229 resident on one MI355X:
     actor, critic, log_std and all Adam state in one flat HBM buffer, updated
