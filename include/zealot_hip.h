@@ -312,6 +312,21 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* ppo, const zl_batch* batch, const zl_pp
                                  long long row0, int rows, const int* perm_dev, float* stats);
 /* Download the gradient buffer, packed like the params (any pointer may be NULL). */
 zl_status zl_ppo_get_grads(zl_ppo* ppo, float* actor, float* critic, float* log_std);
+/* One rollout step for n envs on the device: GpuPolicy::forward
+ * (src/biped/gpu_policy.rs:210-248) and the trainer's sampling loop
+ * (src/bin/biped_train_gpu.rs:910-930) without the host round trip. Row r of
+ * obs (and critic_obs) is normalised with its normaliser state (as
+ * zl_norm_normalize; a NULL state means the rows are already normalised),
+ * then mean = actor(obs_r), action[r * A + k] = mean_k + exp(log_std_k) *
+ * eps[r * A + k], logp[r] = ActorCritic::logp(action, mean) (ppo.rs:297-306)
+ * and value[r] = critic(critic_obs_r). mean (row stride ld_mean) and value
+ * may be NULL; critic_obs and critic_norm are only read when value is not
+ * NULL. Asynchronous on the context's stream; rows go through the nets in
+ * minibatch-sized chunks. */
+zl_status zl_ppo_act(zl_ppo* ppo, const float* obs_norm, const float* obs, int ld_obs,
+                     const float* critic_norm, const float* critic_obs, int ld_critic_obs,
+                     long long n, const float* eps, float* action, float* logp, float* mean,
+                     int ld_mean, float* value);
 /* Critic values for n rows of (normalised) critic obs, in minibatch-sized
  * chunks: values[i] (ActorCritic::value, zealot-rl/src/ppo.rs:290-294). */
 zl_status zl_ppo_values(zl_ppo* ppo, const float* critic_obs, int ld, long long n,

@@ -147,6 +147,10 @@ SIGNATURES = {
     "zl_norm_update": (C.c_int, [vp, vp, C.c_int, vp, C.c_int, C.c_longlong]),
     "zl_norm_commit": (C.c_int, [vp, vp, vp, C.c_int]),
     "zl_norm_normalize": (C.c_int, [vp, vp, C.c_int, vp, C.c_int, C.c_longlong, vp, C.c_int]),
+    "zl_ppo_act": (
+        C.c_int,
+        [vp, vp, vp, C.c_int, vp, vp, C.c_int, C.c_longlong, vp, vp, vp, vp, C.c_int, vp],
+    ),
     "zl_mlp_create": (C.c_int, [vp, ip, C.c_int, C.c_int, C.POINTER(vp)]),
     "zl_mlp_destroy": (None, [vp]),
     "zl_mlp_num_params": (C.c_longlong, [vp]),

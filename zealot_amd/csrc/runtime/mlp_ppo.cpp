@@ -1206,6 +1206,74 @@ static zl_status chunked_forward(zl_ppo* p, bool critic, const float* x, int ld,
   return ZL_OK;
 }
 
+zl_status zl_ppo_act(zl_ppo* p, const float* obs_norm, const float* obs, int ld_obs,
+                     const float* critic_norm, const float* cobs, int ld_cobs, long long n,
+                     const float* eps, float* action, float* logp, float* mean, int ld_mean,
+                     float* value) {
+  if (!p) return ZL_ERR_INVALID;
+  zl_ctx* c = p->c;
+  const int od = p->actor.dims[0], cd = p->critic.dims[0], A = p->A;
+  if (n < 0 || !obs || !eps || !action || !logp || ld_obs < od || (mean && ld_mean < A) ||
+      (value && (!cobs || ld_cobs < cd)) || (!value && critic_norm))
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_act: bad argument");
+  if (n == 0) return ZL_OK;
+  // Normalised inputs go to the padded staging buffers (16-byte aligned rows
+  // for the layer-0 GEMM); raw inputs that are already normalised are read
+  // in place.
+  const int odp = (int)round_up(od, 4), cdp = (int)round_up(cd, 4);
+  const int chunk = (int)std::min<long long>(p->mb_cap, n);
+  zl_status s = ZL_OK;
+  if (obs_norm) {
+    size_t cap = p->obs_pad_floats * 4;
+    if ((s = grow(c, (void**)&p->obs_pad, &cap, (size_t)chunk * odp * 4))) return s;
+    p->obs_pad_floats = cap / 4;
+  }
+  if (critic_norm) {
+    size_t cap = p->cobs_pad_floats * 4;
+    if ((s = grow(c, (void**)&p->cobs_pad, &cap, (size_t)chunk * cdp * 4))) return s;
+    p->cobs_pad_floats = cap / 4;
+  }
+  const int La = p->actor.L, Lc = p->critic.L;
+  for (long long r0 = 0; r0 < n; r0 += chunk) {
+    const int rows = (int)std::min<long long>(chunk, n - r0);
+    NetView v[2] = {{&p->actor, &p->ab, obs + (size_t)r0 * ld_obs, ld_obs},
+                    {&p->critic, &p->cb, value ? cobs + (size_t)r0 * ld_cobs : nullptr, ld_cobs}};
+    if (obs_norm) {
+      if ((s = zl_norm_normalize(c, obs_norm, od, v[0].x, ld_obs, rows, p->obs_pad, odp))) return s;
+      v[0].x = p->obs_pad;
+      v[0].ldx = odp;
+    }
+    if (critic_norm) {
+      if ((s = zl_norm_normalize(c, critic_norm, cd, v[1].x, ld_cobs, rows, p->cobs_pad, cdp)))
+        return s;
+      v[1].x = p->cobs_pad;
+      v[1].ldx = cdp;
+    }
+    s = value ? pair_forward(c, v, p->params, nullptr, rows, nullptr)
+              : net_forward(c, p->actor, p->ab, p->params, v[0].x, v[0].ldx, nullptr, rows, nullptr);
+    if (s) return s;
+    zk::SampleArgs sa{};
+    sa.mean = p->ab.act[La];
+    sa.ldm = p->ab.ld[La];
+    sa.log_std = p->params + p->ls_off;
+    sa.eps = eps + (size_t)r0 * A;
+    sa.action = action + (size_t)r0 * A;
+    sa.logp = logp + r0;
+    sa.rows = rows;
+    sa.A = A;
+    sa.lde = A;
+    sa.lda = A;
+    if ((s = launch(c, K_SAMPLE, (unsigned)cdiv(rows, kThreads), 1, 1, sa))) return s;
+    if (mean && (s = copy_rows(c, mean + (size_t)r0 * ld_mean, ld_mean, p->ab.act[La], p->ab.ld[La],
+                               A, rows, nullptr, 0, nullptr, false)))
+      return s;
+    if (value && (s = copy_rows(c, value + r0, 1, p->cb.act[Lc], p->cb.ld[Lc], 1, rows, nullptr, 0,
+                                nullptr, false)))
+      return s;
+  }
+  return ZL_OK;
+}
+
 zl_status zl_ppo_values(zl_ppo* p, const float* cobs, int ld, long long n, float* values) {
   if (!p) return ZL_ERR_INVALID;
   return chunked_forward(p, true, cobs, ld, n, values, 1, 1);

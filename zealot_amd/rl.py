@@ -321,6 +321,21 @@ class GpuActorCritic:
         self.ctx.check(self.ctx.lib.zl_ppo_get_grads(self.h, _fptr(ga), _fptr(gc), _fptr(gl)), "get_grads")
         return ga, gc, gl, dict(surrogate=st[0], value_loss=st[1], kl=st[2])
 
+    def act(self, obs, n: int, eps, action, logp, mean=None, value=None, critic_obs=None,
+            obs_norm: "GpuNormalizer | None" = None, critic_norm: "GpuNormalizer | None" = None,
+            ld_obs: int | None = None, ld_critic_obs: int | None = None, ld_mean: int | None = None):
+        """One rollout step for n envs (GpuPolicy::forward, src/biped/gpu_policy.rs:
+        210-248, with the trainer's sampling, src/bin/biped_train_gpu.rs:910-930):
+        normalise, actor mean, action = mean + exp(log_std) * eps, logp, and
+        (when `value` is given) the critic value, all on the device."""
+        ctx = self.ctx
+        ctx.check(ctx.lib.zl_ppo_act(
+            self.h, obs_norm.buf.p if obs_norm else None, _dptr(obs), int(ld_obs or self.actor_dims[0]),
+            critic_norm.buf.p if critic_norm else None, _dptr(critic_obs) if critic_obs is not None else None,
+            int(ld_critic_obs or self.critic_dims[0]), int(n), _dptr(eps), _dptr(action), _dptr(logp),
+            _dptr(mean) if mean is not None else None, int(ld_mean or self.action_dim),
+            _dptr(value) if value is not None else None), "zl_ppo_act")
+
     def values(self, critic_obs: DeviceBuffer, n: int, out: DeviceBuffer, ld: int | None = None):
         ld = self.critic_dims[0] if ld is None else ld
         self.ctx.check(self.ctx.lib.zl_ppo_values(self.h, critic_obs.p, ld, n, out.p), "zl_ppo_values")
