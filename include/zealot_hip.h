@@ -327,6 +327,38 @@ zl_status zl_ppo_act(zl_ppo* ppo, const float* obs_norm, const float* obs, int l
                      const float* critic_norm, const float* critic_obs, int ld_critic_obs,
                      long long n, const float* eps, float* action, float* logp, float* mean,
                      int ld_mean, float* value);
+/* ActorCritic::save (zealot-rl/src/ppo.rs:512-570): a .safetensors image with
+ * the reference's tensors (all F32) "actor.w_{l}" [out, in], "actor.b_{l}"
+ * [out], "critic.*" likewise, "log_std" [A], "obs_norm.mean" / ".m2" [dim],
+ * "obs_norm.count" [1], "critic_norm.*" likewise and "lr" [1]. obs_norm /
+ * critic_norm are normaliser states (zl_norm_*); NULL saves Normalizer::new.
+ * with_optimizer != 0 also writes the Adam moments ("adam_m.<net>.w_{l}",
+ * "adam_v.*", "adam_m.log_std", "adam_v.log_std", F32) and the step counters
+ * ("adam.t", "adam.gstep", I64 [1]), which the reference's load ignores.
+ * Blocks until the device state is read. */
+zl_status zl_ppo_save(zl_ppo* ppo, const float* obs_norm, const float* critic_norm,
+                      int with_optimizer, const char* path);
+/* The same image in memory: *size gets its byte count; buf may be NULL to
+ * query the size only; otherwise cap must be >= *size. */
+zl_status zl_ppo_save_bytes(zl_ppo* ppo, const float* obs_norm, const float* critic_norm,
+                            int with_optimizer, void* buf, size_t cap, size_t* size);
+/* ActorCritic::load / load_from_bytes (ppo.rs:572-650) into an existing
+ * handle whose net dims equal the file's (zl_checkpoint_dims reads them):
+ * params, log_std, lr, and the normaliser states into obs_norm / critic_norm
+ * (NULL skips one). The Adam state is reset as the reference's load does,
+ * unless restore_optimizer != 0 and the image carries the "adam.*" tensors,
+ * which are then restored. Tensors the loader reads must be F32 (I64 for the
+ * counters). Blocks until done. */
+zl_status zl_ppo_load(zl_ppo* ppo, float* obs_norm, float* critic_norm, int restore_optimizer,
+                      const char* path);
+zl_status zl_ppo_load_bytes(zl_ppo* ppo, float* obs_norm, float* critic_norm,
+                            int restore_optimizer, const void* buf, size_t size);
+/* Net dims of a checkpoint image (the reference's load reconstructs them from
+ * the weight shapes, ppo.rs:585-610): n_actor / n_critic get the counts;
+ * actor_dims / critic_dims (may be NULL) get the dims when count <= cap.
+ * Host only, no context; errors via zl_global_error. */
+zl_status zl_checkpoint_dims(const void* buf, size_t size, int* actor_dims, int* n_actor,
+                             int* critic_dims, int* n_critic, int cap);
 /* Critic values for n rows of (normalised) critic obs, in minibatch-sized
  * chunks: values[i] (ActorCritic::value, zealot-rl/src/ppo.rs:290-294). */
 zl_status zl_ppo_values(zl_ppo* ppo, const float* critic_obs, int ld, long long n,

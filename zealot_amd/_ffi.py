@@ -151,6 +151,11 @@ SIGNATURES = {
         C.c_int,
         [vp, vp, vp, C.c_int, vp, vp, C.c_int, C.c_longlong, vp, vp, vp, vp, C.c_int, vp],
     ),
+    "zl_ppo_save": (C.c_int, [vp, vp, vp, C.c_int, C.c_char_p]),
+    "zl_ppo_save_bytes": (C.c_int, [vp, vp, vp, C.c_int, vp, C.c_size_t, C.POINTER(C.c_size_t)]),
+    "zl_ppo_load": (C.c_int, [vp, vp, vp, C.c_int, C.c_char_p]),
+    "zl_ppo_load_bytes": (C.c_int, [vp, vp, vp, C.c_int, vp, C.c_size_t]),
+    "zl_checkpoint_dims": (C.c_int, [vp, C.c_size_t, ip, ip, ip, ip, C.c_int]),
     "zl_mlp_create": (C.c_int, [vp, ip, C.c_int, C.c_int, C.POINTER(vp)]),
     "zl_mlp_destroy": (None, [vp]),
     "zl_mlp_num_params": (C.c_longlong, [vp]),

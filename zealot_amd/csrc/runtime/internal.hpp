@@ -231,4 +231,12 @@ zl_status ensure_ws(zl_ctx* c, size_t floats);
 // out[k] = sum over b of part[k * blocks + b], k < width (zk_row_sum).
 zl_status reduce_rows(zl_ctx* c, const float* part, int width, int blocks, float* out);
 
+// zl_ppo internals for the checkpoint code (defined in mlp_ppo.cpp).
+zl_ctx* ppo_ctx(zl_ppo* p);
+void ppo_dims(const zl_ppo* p, std::vector<int>* actor, std::vector<int>* critic);
+// Packed moments (layout of zl_ppo_get_moments), all six non-NULL.
+zl_status ppo_set_moments(zl_ppo* p, const float* ma, const float* va, const float* mc,
+                          const float* vc, const float* mls, const float* vls);
+void ppo_set_counters(zl_ppo* p, int t, unsigned long long gstep);
+
 }  // namespace zl

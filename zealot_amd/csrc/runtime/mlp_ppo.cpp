@@ -1286,3 +1286,37 @@ zl_status zl_ppo_actor_mean(zl_ppo* p, const float* obs, int ld, long long n, fl
 }
 
 }  // extern "C"
+
+// ---- accessors for the checkpoint code (checkpoint.cpp)
+namespace zl {
+
+zl_ctx* ppo_ctx(zl_ppo* p) { return p->c; }
+
+void ppo_dims(const zl_ppo* p, std::vector<int>* actor, std::vector<int>* critic) {
+  *actor = p->actor.dims;
+  *critic = p->critic.dims;
+}
+
+zl_status ppo_set_moments(zl_ppo* p, const float* ma, const float* va, const float* mc,
+                          const float* vc, const float* mls, const float* vls) {
+  zl_ctx* c = p->c;
+  std::vector<float> hm((size_t)p->nflat, 0.0f), hv((size_t)p->nflat, 0.0f);
+  p->actor.scatter(ma, hm.data());
+  p->actor.scatter(va, hv.data());
+  p->critic.scatter(mc, hm.data());
+  p->critic.scatter(vc, hv.data());
+  std::memcpy(hm.data() + p->ls_off, mls, (size_t)p->A * 4);
+  std::memcpy(hv.data() + p->ls_off, vls, (size_t)p->A * 4);
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  ZL_HIP(c, hipMemcpyAsync(p->m, hm.data(), hm.size() * 4, hipMemcpyHostToDevice, c->stream));
+  ZL_HIP(c, hipMemcpyAsync(p->v, hv.data(), hv.size() * 4, hipMemcpyHostToDevice, c->stream));
+  ZL_HIP(c, hipStreamSynchronize(c->stream));
+  return ZL_OK;
+}
+
+void ppo_set_counters(zl_ppo* p, int t, unsigned long long gstep) {
+  p->hstate.t = t;
+  p->hstate.gstep = gstep;
+}
+
+}  // namespace zl

@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _ffi
-from .device import Context, DeviceBuffer
+from .device import Context, DeviceBuffer, ZealotError
 
 
 def _fptr(a: np.ndarray) -> C.c_void_p:
@@ -243,6 +243,18 @@ class GpuPendingNorm:
         return float(self.buf.numpy()[2 * self.dim])
 
 
+def checkpoint_dims(data: bytes):
+    """(actor dims, critic dims) of a checkpoint image (host only)."""
+    lib = _ffi.load_library()
+    cap = 64
+    ad, cd = (C.c_int * cap)(), (C.c_int * cap)()
+    na, nc = C.c_int(), C.c_int()
+    st = lib.zl_checkpoint_dims(data, len(data), ad, C.byref(na), cd, C.byref(nc), cap)
+    if st != _ffi.ZL_OK:
+        raise ZealotError(st, "zl_checkpoint_dims: " + lib.zl_global_error().decode())
+    return list(ad[:na.value]), list(cd[:nc.value])
+
+
 class GpuActorCritic:
     """The ActorCritic of zealot-rl/src/ppo.rs:208-229 resident on one MI355X:
     actor, critic, log_std and all Adam state in one flat HBM buffer, updated
@@ -263,6 +275,48 @@ class GpuActorCritic:
         self.h = h
         self.na = packed_count(self.actor_dims)
         self.nc = packed_count(self.critic_dims)
+        # Running normalisers of the policy and critic observations (ppo.rs:217-220).
+        self.obs_norm = GpuNormalizer(ctx, self.actor_dims[0])
+        self.critic_norm = GpuNormalizer(ctx, self.critic_dims[0])
+
+    def record_obs(self, obs, critic_obs, rows: int, ld_obs: int | None = None,
+                   ld_critic_obs: int | None = None):
+        """ActorCritic::record_obs (ppo.rs:276-279) for `rows` observation pairs, in order."""
+        self.obs_norm.update(obs, rows, ld_obs)
+        self.critic_norm.update(critic_obs, rows, ld_critic_obs)
+
+    def save(self, path: str, with_optimizer: bool = False):
+        """ActorCritic::save (ppo.rs:512-570) to a .safetensors file; with_optimizer
+        adds the Adam moments and counters (which the reference drops)."""
+        self.ctx.check(self.ctx.lib.zl_ppo_save(self.h, self.obs_norm.buf.p, self.critic_norm.buf.p,
+                                                int(with_optimizer), str(path).encode()), "zl_ppo_save")
+
+    def save_bytes(self, with_optimizer: bool = False) -> bytes:
+        n = C.c_size_t()
+        lib, on, cn = self.ctx.lib, self.obs_norm.buf.p, self.critic_norm.buf.p
+        self.ctx.check(lib.zl_ppo_save_bytes(self.h, on, cn, int(with_optimizer), None, 0, C.byref(n)),
+                       "zl_ppo_save_bytes")
+        buf = C.create_string_buffer(n.value)
+        self.ctx.check(lib.zl_ppo_save_bytes(self.h, on, cn, int(with_optimizer), buf, n.value, C.byref(n)),
+                       "zl_ppo_save_bytes")
+        return buf.raw[:n.value]
+
+    def load_into(self, data: bytes, restore_optimizer: bool = False):
+        """ActorCritic::load_from_bytes into this handle (dims must match)."""
+        self.ctx.check(self.ctx.lib.zl_ppo_load_bytes(self.h, self.obs_norm.buf.p, self.critic_norm.buf.p,
+                                                      int(restore_optimizer), data, len(data)),
+                       "zl_ppo_load_bytes")
+
+    @classmethod
+    def load(cls, ctx: Context, path: str, minibatch_rows: int,
+             restore_optimizer: bool = False) -> "GpuActorCritic":
+        """ActorCritic::load (ppo.rs:572-650): dims from the file's weight shapes."""
+        with open(path, "rb") as f:
+            data = f.read()
+        ad, cd = checkpoint_dims(data)
+        ac = cls(ctx, ad, cd, minibatch_rows)
+        ac.load_into(data, restore_optimizer)
+        return ac
 
     def set_params(self, actor, critic, log_std, lr: float):
         a = np.ascontiguousarray(actor, np.float32)
