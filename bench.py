@@ -61,6 +61,66 @@ def cpu_baseline(ro, actor, critic, log_std, mean_old, action, logp_old, values,
                       f"{threads} threads: {dt:.1f} s"}
 
 
+def _timed(ctx, fn, reps):
+    fn()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    ctx.synchronize()
+    return (time.perf_counter() - t0) / reps
+
+
+def aux_measurements(ctx, gac, ro, d_obs, ld, n):
+    """The rows around the update: the on-device rollout step (GpuPolicy::
+    forward + sampling for 4096 envs, the actor-inference configuration) and
+    the observation normaliser over one rollout step and over the whole
+    update batch. Wall time over repeated calls on the context stream."""
+    from zealot_amd import synth
+    from zealot_amd.rl import GpuNormalizer
+
+    ad, cd = synth.ACTOR_DIMS, synth.CRITIC_DIMS
+    od = ad[0]
+    envs = N_ENVS
+    obs_norm = GpuNormalizer(ctx, od)
+    obs_norm.update(d_obs, n, ld)  # a non-trivial transform
+    eps = ctx.to_device(ro["eps"][:envs])
+    act, lp, mean, val = ctx.alloc((envs, ad[-1])), ctx.alloc(envs), ctx.alloc((envs, ad[-1])), ctx.alloc(envs)
+    flop_actor = 2.0 * envs * sum(ad[l] * ad[l + 1] for l in range(len(ad) - 1))
+    flop_critic = 2.0 * envs * sum(cd[l] * cd[l + 1] for l in range(len(cd) - 1))
+    t_act = _timed(ctx, lambda: gac.act(d_obs, envs, eps, act, lp, ld_obs=ld, obs_norm=obs_norm), 50)
+    t_act_v = _timed(ctx, lambda: gac.act(d_obs, envs, eps, act, lp, mean=mean, value=val, critic_obs=d_obs,
+                                          obs_norm=obs_norm, critic_norm=obs_norm, ld_obs=ld,
+                                          ld_critic_obs=ld), 50)
+    staged = ctx.alloc((n, od))
+    t_norm = _timed(ctx, lambda: obs_norm.normalize(d_obs, n, staged, ld_x=ld, ld_out=od), 20)
+    scratch = GpuNormalizer(ctx, od)
+    t_upd_step = _timed(ctx, lambda: scratch.update(d_obs, envs, ld), 50)
+    t_upd_all = _timed(ctx, lambda: scratch.update(d_obs, n, ld), 20)
+    norm_bytes = 2.0 * n * od * 4  # read x once, write out once
+    return {
+        "rollout_step": {
+            "workload": f"{envs} envs: normalise obs [{envs}x{od}], actor {'-'.join(map(str, ad))}, "
+                        f"sample a = mean + exp(log_std) * eps, logp",
+            "us": t_act * 1e6, "envs_per_s": envs / t_act,
+            "gemm_tflops": flop_actor / t_act / 1e12,
+            "with_critic_value_us": t_act_v * 1e6,
+            "with_critic_gemm_tflops": (flop_actor + flop_critic) / t_act_v / 1e12,
+        },
+        "obs_normalize": {
+            "workload": f"Normalizer::normalize of the update batch [{n}x{od}]",
+            "us": t_norm * 1e6, "GBps": norm_bytes / t_norm / 1e9,
+            "hbm_frac": norm_bytes / t_norm / 8e12,
+        },
+        "obs_norm_update": {
+            "workload": f"Normalizer::update / PendingNorm::push of [{envs}x{od}] (one rollout step) and "
+                        f"[{n}x{od}] (the batch)",
+            "step_us": t_upd_step * 1e6, "batch_us": t_upd_all * 1e6,
+            "batch_GBps_one_read": n * od * 4 / t_upd_all / 1e9,
+        },
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -213,6 +273,7 @@ def main():
             "launches_per_step": dom_cnt,
         },
     }
+    out["aux"] = aux_measurements(ctx, gac, ro, d_obs, LD, n)
     if not args.no_cpu_baseline:
         mean_old = d_mean.numpy()
         action = d_act.numpy()

@@ -81,6 +81,10 @@ LARGE_CASES = [
     (13001, 1000, 132, False, True),
     (13001, 1000, 132, False, False),
     (70001, 130, 20, False, True),
+    # Rollout-size forwards: the tile shrinks until every CU has a workgroup
+    # (64x64 here, 32x64 when even that leaves CUs idle).
+    (4001, 300, 76, False, True),
+    (3001, 100, 132, False, True),
 ]
 
 

@@ -622,6 +622,8 @@ ZK_GEMM(zk_gemm_ak_bk_96x128x32_w22k2, true, true, 96, 128, 32, 2, 2, 2, true)
 ZK_GEMM(zk_gemm_ak_bk_128x128x32_w24, true, true, 128, 128, 32, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_128x128x32_w22, true, true, 128, 128, 32, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_128x128x16_w22, true, true, 128, 128, 16, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_64x64x32_w22, true, true, 64, 64, 32, 2, 2, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_32x64x32_w12, true, true, 32, 64, 32, 1, 2, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_96x32x32_w21, true, true, 96, 32, 32, 2, 1, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, 1, true)

@@ -44,13 +44,15 @@ __device__ void norm_set_body(const NormArgs& p) {
   p.state[i] = i < p.dim ? 0.0f : prior;
 }
 
-// Normalizer::normalize (ppo.rs:198-205), rows [blockIdx.x * kNormApplyRows,
+// Normalizer::normalize (ppo.rs:198-205), rows [blockIdx.x * rows_per_block,
 // ...): var = max(m2 / count, 1e-8), out = clamp((x - mean) / sqrt(var), -5, 5)
 // with correctly rounded division and square root. For dim <= 256 a pass
-// covers 256 / dim whole rows, each thread one fixed column.
+// covers 256 / dim whole rows, each thread one fixed column. Dynamic LDS:
+// 2 * dim floats (mean, sd).
 __device__ void norm_apply_body(const NormArgs& p) {
-  __shared__ float s_mean[kNormMaxDim];
-  __shared__ float s_sd[kNormMaxDim];
+  extern __shared__ float s_norm[];
+  float* s_mean = s_norm;
+  float* s_sd = s_norm + p.dim;
   const int t = threadIdx.x;
   const float count = p.state[2 * p.dim];
   for (int c = t; c < p.dim; c += kThreads) {
@@ -59,8 +61,8 @@ __device__ void norm_apply_body(const NormArgs& p) {
     s_sd[c] = sqrtf(var);
   }
   __syncthreads();
-  const long long r0 = (long long)blockIdx.x * kNormApplyRows;
-  const long long r1 = min(p.rows, r0 + kNormApplyRows);
+  const long long r0 = (long long)blockIdx.x * p.rows_per_block;
+  const long long r1 = min(p.rows, r0 + p.rows_per_block);
   if (p.dim <= kThreads) {
     const int g = kThreads / p.dim;  // rows per pass
     const int rr = t / p.dim, c = t - rr * p.dim;

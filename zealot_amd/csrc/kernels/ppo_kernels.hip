@@ -613,7 +613,41 @@ __device__ void copy_rows_body(const CopyRowsArgs& p) {
 }
 
 // ActorCritic::sample + logp (zealot-rl/src/ppo.rs:314-323, :297-305) with
-// the Gaussian noise supplied by the caller.
+// the Gaussian noise supplied by the caller, A <= G: a lane group of G lanes
+// per row, lane k on action component k (coalesced row reads and writes);
+// the logp terms are added in component order by the row's lane 0, as the
+// reference's sequential sum does.
+template <int G>
+__device__ void sample_lanes_body(const SampleArgs& p) {
+  constexpr int RPB = kThreads / G;  // rows per block
+  __shared__ float s_ls[G], s_sd[G];
+  __shared__ float s_term[kThreads];
+  if (p.guard && *p.guard == 0) return;
+  const int t = threadIdx.x, k = t % G, rr = t / G;
+  if (t < G && t < p.A) {
+    s_ls[t] = p.log_std[t];
+    s_sd[t] = expf(s_ls[t]);
+  }
+  __syncthreads();
+  const long long r = (long long)blockIdx.x * RPB + rr;
+  float term = 0.f;
+  if (r < p.rows && k < p.A) {
+    const float mu = p.mean[r * p.ldm + k];
+    const float a = mu + s_sd[k] * p.eps[r * p.lde + k];
+    p.action[r * p.lda + k] = a;
+    const float d = (a - mu) / s_sd[k];
+    term = -0.5f * d * d - s_ls[k] - kLogSqrt2Pi;
+  }
+  s_term[t] = term;
+  __syncthreads();
+  if (k == 0 && r < p.rows) {
+    float lp = 0.f;
+    for (int j = 0; j < p.A; ++j) lp += s_term[rr * G + j];
+    p.logp[r] = lp;
+  }
+}
+
+// Any A: one thread per row.
 __device__ void sample_body(const SampleArgs& p) {
   if (p.guard && *p.guard == 0) return;
   const int r = blockIdx.x * kThreads + threadIdx.x;
@@ -668,4 +702,6 @@ ZK_KERNEL(zk_elu_backward, EluBwdArgs, elu_backward_body)
 ZK_KERNEL(zk_row_sum, RowSumArgs, row_sum_body)
 ZK_KERNEL(zk_copy_rows, CopyRowsArgs, copy_rows_body)
 ZK_KERNEL(zk_sample, SampleArgs, sample_body)
+extern "C" __global__ __launch_bounds__(256) void zk_sample_g32(zk::SampleArgs p) { zk::sample_lanes_body<32>(p); }
+extern "C" __global__ __launch_bounds__(256) void zk_sample_g64(zk::SampleArgs p) { zk::sample_lanes_body<64>(p); }
 ZK_KERNEL(zk_clamp, ClampArgs, clamp_body)

@@ -280,7 +280,6 @@ struct SampleArgs {
 // with count 0 is empty (its mean and m2 are zero).
 constexpr int kNormMaxDim = 4096;
 constexpr int kNormChunkRows = 256;    // rows per partial-statistics chunk
-constexpr int kNormApplyRows = 256;    // rows per zk_norm_apply block
 constexpr int kNormFoldThreads = 1024;  // zk_norm_merge / zk_norm_commit block
 struct NormArgs {
   const float* x;   // [rows x ldx]
@@ -290,6 +289,7 @@ struct NormArgs {
   float* part;      // [nchunks x 2 x dim]: per chunk mean[dim], then M2[dim]
   long long rows;
   int dim, ldx, ldo, nchunks;
+  int rows_per_block;  // zk_norm_apply
   int unit_prior;   // zk_norm_set: 1 = Normalizer::new, 0 = empty pending state
 };
 

@@ -39,6 +39,8 @@ enum KernelId : int {
   K_NORM_STATS,
   K_NORM_MERGE,
   K_NORM_COMMIT,
+  K_SAMPLE_G32,
+  K_SAMPLE_G64,
   K_GEMM_BASE
 };
 
@@ -230,6 +232,8 @@ zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r);
 zl_status ensure_ws(zl_ctx* c, size_t floats);
 // out[k] = sum over b of part[k * blocks + b], k < width (zk_row_sum).
 zl_status reduce_rows(zl_ctx* c, const float* part, int width, int blocks, float* out);
+// Sampling + logp (zk_sample_g32 / _g64 for A <= 32 / 64, else zk_sample).
+zl_status launch_sample(zl_ctx* c, const zk::SampleArgs& a);
 
 // zl_ppo internals for the checkpoint code (defined in mlp_ppo.cpp).
 zl_ctx* ppo_ctx(zl_ppo* p);

@@ -1263,7 +1263,7 @@ zl_status zl_ppo_act(zl_ppo* p, const float* obs_norm, const float* obs, int ld_
     sa.A = A;
     sa.lde = A;
     sa.lda = A;
-    if ((s = launch(c, K_SAMPLE, (unsigned)cdiv(rows, kThreads), 1, 1, sa))) return s;
+    if ((s = launch_sample(c, sa))) return s;
     if (mean && (s = copy_rows(c, mean + (size_t)r0 * ld_mean, ld_mean, p->ab.act[La], p->ab.ld[La],
                                A, rows, nullptr, 0, nullptr, false)))
       return s;

@@ -79,7 +79,12 @@ zl_status zl_norm_normalize(zl_ctx* c, const float* state, int dim, const float*
   a.dim = dim;
   a.ldx = ld_x;
   a.ldo = ld_out;
-  return launch(c, K_NORM_APPLY, (unsigned)cdiv(rows, zk::kNormApplyRows), 1, 1, a);
+  // One batch of 4 loads per thread for dim <= 256 (4 passes of 256 / dim
+  // rows), 8 rows per block otherwise: thousands of blocks for a rollout
+  // batch, enough to fill the chip for one env step.
+  a.rows_per_block = dim <= kThreads ? 4 * (kThreads / dim) : 8;
+  return launch(c, K_NORM_APPLY, (unsigned)cdiv(rows, a.rows_per_block), 1, 1, a,
+                (unsigned)(2 * dim * sizeof(float)));
 }
 
 }  // extern "C"

@@ -19,7 +19,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_adam",          "zk_epoch_begin", "zk_kl",         "zk_epoch_end",   "zk_gae",
     "zk_adv_norm",      "zk_elu_backward", "zk_row_sum",   "zk_copy_rows",   "zk_sample",
     "zk_clamp",         "zk_reduce_all",  "zk_actor_loss_g64", "zk_norm_set",   "zk_norm_apply",
-    "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit",
+    "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
 };
 
 // {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
@@ -31,6 +31,8 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bk_128x128x32_w24", true, true, 128, 128, 32, 512, true},
     {"zk_gemm_ak_bk_128x128x32_w22", true, true, 128, 128, 32, 256, true},
     {"zk_gemm_ak_bk_128x128x16_w22", true, true, 128, 128, 16, 256, true},
+    {"zk_gemm_ak_bk_64x64x32_w22", true, true, 64, 64, 32, 256, true},
+    {"zk_gemm_ak_bk_32x64x32_w12", true, true, 32, 64, 32, 128, true},
     {"zk_gemm_ak_bk_128x32x16_w41", true, true, 128, 32, 16, 256, true},
     {"zk_gemm_ak_bk_96x32x32_w21", true, true, 96, 32, 32, 128, true},
     {"zk_gemm_ak_bk_256x16x16_w41", true, true, 256, 16, 16, 256, true},
@@ -165,8 +167,20 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
         name = "zk_gemm_ak_bk_256x16x16_w41";
       else if (N <= 32)
         name = "zk_gemm_ak_bk_128x32x16_w41";
-      else
-        name = M >= 4096 ? "zk_gemm_ak_bk_96x128x32_w24" : "zk_gemm_ak_bk_64x128x16_w22";
+      else {
+        // Largest tile that still gives every CU a workgroup (small-batch
+        // forwards such as a 4096-env rollout step), else the smallest.
+        static const char* const kFill[4] = {"zk_gemm_ak_bk_96x128x32_w24", "zk_gemm_ak_bk_64x128x16_w22",
+                                             "zk_gemm_ak_bk_64x64x32_w22", "zk_gemm_ak_bk_32x64x32_w12"};
+        static const int kTile[4][2] = {{96, 128}, {64, 128}, {64, 64}, {32, 64}};
+        int pick = 3;
+        for (int i = 0; i < 4; ++i)
+          if (cdiv(M, kTile[i][0]) * cdiv(N, kTile[i][1]) >= 256) {
+            pick = i;
+            break;
+          }
+        name = kFill[pick];
+      }
       break;
     case L_AK_BN:
       // Data gradients (ELU' epilogue) take the variant that prefetches the
@@ -424,6 +438,12 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
 }
 
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d) { return run_gemm_batch(c, &d, 1); }
+
+zl_status launch_sample(zl_ctx* c, const zk::SampleArgs& a) {
+  if (a.A <= 32) return launch(c, K_SAMPLE_G32, (unsigned)cdiv(a.rows, kThreads / 32), 1, 1, a);
+  if (a.A <= 64) return launch(c, K_SAMPLE_G64, (unsigned)cdiv(a.rows, kThreads / 64), 1, 1, a);
+  return launch(c, K_SAMPLE, (unsigned)cdiv(a.rows, kThreads), 1, 1, a);
+}
 
 // Sum the component-major [width x blocks] partials of zk_actor_loss over
 // blocks into out[width] (zk_row_sum, fixed order).
@@ -1127,7 +1147,7 @@ zl_status zl_sample_actions(zl_ctx* c, const float* mean, int ld_mean, const flo
   a.ldm = ld_mean;
   a.lde = A;
   a.lda = A;
-  return launch(c, K_SAMPLE, (unsigned)cdiv(rows, kThreads), 1, 1, a);
+  return launch_sample(c, a);
 }
 
 }  // extern "C"
