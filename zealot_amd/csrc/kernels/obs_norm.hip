@@ -5,8 +5,9 @@
 // one observation at a time (Welford); here a batch of rows is cut into
 // chunks of kNormChunkRows, each chunk's mean and sum of squared deviations
 // are taken two-pass in a fixed order (zk_norm_stats), and the chunks are
-// merged into the state in row order with the parallel-Welford (Chan) update
-// that Normalizer::commit uses (zk_norm_merge). mean and m2 therefore agree
+// merged with the parallel-Welford (Chan) update that Normalizer::commit uses:
+// contiguous runs of chunks in row order, then the state with the runs in
+// order (zk_norm_merge). mean and m2 therefore agree
 // with the one-at-a-time fold to fp32 rounding, not bit for bit; count
 // follows the reference exactly (see count_add_ones). zk_norm_commit and
 // zk_norm_apply repeat the reference's operation order and are bit-exact.
@@ -144,37 +145,62 @@ __device__ void norm_stats_body(const NormArgs& p) {
   }
 }
 
-// Fold the chunks into the state in row order (one block). Each merge is
-// the Chan update with Normalizer::commit's operation order (ppo.rs:186-190);
-// an empty state (count 0, a pending one) takes the first chunk as is.
-__device__ void norm_merge_body(const NormArgs& p) {
-  const int t = threadIdx.x;
-  const float count0 = p.state[2 * p.dim];
-  for (int c = t; c < p.dim; c += kNormFoldThreads) {
-    float mean = p.state[c], m2 = p.state[p.dim + c];
-    float n1 = count0;
-    for (int k = 0; k < p.nchunks; ++k) {
-      const long long r0 = (long long)k * kNormChunkRows;
-      const float n2 = (float)(min(p.rows, r0 + kNormChunkRows) - r0);
-      const float cm = p.part[(long long)(2 * k) * p.dim + c];
-      const float cq = p.part[(long long)(2 * k + 1) * p.dim + c];
-      if (n1 == 0.0f) {
-        mean = cm;
-        m2 = cq;
-        n1 = n2;
-        continue;
-      }
-      const float tot = n1 + n2;
-      const float d = cm - mean;
-      mean += d * n2 / tot;
-      m2 += cq + d * d * n1 * n2 / tot;
-      n1 = tot;
-    }
-    p.state[c] = mean;
-    p.state[p.dim + c] = m2;
+// Chan merge of (n2, m_b, q_b) into (n1, mean, m2), in Normalizer::commit's
+// operation order (ppo.rs:186-190); an empty left side takes the right one.
+__device__ __forceinline__ void chan_merge(float& n1, float& mean, float& m2, float n2, float mb,
+                                           float qb) {
+  if (n2 == 0.0f) return;
+  if (n1 == 0.0f) {
+    n1 = n2;
+    mean = mb;
+    m2 = qb;
+    return;
   }
-  __syncthreads();  // every thread has read count0
-  if (t == 0) p.state[2 * p.dim] = count_add_ones(count0, p.rows);
+  const float tot = n1 + n2;
+  const float d = mb - mean;
+  mean += d * n2 / tot;
+  m2 += qb + d * d * n1 * n2 / tot;
+  n1 = tot;
+}
+
+// Fold the chunks into the state (one block). Each column has T threads
+// (T = the largest power of two <= 1024 / dim, at most 32); thread j merges
+// the j-th contiguous run of chunks in row order, then the column's first
+// thread merges the state with the T runs in order. The order is fixed, so
+// the result is the same on every run.
+__device__ void norm_merge_body(const NormArgs& p) {
+  __shared__ float s_part[kNormFoldThreads][3];
+  const int t = threadIdx.x;
+  int T = 1;
+  while (T < 32 && 2 * T * p.dim <= kNormFoldThreads) T *= 2;
+  const int per = (p.nchunks + T - 1) / T;
+  const float count0 = p.state[2 * p.dim];
+  const int cols_per_pass = kNormFoldThreads / T;
+  for (int c0 = 0; c0 < p.dim; c0 += cols_per_pass) {
+    const int c = c0 + t / T, j = t % T;
+    float n = 0.0f, mean = 0.0f, m2 = 0.0f;
+    if (c < p.dim) {
+      const int k1 = min(p.nchunks, (j + 1) * per);
+      for (int k = j * per; k < k1; ++k) {
+        const long long r0 = (long long)k * kNormChunkRows;
+        const float n2 = (float)(min(p.rows, r0 + kNormChunkRows) - r0);
+        chan_merge(n, mean, m2, n2, p.part[(long long)(2 * k) * p.dim + c],
+                   p.part[(long long)(2 * k + 1) * p.dim + c]);
+      }
+    }
+    s_part[t][0] = n;
+    s_part[t][1] = mean;
+    s_part[t][2] = m2;
+    __syncthreads();
+    if (c < p.dim && j == 0) {
+      float n1 = count0, sm = p.state[c], sq = p.state[p.dim + c];
+      for (int i = 0; i < T; ++i) chan_merge(n1, sm, sq, s_part[t + i][0], s_part[t + i][1], s_part[t + i][2]);
+      p.state[c] = sm;
+      p.state[p.dim + c] = sq;
+    }
+    __syncthreads();
+  }
+  if (t == 0) p.state[2 * p.dim] = count_add_ones(count0, p.rows);  // count0 read by all above
 }
 
 // Normalizer::commit (ppo.rs:179-195): merge the pending state, then empty it.
