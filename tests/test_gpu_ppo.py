@@ -155,6 +155,34 @@ def test_minibatch_grads_with_perm(ctx, hidden, n, start, mb):
     assert e_gpu <= TOL
 
 
+@pytest.mark.parametrize("ad,cd", [([37, 64, 160, 40], [37, 64, 160, 1]),   # H > 128, A > 32
+                                   ([37, 96, 30, 3], [37, 96, 30, 1])])      # H = 30: padded tile
+def test_minibatch_grads_head_variants(ctx, ad, cd):
+    """Output layers outside the fused head kernel's range (last hidden width
+    > 128 or more than 32 actions: separate head GEMMs and loss kernels) and
+    inside it with a hidden width that is not a multiple of 16."""
+    g = np.random.default_rng(17)
+    actor = synth.kaiming_uniform_net(g, ad, 0.1)
+    critic = synth.kaiming_uniform_net(g, cd, 0.1)
+    n = 3000
+    batch, log_std = make_batch(n, ad, cd, actor, critic, seed=5)
+    move_off_branch_boundaries(batch, ad, cd, actor, critic, log_std)
+    gac = GpuActorCritic(ctx, ad, cd, n)
+    gac.set_params(actor, critic, log_std, 1e-3)
+    db = DeviceBatch(ctx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
+                     batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
+    ga, gc, gl, st = gac.minibatch_grads(db, PpoConfig(entropy_coef=0.01), 0, n)
+    idx = np.arange(n)
+    ra, rc, rl, rst = zo.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
+    _, _, tl, _ = np_ref.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
+    e = (per_tensor_err(ad, ga, ra), per_tensor_err(cd, gc, rc), rel_amax(gl, tl))
+    print(f"[gpu] head variant {ad} / {cd}: actor {e[0]:.2e} critic {e[1]:.2e} log_std {e[2]:.2e}", flush=True)
+    assert max(e) <= TOL
+    assert abs(st["surrogate"] - rst[0]) <= 1e-4 * max(1, abs(rst[0]))
+    assert abs(st["value_loss"] - rst[1]) <= 1e-4 * max(1, abs(rst[1]))
+    gac.close()
+
+
 def _param_delta_report(p0, pg, pc, lr, steps):
     dg, dc = (pg - p0).astype(np.float64), (pc - p0).astype(np.float64)
     diff = np.abs(dg - dc)

@@ -1,0 +1,349 @@
+// head.hip — the output layer of the actor and the critic fused with the PPO
+// losses of one minibatch (zealot-rl/src/ppo.rs:410-451, net.rs:88-140 for
+// the last layer): per tile of kHeadRows rows, the head forward, the actor's
+// clipped surrogate / the critic's clipped value loss, the head's data
+// gradient times ELU' of the last hidden activations (dL/dz of the last
+// hidden layer), and the head's weight and bias gradients as per-block
+// partials. The activations of a tile are read once into LDS and every
+// intermediate (means, their gradients) stays there. All sums run in a fixed
+// order, so the results are the same on every run.
+#pragma once
+#include "common.hip"
+#include "ppo_kernels.hip"
+
+namespace zk {
+
+// Block barrier for LDS only: this wave's LDS writes complete, then
+// s_barrier. Unlike __syncthreads it does not wait for outstanding global
+// loads and stores, so the loss inputs stay in flight across the forward and
+// the stores drain in the background.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+constexpr int kHeadPitch = kHeadMaxHidden + 4;  // LDS row pitch of the activation tile
+constexpr int kHeadDPitch = kHeadMaxActions + 4;
+constexpr int kHeadLds =
+    kHeadRows * kHeadPitch + kHeadMaxActions * kHeadPitch + kHeadRows * kHeadDPitch + 8 * 34;
+
+// Rows [r0, r0 + nr) of x into sx (kHeadRows x kHeadPitch), zero past nr
+// rows and past H columns (up to kHeadMaxHidden).
+__device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, int nr, float* sx) {
+  constexpr int QPR = kHeadMaxHidden / 4;  // float4 quads per row
+  for (int i = threadIdx.x; i < kHeadRows * QPR; i += kThreads) {
+    const int r = i / QPR, c = (i % QPR) * 4;
+    float4 v = {0.f, 0.f, 0.f, 0.f};
+    if (r < nr && c < q.H) {
+      v = *reinterpret_cast<const float4*>(q.x + (r0 + r) * q.ldx + c);
+      if (c + 1 >= q.H) v.y = 0.f;
+      if (c + 2 >= q.H) v.z = 0.f;
+      if (c + 3 >= q.H) v.w = 0.f;
+    }
+    *reinterpret_cast<float4*>(sx + r * kHeadPitch + c) = v;
+  }
+}
+
+__device__ void head_actor(const HeadArgs& p, float* smem) {
+  const HeadNet& q = p.net[0];
+  float* sx = smem;                                      // activations [R x pitch]
+  float* sw = sx + kHeadRows * kHeadPitch;               // weights [32 x pitch], rows >= A zero
+  float* sd = sw + kHeadMaxActions * kHeadPitch;         // means, then dL/dmean [R x dpitch]
+  float* sred = sd + kHeadRows * kHeadDPitch;            // [8 groups][34]
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int A = p.A, H = q.H;
+
+  for (int i = t; i < kHeadMaxActions * (kHeadMaxHidden / 4); i += kThreads) {
+    const int m = i / (kHeadMaxHidden / 4), c = (i % (kHeadMaxHidden / 4)) * 4;
+    float4 v = {0.f, 0.f, 0.f, 0.f};
+    if (m < A && c < H) {
+      v.x = q.w[(long long)m * q.ldw + c];
+      v.y = c + 1 < H ? q.w[(long long)m * q.ldw + c + 1] : 0.f;
+      v.z = c + 2 < H ? q.w[(long long)m * q.ldw + c + 2] : 0.f;
+      v.w = c + 3 < H ? q.w[(long long)m * q.ldw + c + 3] : 0.f;
+    }
+    *reinterpret_cast<float4*>(sw + m * kHeadPitch + c) = v;
+  }
+
+  // Loss lanes: 8 groups of 32, lane k on action component k.
+  const int grp = t >> 5, k = t & 31, base = (t & 63) - k;
+  const bool on = k < A;
+  const float ls = on ? p.log_std[k] : 0.f;
+  const float sdv = expf(ls);
+  const float inv_var = expf(-2.0f * ls);
+  const float inv_sd = expf(-ls);
+  const float lo = 1.0f - p.clip, hi = 1.0f + p.clip;
+  float gacc = 0.f, sacc = 0.f, kacc = 0.f;
+  float dbias = 0.f;  // thread t < 32: bias gradient of component t
+  floatx4 wacc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) wacc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  struct In {
+    float act, lpo, adv, mo;
+  };
+  constexpr int RG = kHeadRows / 8;  // rows per loss group
+  const long long ntiles = (p.rows + kHeadRows - 1) / kHeadRows;
+  for (int tt = 0; tt < p.tiles_per_block; ++tt) {
+    const long long tile = blockIdx.x + (long long)tt * gridDim.x;
+    if (tile >= ntiles) break;  // uniform
+    const long long r0 = tile * kHeadRows;
+    const int nr = (int)min((long long)kHeadRows, p.rows - r0);
+    // Loss inputs of the group's rows, in flight during the tile load and
+    // the forward (group g takes rows g, g + 8, ...).
+    In in[RG];
+#pragma unroll
+    for (int j = 0; j < RG; ++j) {
+      const int row = grp + 8 * j;
+      In x{0.f, 0.f, 0.f, 0.f};
+      if (row < nr) {
+        const long long s = p.perm ? p.perm[p.row0 + r0 + row] : (long long)(p.row0 + r0 + row);
+        x.act = on ? p.action[s * p.ldact + k] : 0.f;
+        x.lpo = p.logp_old[s];
+        x.adv = p.adv[s];
+        x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
+      }
+      in[j] = x;
+    }
+    lds_barrier();  // the previous tile's LDS reads are done
+    head_load_tile(q, r0, nr, sx);
+    lds_barrier();
+
+    // Head forward: wave w computes rows 16w..16w+15, components 0..31.
+    {
+      floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+      for (int c16 = 0; c16 < kHeadMaxHidden / 16; ++c16) {
+        const float4 af = *reinterpret_cast<const float4*>(sx + (16 * wave + lr) * kHeadPitch + 16 * c16 + 4 * lg);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const float4 bf = *reinterpret_cast<const float4*>(sw + (16 * j + lr) * kHeadPitch + 16 * c16 + 4 * lg);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc[j], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int m = 16 * j + lr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * wave + 4 * lg + r;
+          const float mu = m < A ? acc[j][r] + q.b[m] : 0.f;
+          sd[row * kHeadDPitch + m] = mu;
+          if (m < A && row < nr) q.out[(r0 + row) * q.ldo + m] = mu;
+        }
+      }
+    }
+    lds_barrier();
+
+    // Losses (ppo.rs:411-432, as zk_actor_loss).
+    {
+#pragma unroll
+      for (int j = 0; j < RG; ++j) {
+        const int row = grp + 8 * j;
+        if (row >= nr) {  // group-uniform
+          sd[row * kHeadDPitch + k] = 0.f;
+          continue;
+        }
+        const float mu = sd[row * kHeadDPitch + k];
+        const float act = in[j].act;
+        const float dz = (act - mu) / sdv;
+        const float lp = lanes_sum_ordered<32>(on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f, base, A);
+        const float ratio = expf(lp - in[j].lpo);
+        const float a = in[j].adv;
+        const float surr = fminf(ratio * a, clampf(ratio, lo, hi) * a);
+        const bool clipped = (a >= 0.0f && ratio > hi) || (a < 0.0f && ratio < lo);
+        float gm = 0.f, cc = 0.f;
+        if (!clipped) {
+          const float d = act - mu;
+          gm = -(a * ratio * d * inv_var) * p.scale;
+          const float dls = a * ratio * ((d * d) * inv_var - 1.0f);
+          cc = -dls * p.scale;
+        }
+        cc += -p.entropy_coef * p.scale;
+        if (on) gacc += cc;
+        sacc += surr * p.scale;
+        if (p.mean_old) {
+          const float y = (mu - in[j].mo) * inv_sd;
+          kacc += lanes_sum_ordered<32>(on ? 0.5f * (y * y) : 0.f, base, A) * p.scale;
+        }
+        sd[row * kHeadDPitch + k] = on ? gm : 0.f;  // the group's own row: no other reader yet
+      }
+    }
+    lds_barrier();
+
+    // Data gradient of the head times ELU' of the activations: wave w, rows
+    // 16w..16w+15, all hidden columns.
+    {
+      floatx4 dacc[kHeadMaxHidden / 16];
+#pragma unroll
+      for (int j = 0; j < kHeadMaxHidden / 16; ++j) dacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c16 = 0; c16 < kHeadMaxActions / 16; ++c16) {
+        const float4 af = *reinterpret_cast<const float4*>(sd + (16 * wave + lr) * kHeadDPitch + 16 * c16 + 4 * lg);
+        const float* wr = sw + (16 * c16 + 4 * lg) * kHeadPitch + lr;
+#pragma unroll
+        for (int j = 0; j < kHeadMaxHidden / 16; ++j) {
+          dacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, wr[16 * j], dacc[j], 0, 0, 0);
+          dacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, wr[kHeadPitch + 16 * j], dacc[j], 0, 0, 0);
+          dacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, wr[2 * kHeadPitch + 16 * j], dacc[j], 0, 0, 0);
+          dacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, wr[3 * kHeadPitch + 16 * j], dacc[j], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kHeadMaxHidden / 16; ++j) {
+        const int n = 16 * j + lr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * wave + 4 * lg + r;
+          if (row < nr && n < H)
+            q.dz[(r0 + row) * q.ldz + n] = dacc[j][r] * elu_grad_from_act(sx[row * kHeadPitch + n]);
+        }
+      }
+    }
+
+    // Weight gradient partial dW += dmean^T . x over this tile's rows: wave w
+    // takes hidden columns 32w..32w+31; the bias gradient is the column sum.
+#pragma unroll
+    for (int r16 = 0; r16 < kHeadRows / 16; ++r16) {
+      float av[2][4], bv[2][4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int row = 16 * r16 + 4 * lg + c;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) av[i][c] = sd[row * kHeadDPitch + 16 * i + lr];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) bv[j][c] = sx[row * kHeadPitch + 32 * wave + 16 * j + lr];
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            wacc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][c], bv[j][c], wacc[i][j], 0, 0, 0);
+    }
+    if (t < kHeadMaxActions)
+      for (int row = 0; row < kHeadRows; ++row) dbias += sd[row * kHeadDPitch + t];
+  }
+
+  // Partials of this block.
+  const int blk = blockIdx.x, nblk = gridDim.x;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = 32 * wave + 16 * j + lr;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * i + 4 * lg + r;
+        if (m < A && n < H) q.wpart[((long long)blk * A + m) * H + n] = wacc[i][j][r];
+      }
+    }
+  if (t < A) q.bpart[(long long)blk * A + t] = dbias;
+  sred[grp * 34 + k] = gacc;
+  if (k == 0) {
+    sred[grp * 34 + 32] = sacc;
+    sred[grp * 34 + 33] = kacc;
+  }
+  lds_barrier();
+  if (t < A) {
+    float g = 0.f;
+    for (int j = 0; j < 8; ++j) g += sred[j * 34 + t];
+    p.gls_part[(long long)t * nblk + blk] = g;
+  } else if (t == 64 || t == 65) {
+    const int qq = t - 64;
+    float v = 0.f;
+    for (int j = 0; j < 8; ++j) v += sred[j * 34 + 32 + qq];
+    p.astat_part[(long long)qq * nblk + blk] = v;
+  }
+}
+
+__device__ void head_critic(const HeadArgs& p, float* smem) {
+  const HeadNet& q = p.net[1];
+  float* sx = smem;
+  float* sw = sx + kHeadRows * kHeadPitch;  // w[0..H)
+  float* sdv = sw + kHeadMaxActions * kHeadPitch;  // dL/dvalue per row
+  float* sred = sdv + kHeadRows * kHeadDPitch;
+  const int t = threadIdx.x;
+  const int H = q.H;
+  for (int i = t; i < kHeadMaxHidden; i += kThreads) sw[i] = i < H ? q.w[i] : 0.f;
+  const float bias = q.b[0];
+  float vacc = 0.f, dw = 0.f, db = 0.f;
+  const long long ntiles = (p.rows + kHeadRows - 1) / kHeadRows;
+  for (int tt = 0; tt < p.tiles_per_block; ++tt) {
+    const long long tile = blockIdx.x + (long long)tt * gridDim.x;
+    if (tile >= ntiles) break;  // uniform
+    const long long r0 = tile * kHeadRows;
+    const int nr = (int)min((long long)kHeadRows, p.rows - r0);
+    const int row = t >> 2, u = t & 3;
+    float vo = 0.f, R = 0.f;  // loss inputs, in flight during the tile load
+    if (u == 0 && row < nr) {
+      const long long s = p.perm ? p.perm[p.row0 + r0 + row] : (long long)(p.row0 + r0 + row);
+      vo = p.value_old[s];
+      R = p.ret[s];
+    }
+    lds_barrier();
+    head_load_tile(q, r0, nr, sx);
+    lds_barrier();
+    // value = b + sum_k w_k x_k: four lanes per row, 32 columns each, then
+    // the four partial sums in order.
+    {
+      float part = 0.f;
+      for (int c = 32 * u; c < 32 * u + 32; ++c) part += sx[row * kHeadPitch + c] * sw[c];
+      const int l0 = (t & 63) & ~3;
+      const float p0 = __shfl(part, l0, 64), p1 = __shfl(part, l0 + 1, 64);
+      const float p2 = __shfl(part, l0 + 2, 64), p3 = __shfl(part, l0 + 3, 64);
+      if (u == 0) {
+        float dv = 0.f;
+        if (row < nr) {
+          const float v = bias + (((p0 + p1) + p2) + p3);
+          q.out[(r0 + row) * q.ldo] = v;
+          // ppo.rs:436-450, as zk_value_loss.
+          const float vc = vo + clampf(v - vo, -p.clip, p.clip);
+          const float lu = (v - R) * (v - R);
+          const float lc = (vc - R) * (vc - R);
+          float vloss, g;
+          if (lc > lu) {
+            vloss = lc;
+            g = 2.0f * (vc - R);
+          } else {
+            vloss = lu;
+            g = 2.0f * (v - R);
+          }
+          vacc += vloss * p.scale;
+          dv = p.value_coef * g * p.scale;
+        }
+        sdv[row] = dv;
+      }
+    }
+    lds_barrier();
+    for (int e = t; e < kHeadRows * kHeadMaxHidden; e += kThreads) {
+      const int row = e / kHeadMaxHidden, n = e % kHeadMaxHidden;
+      if (row < nr && n < H)
+        q.dz[(r0 + row) * q.ldz + n] = (sdv[row] * sw[n]) * elu_grad_from_act(sx[row * kHeadPitch + n]);
+    }
+    if (t < kHeadMaxHidden) {
+      for (int row = 0; row < kHeadRows; ++row) dw += sdv[row] * sx[row * kHeadPitch + t];
+    } else if (t == kThreads - 1) {
+      for (int row = 0; row < kHeadRows; ++row) db += sdv[row];
+    }
+  }
+  const int blk = blockIdx.x;
+  if (t < H) q.wpart[(long long)blk * H + t] = dw;
+  if (t == kThreads - 1) q.bpart[blk] = db;
+  const float tot = block_sum(vacc, sred);
+  if (t == 0) p.vstat_part[blk] = tot;
+}
+
+}  // namespace zk
+
+extern "C" __global__ __launch_bounds__(256) void zk_head(zk::HeadArgs p) {
+  __shared__ __align__(16) float smem[zk::kHeadLds];
+  if (p.guard && *p.guard == 0) return;
+  if (blockIdx.z == 0)
+    zk::head_actor(p, smem);
+  else
+    zk::head_critic(p, smem);
+}

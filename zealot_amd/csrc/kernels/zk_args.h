@@ -154,6 +154,43 @@ struct ValueLossArgs {
   float clip, value_coef, scale;
 };
 
+// zk_head: the output layer of both nets fused with the PPO losses for one
+// minibatch (blockIdx.z: 0 actor, 1 critic). Tiles of kHeadRows rows are
+// strided over the blocks of a net; the last hidden width is at most
+// kHeadMaxHidden and the action dim at most kHeadMaxActions.
+constexpr int kHeadRows = 64;
+constexpr int kHeadMaxBlocks = 512;
+constexpr int kHeadMaxHidden = 128;
+constexpr int kHeadMaxActions = 32;
+struct HeadNet {
+  const float* x;  // [rows x ldx] last hidden activations (after ELU)
+  const float* w;  // [nout x ldw] output-layer weights
+  const float* b;  // [nout]
+  float* out;      // [rows x ldo] output (actor mean / critic value)
+  float* dz;       // [rows x ldz] dL/dz of the last hidden layer
+  float* wpart;    // [blocks x nout x H] weight-gradient partials
+  float* bpart;    // [blocks x nout] bias-gradient partials
+  int ldx, ldw, ldo, ldz, H;
+};
+struct HeadArgs {
+  HeadNet net[2];
+  const float* action;    // [n x ldact]
+  const float* logp_old;  // [n]
+  const float* adv;       // [n]
+  const float* mean_old;  // [n x ldmo], nullable
+  const float* log_std;   // [A]
+  const float* value_old; // [n]
+  const float* ret;       // [n]
+  const int* perm;        // sample = perm ? perm[row0 + r] : row0 + r
+  float* gls_part;        // [A x blocks] log_std gradient partials
+  float* astat_part;      // [2 x blocks] surrogate, kl partials
+  float* vstat_part;      // [blocks] value-loss partials
+  const int* guard;
+  long long rows;
+  int row0, A, ldact, ldmo, tiles_per_block;
+  float clip, entropy_coef, value_coef, scale;
+};
+
 struct SumsqArgs {
   const float* x;
   float* part;           // one partial per block

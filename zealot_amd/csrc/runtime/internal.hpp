@@ -34,6 +34,7 @@ enum KernelId : int {
   K_CLAMP,
   K_REDUCE_ALL,
   K_ACTOR_LOSS_G64,
+  K_HEAD,
   K_NORM_SET,
   K_NORM_APPLY,
   K_NORM_STATS,

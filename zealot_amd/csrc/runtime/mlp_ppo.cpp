@@ -232,7 +232,17 @@ struct NetView {
 // Forward of both nets, layer by layer, each layer's two GEMMs in one launch
 // when the nets have the same depth (otherwise one after the other).
 static zl_status pair_forward(zl_ctx* c, const NetView v[2], const float* params,
-                              const int* permx, int rows, const int* guard) {
+                              const int* permx, int rows, const int* guard, int layers = -1) {
+  if (layers >= 0 && v[0].nl->L == v[1].nl->L) {
+    for (int l = 0; l < layers; ++l) {
+      GemmDesc d[2];
+      for (int i = 0; i < 2; ++i)
+        d[i] = fwd_desc(*v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard, l);
+      zl_status s = run_gemm_batch(c, d, 2);
+      if (s) return s;
+    }
+    return ZL_OK;
+  }
   if (v[0].nl->L != v[1].nl->L) {
     for (int i = 0; i < 2; ++i) {
       zl_status s = net_forward(c, *v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard);
@@ -256,15 +266,19 @@ static zl_status pair_forward(zl_ctx* c, const NetView v[2], const float* params
 struct PartialPlan {
   std::vector<size_t> off[2], size[2];
   size_t total = 0;
-  void build(const zl_ctx* c, const NetLayout* nl[2], int rows) {
+  // With fused_head the output layer's region holds zk_head's per-block
+  // partials: weights [kHeadMaxBlocks x out x in], then biases [.. x out].
+  void build(const zl_ctx* c, const NetLayout* nl[2], int rows, bool fused_head) {
     total = 0;
     for (int i = 0; i < 2; ++i) {
       off[i].assign(nl[i]->L, 0);
       size[i].assign(nl[i]->L, 0);
       for (int l = 0; l < nl[i]->L; ++l) {
         off[i][l] = total;
-        size[i][l] = gemm_ws_floats(c, nl[i]->dims[l + 1], nl[i]->dims[l], rows, false, false,
-                                    zk::kEpiStore);
+        const long long M = nl[i]->dims[l + 1], N = nl[i]->dims[l];
+        size[i][l] = fused_head && l == nl[i]->L - 1
+                         ? (size_t)zk::kHeadMaxBlocks * (M * N + M)
+                         : gemm_ws_floats(c, (int)M, (int)N, rows, false, false, zk::kEpiStore);
         total += round_up((long long)size[i][l], 64);
       }
     }
@@ -278,10 +292,10 @@ struct PartialPlan {
 static zl_status pair_backward(zl_ctx* c, const NetView v[2], const float* params, float* grads,
                                const int* permx, int rows, const float* const top[2],
                                const int ld_top[2], const int* guard, float* pws,
-                               const PartialPlan& pp, zk::ReduceSeg* segs) {
+                               const PartialPlan& pp, zk::ReduceSeg* segs, int depth0 = 0) {
   const int L[2] = {v[0].nl->L, v[1].nl->L};
   const bool paired = L[0] == L[1];
-  for (int depth = 0; depth < std::max(L[0], L[1]); ++depth) {
+  for (int depth = depth0; depth < std::max(L[0], L[1]); ++depth) {
     GemmDesc w[2], d[2];
     int nw = 0, nd = 0;
     for (int i = 0; i < 2; ++i) {
@@ -493,6 +507,10 @@ struct zl_ppo {
   float *params = nullptr, *grads = nullptr, *m = nullptr, *v = nullptr;
   NetBuffers ab, cb;
   int mb_cap = 0;
+  // The output layers and the losses run as one zk_head launch (last hidden
+  // widths <= kHeadMaxHidden, A <= kHeadMaxActions, equal depths;
+  // ZL_FUSED_HEAD=0 turns it off).
+  bool fused_head = false;
   // Reduction partials.
   float* gls_part = nullptr;  // [nb x A]
   float* astat_part = nullptr;
@@ -543,7 +561,7 @@ zl_status grow(zl_ctx* c, void** p, size_t* cap, size_t bytes) {
 // and grow their buffer (outside graph capture: may synchronize).
 zl_status ensure_partials(zl_ppo* p, int rows) {
   const NetLayout* nls[2] = {&p->actor, &p->critic};
-  p->pplan.build(p->c, nls, rows);
+  p->pplan.build(p->c, nls, rows, p->fused_head);
   size_t cap = p->pws_cap * 4;
   zl_status s = grow(p->c, (void**)&p->pws, &cap, p->pplan.total * 4 + 4);
   p->pws_cap = cap / 4;
@@ -553,15 +571,37 @@ zl_status ensure_partials(zl_ppo* p, int rows) {
 // Backward of both nets for one minibatch plus the all-layer reduction with
 // the grad-norm partials; nsq / nsq_a receive the partial counts (all, actor).
 zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, int rows,
-                              const int* guard, int* nsq, int* nsq_a) {
+                              const int* guard, int* nsq, int* nsq_a, int head_blocks) {
   zl_ctx* c = p->c;
   const int La = p->actor.L, Lc = p->critic.L;
   const float* top[2] = {p->ab.delta[La - 1], p->cb.delta[Lc - 1]};
   const int ldt[2] = {p->ab.ld[La], p->cb.ld[Lc]};
   zk::ReduceSeg segs[zk::kMaxReduceSegs];
+  // With the fused head, zk_head has produced dL/dz of the last hidden layers
+  // and the output layers' gradient partials: the backward starts one layer
+  // down and the output layers' segments describe those partials.
   zl_status s = pair_backward(c, v, p->params, p->grads, permx, rows, top, ldt, guard, p->pws,
-                              p->pplan, segs);
+                              p->pplan, segs, head_blocks > 0 ? 1 : 0);
   if (s) return s;
+  if (head_blocks > 0) {
+    for (int i = 0; i < 2; ++i) {
+      const NetLayout& nl = i == 0 ? p->actor : p->critic;
+      const int l = nl.L - 1;
+      const long long M = nl.dims[l + 1], N = nl.dims[l];
+      float* part = p->pws + p->pplan.off[i][l];
+      zk::ReduceSeg& r = segs[i * La + l];
+      r = zk::ReduceSeg{};
+      r.part = part;
+      r.rowpart = part + (size_t)zk::kHeadMaxBlocks * M * N;
+      r.out = p->grads + nl.w_off[l];
+      r.rowout = p->grads + nl.b_off[l];
+      r.mn = M * N;
+      r.cols = (int)N;
+      r.ldo = nl.ldw[l];
+      r.rows = (int)M;
+      r.splits = head_blocks;
+    }
+  }
   zk::ReduceSeg lay[zk::kMaxReduceSegs];
   std::copy(segs, segs + La + Lc, lay);
   const int blocks = reduce_all_layout(lay, La + Lc);
@@ -570,6 +610,120 @@ zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, i
   *nsq = blocks;
   *nsq_a = lay[La].blk0;
   return launch_reduce_all(c, segs, La + Lc, p->sq_part, guard);
+}
+
+// Loss-partial and grad-norm-partial counts of one minibatch pass.
+struct PassCounts {
+  int nb_a = 0, nb_v = 0, nsq = 0, nsq_a = 0;
+};
+
+// One minibatch: forward of both nets, the PPO losses, backward, and the
+// all-layer reduction with the grad-norm partials (the accumulation of
+// zealot-rl/src/ppo.rs:406-462 before clip / Adam). `px` gathers the
+// layer-0 rows; samples of the batch are perm[row0 + r] (or row0 + r).
+zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int* perm, int row0,
+                         int rows, const zl_batch* b, const zl_ppo_config* cfg, float scale,
+                         const int* guard, PassCounts* pc) {
+  zl_ctx* c = p->c;
+  const int La = p->actor.L, Lc = p->critic.L, A = p->A;
+  zl_status s = pair_forward(c, v, p->params, px, rows, guard, p->fused_head ? La - 1 : -1);
+  if (s) return s;
+  int head_blocks = 0;
+  if (p->fused_head) {
+    const long long tiles = cdiv(rows, zk::kHeadRows);
+    const long long tpb = cdiv(tiles, zk::kHeadMaxBlocks);
+    head_blocks = (int)cdiv(tiles, tpb);
+    zk::HeadArgs h{};
+    for (int i = 0; i < 2; ++i) {
+      const NetLayout& nl = i == 0 ? p->actor : p->critic;
+      const NetBuffers& nb = i == 0 ? p->ab : p->cb;
+      const int l = nl.L - 1;
+      zk::HeadNet& q = h.net[i];
+      q.x = nb.act[l];
+      q.ldx = nb.ld[l];
+      q.w = p->params + nl.w_off[l];
+      q.ldw = nl.ldw[l];
+      q.b = p->params + nl.b_off[l];
+      q.out = nb.act[l + 1];
+      q.ldo = nb.ld[l + 1];
+      q.dz = nb.delta[l - 1];
+      q.ldz = nb.ld[l];
+      q.H = nl.dims[l];
+      q.wpart = p->pws + p->pplan.off[i][l];
+      q.bpart = q.wpart + (size_t)zk::kHeadMaxBlocks * nl.dims[l + 1] * nl.dims[l];
+    }
+    h.action = b->action;
+    h.ldact = b->ld_action;
+    h.logp_old = b->logp_old;
+    h.adv = b->adv;
+    h.mean_old = b->mean_old;
+    h.ldmo = b->ld_mean_old;
+    h.log_std = p->params + p->ls_off;
+    h.value_old = b->value_old;
+    h.ret = b->ret;
+    h.perm = perm;
+    h.row0 = row0;
+    h.rows = rows;
+    h.A = A;
+    h.tiles_per_block = (int)tpb;
+    h.clip = cfg->clip;
+    h.entropy_coef = cfg->entropy_coef;
+    h.value_coef = cfg->value_coef;
+    h.scale = scale;
+    h.gls_part = p->gls_part;
+    h.astat_part = p->astat_part;
+    h.vstat_part = p->vstat_part;
+    h.guard = guard;
+    if ((s = launch(c, K_HEAD, (unsigned)head_blocks, 1, 2, h))) return s;
+    pc->nb_a = pc->nb_v = head_blocks;
+  } else {
+    const LossShape lsh = actor_loss_shape(rows, A);
+    zk::ActorLossArgs al{};
+    al.mean = p->ab.act[La];
+    al.ldm = p->ab.ld[La];
+    al.action = b->action;
+    al.ldact = b->ld_action;
+    al.adv = b->adv;
+    al.logp_old = b->logp_old;
+    al.mean_old = b->mean_old;
+    al.ldmo = b->ld_mean_old;
+    al.log_std = p->params + p->ls_off;
+    al.perm = perm;
+    al.row0 = row0;
+    al.rows = rows;
+    al.A = A;
+    al.delta = p->ab.delta[La - 1];
+    al.ldd = p->ab.ld[La];
+    al.gls_part = p->gls_part;
+    al.stat_part = p->astat_part;
+    al.guard = guard;
+    al.clip = cfg->clip;
+    al.entropy_coef = cfg->entropy_coef;
+    al.scale = scale;
+    al.rows_per_block = lsh.rows_per_block;
+    al.group = lsh.group;
+    if ((s = launch(c, lsh.kernel, (unsigned)lsh.blocks, 1, 1, al, 0, zk::kLossThreads))) return s;
+    const int nbv = (int)cdiv(rows, kThreads);
+    zk::ValueLossArgs vl{};
+    vl.v = p->cb.act[Lc];
+    vl.ldv = p->cb.ld[Lc];
+    vl.value_old = b->value_old;
+    vl.ret = b->ret;
+    vl.perm = perm;
+    vl.row0 = row0;
+    vl.rows = rows;
+    vl.delta = p->cb.delta[Lc - 1];
+    vl.ldd = p->cb.ld[Lc];
+    vl.stat_part = p->vstat_part;
+    vl.guard = guard;
+    vl.clip = cfg->clip;
+    vl.value_coef = cfg->value_coef;
+    vl.scale = scale;
+    if ((s = launch(c, K_VALUE_LOSS, (unsigned)nbv, 1, 1, vl))) return s;
+    pc->nb_a = lsh.blocks;
+    pc->nb_v = nbv;
+  }
+  return backward_and_reduce(p, v, px, rows, guard, &pc->nsq, &pc->nsq_a, head_blocks);
 }
 
 struct Plan {
@@ -603,9 +757,8 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
                   pl.n, nullptr, 0, guard, true);
     if (s) return s;
   }
-  const int La = p->actor.L, Lc = p->critic.L;
+  const int La = p->actor.L;
   const int nb = (int)cdiv(pl.mb, kThreads);
-  const LossShape ls_shape = actor_loss_shape(pl.mb, A);
   const float* log_std = p->params + p->ls_off;
   for (int e = 0; e < pl.epochs; ++e) {
     zk::EpochBeginArgs eb{};
@@ -620,54 +773,12 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       const float* xa = perm_e ? pl.X : pl.X + (size_t)row0 * pl.ldx;
       const float* xc = perm_e ? pl.XC : pl.XC + (size_t)row0 * pl.ldxc;
       const NetView v[2] = {{&p->actor, &p->ab, xa, pl.ldx}, {&p->critic, &p->cb, xc, pl.ldxc}};
-      if ((s = pair_forward(c, v, p->params, px, pl.mb, guard))) return s;
-      zk::ActorLossArgs al{};
-      al.mean = p->ab.act[La];
-      al.ldm = p->ab.ld[La];
-      al.action = b->action;
-      al.ldact = b->ld_action;
-      al.adv = b->adv;
-      al.logp_old = b->logp_old;
-      al.mean_old = b->mean_old;
-      al.ldmo = b->ld_mean_old;
-      al.log_std = log_std;
-      al.perm = perm_e;
-      al.row0 = row0;
-      al.rows = pl.mb;
-      al.A = A;
-      al.delta = p->ab.delta[La - 1];
-      al.ldd = p->ab.ld[La];
-      al.gls_part = p->gls_part;
-      al.stat_part = p->astat_part;
-      al.guard = guard;
-      al.clip = cfg->clip;
-      al.entropy_coef = cfg->entropy_coef;
-      al.scale = pl.pp.scale;
-      al.rows_per_block = ls_shape.rows_per_block;
-      al.group = ls_shape.group;
-      if ((s = launch(c, ls_shape.kernel, (unsigned)ls_shape.blocks, 1, 1, al, 0, zk::kLossThreads)))
-        return s;
-      zk::ValueLossArgs vl{};
-      vl.v = p->cb.act[Lc];
-      vl.ldv = p->cb.ld[Lc];
-      vl.value_old = b->value_old;
-      vl.ret = b->ret;
-      vl.perm = perm_e;
-      vl.row0 = row0;
-      vl.rows = pl.mb;
-      vl.delta = p->cb.delta[Lc - 1];
-      vl.ldd = p->cb.ld[Lc];
-      vl.stat_part = p->vstat_part;
-      vl.guard = guard;
-      vl.clip = cfg->clip;
-      vl.value_coef = cfg->value_coef;
-      vl.scale = pl.pp.scale;
-      if ((s = launch(c, K_VALUE_LOSS, (unsigned)nb, 1, 1, vl))) return s;
-      int nsq = 0, nsq_a = 0;
-      if ((s = backward_and_reduce(p, v, px, pl.mb, guard, &nsq, &nsq_a))) return s;
+      PassCounts pc;
+      if ((s = minibatch_pass(p, v, px, perm_e, row0, pl.mb, b, cfg, pl.pp.scale, guard, &pc))) return s;
+      const int nsq = pc.nsq, nsq_a = pc.nsq_a;
       {
         auto ch = [](long long n) { return cdiv(n, zk::kFinalizeChunk); };
-        const long long chunks = (2 + A) * ch(ls_shape.blocks) + ch(nb) + ch(nsq_a) + ch(nsq - nsq_a);
+        const long long chunks = (2 + A) * ch(pc.nb_a) + ch(pc.nb_v) + ch(nsq_a) + ch(nsq - nsq_a);
         if (chunks > zk::kFinalizeMaxChunks)
           return fail(c, ZL_ERR_INVALID, "finalize: %lld partial chunks > %d", chunks,
                       zk::kFinalizeMaxChunks);
@@ -682,8 +793,8 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       fz.g_logstd = p->grads + p->ls_off;
       fz.guard = guard;
       fz.pp = pl.pp;
-      fz.nb_a = ls_shape.blocks;
-      fz.nb_v = nb;
+      fz.nb_a = pc.nb_a;
+      fz.nb_v = pc.nb_v;
       fz.nsq = nsq;
       fz.nsq_a = nsq_a;
       if ((s = launch(c, K_FINALIZE, 1, 1, 1, fz, 0, zk::kFinalizeThreads))) return s;
@@ -767,6 +878,12 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
   p->ls_off = p->critic.end;
   p->nflat = p->ls_off + round_up(p->A, 64);
   p->mb_cap = mb;
+  {
+    const int ha = adims[na - 2], hc = cdims[nc - 2];
+    const char* env = getenv("ZL_FUSED_HEAD");
+    p->fused_head = na == nc && na >= 3 && ha <= zk::kHeadMaxHidden && hc <= zk::kHeadMaxHidden &&
+                    p->A <= zk::kHeadMaxActions && !(env && atoi(env) == 0);
+  }
   const size_t bytes = (size_t)p->nflat * 4;
   zl_status s = ZL_OK;
   auto dalloc = [&](void** ptr, size_t nbytes) {
@@ -781,7 +898,8 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
   dalloc((void**)&p->v, bytes);
   if (!s) s = p->ab.alloc(c, p->actor, mb);
   if (!s) s = p->cb.alloc(c, p->critic, mb);
-  p->nb_cap = (int)std::max<long long>(cdiv(mb, kThreads), kLossMaxBlocks);
+  p->nb_cap = (int)std::max<long long>(std::max<long long>(cdiv(mb, kThreads), kLossMaxBlocks),
+                                         zk::kHeadMaxBlocks);
   dalloc((void**)&p->gls_part, (size_t)p->nb_cap * p->A * 4);
   dalloc((void**)&p->astat_part, (size_t)p->nb_cap * 2 * 4);
   dalloc((void**)&p->vstat_part, (size_t)p->nb_cap * 4);
@@ -1115,54 +1233,13 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
   if ((s = copy_rows(c, p->cobs_pad, cdp, b->critic_obs, b->ld_critic_obs, cd, rows, perm_dev,
                      (int)row0, nullptr, true)))
     return s;
-  const int La = p->actor.L, Lc = p->critic.L, A = p->A;
-  const int nb = (int)cdiv(rows, kThreads);
+  const int A = p->A;
   if ((s = ensure_partials(p, rows))) return s;
   const NetView v[2] = {{&p->actor, &p->ab, p->obs_pad, odp}, {&p->critic, &p->cb, p->cobs_pad, cdp}};
-  if ((s = pair_forward(c, v, p->params, nullptr, rows, nullptr))) return s;
-  const float scale = 1.0f / (float)rows;
-  zk::ActorLossArgs al{};
-  al.mean = p->ab.act[La];
-  al.ldm = p->ab.ld[La];
-  al.action = b->action;
-  al.ldact = b->ld_action;
-  al.adv = b->adv;
-  al.logp_old = b->logp_old;
-  al.mean_old = b->mean_old;
-  al.ldmo = b->ld_mean_old;
-  al.log_std = p->params + p->ls_off;
-  al.perm = perm_dev;
-  al.row0 = (int)row0;
-  al.rows = rows;
-  al.A = A;
-  al.delta = p->ab.delta[La - 1];
-  al.ldd = p->ab.ld[La];
-  al.gls_part = p->gls_part;
-  al.stat_part = p->astat_part;
-  al.clip = cfg->clip;
-  al.entropy_coef = cfg->entropy_coef;
-  al.scale = scale;
-  const LossShape lsh = actor_loss_shape(rows, A);
-  al.rows_per_block = lsh.rows_per_block;
-  al.group = lsh.group;
-  if ((s = launch(c, lsh.kernel, (unsigned)lsh.blocks, 1, 1, al, 0, zk::kLossThreads))) return s;
-  zk::ValueLossArgs vl{};
-  vl.v = p->cb.act[Lc];
-  vl.ldv = p->cb.ld[Lc];
-  vl.value_old = b->value_old;
-  vl.ret = b->ret;
-  vl.perm = perm_dev;
-  vl.row0 = (int)row0;
-  vl.rows = rows;
-  vl.delta = p->cb.delta[Lc - 1];
-  vl.ldd = p->cb.ld[Lc];
-  vl.stat_part = p->vstat_part;
-  vl.clip = cfg->clip;
-  vl.value_coef = cfg->value_coef;
-  vl.scale = scale;
-  if ((s = launch(c, K_VALUE_LOSS, (unsigned)nb, 1, 1, vl))) return s;
-  int nsq = 0, nsq_a = 0;
-  if ((s = backward_and_reduce(p, v, nullptr, rows, nullptr, &nsq, &nsq_a))) return s;
+  PassCounts pc;
+  if ((s = minibatch_pass(p, v, nullptr, perm_dev, (int)row0, rows, b, cfg, 1.0f / (float)rows,
+                          nullptr, &pc)))
+    return s;
   // Fixed-order sums of the per-block partials.
   auto reduce = [&](const float* part, int width, int parts, float* out) {
     zk::SplitReduceArgs r{};
@@ -1174,9 +1251,9 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
     r.splits = parts;
     return launch_splitk_reduce(c, r);
   };
-  if ((s = reduce_rows(c, p->gls_part, A, lsh.blocks, p->grads + p->ls_off))) return s;
-  if ((s = reduce_rows(c, p->astat_part, 2, lsh.blocks, p->stat_out))) return s;
-  if ((s = reduce(p->vstat_part, 1, nb, p->stat_out + 2))) return s;
+  if ((s = reduce_rows(c, p->gls_part, A, pc.nb_a, p->grads + p->ls_off))) return s;
+  if ((s = reduce_rows(c, p->astat_part, 2, pc.nb_a, p->stat_out))) return s;
+  if ((s = reduce(p->vstat_part, 1, pc.nb_v, p->stat_out + 2))) return s;
   float h[3];
   ZL_HIP(c, hipMemcpyAsync(h, p->stat_out, sizeof(h), hipMemcpyDeviceToHost, c->stream));
   ZL_HIP(c, hipStreamSynchronize(c->stream));

@@ -18,7 +18,8 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_splitk_reduce", "zk_actor_loss",  "zk_value_loss", "zk_sumsq",       "zk_finalize",
     "zk_adam",          "zk_epoch_begin", "zk_kl",         "zk_epoch_end",   "zk_gae",
     "zk_adv_norm",      "zk_elu_backward", "zk_row_sum",   "zk_copy_rows",   "zk_sample",
-    "zk_clamp",         "zk_reduce_all",  "zk_actor_loss_g64", "zk_norm_set",   "zk_norm_apply",
+    "zk_clamp",         "zk_reduce_all",  "zk_actor_loss_g64", "zk_head",       "zk_norm_set",
+    "zk_norm_apply",
     "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
 };
 
