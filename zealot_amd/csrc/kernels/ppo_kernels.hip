@@ -219,100 +219,50 @@ __device__ void sumsq_body(const SumsqArgs& p) {
 __device__ void finalize_body(const FinalizeArgs& p) {
   // Quantities 0..4: surrogate, kl, value loss, actor and critic squared
   // norms; 5..5+A-1: the log_std gradient, each a sum over per-block
-  // partials. Every quantity's partials are cut into chunks of kChunk terms;
-  // chunk i is summed by wavefront i % 16 (lane-strided, fixed order), and
-  // each quantity then adds its chunk sums in chunk order: a fixed grouping,
-  // so the result is deterministic.
+  // partials. A group of 32 lanes takes quantities g, g + 32, ...: lane l
+  // adds partials l, l + 32, ... in order (loads issued 8 at a time), then
+  // the group's lanes are combined by a fixed butterfly, so the result is
+  // deterministic.
   constexpr int kMaxA = 256;
-  constexpr int kChunk = kFinalizeChunk;
-  constexpr int kMaxChunks = kFinalizeMaxChunks;
   __shared__ float q[5 + kMaxA];
-  __shared__ float cs[kMaxChunks];
   if (p.guard && *p.guard == 0) return;
   const int t = threadIdx.x;
   const int wave = t >> 6, lane = t & 63;
   const int A = p.pp.A;
   const int nq = 5 + A;
-  auto range = [&](int j, const float*& ptr, int& n, int& stride) {
+  const int grp = t >> 5, gln = t & 31;
+  constexpr int kGroups = kFinalizeThreads / 32;
+  for (int j = grp; j < nq; j += kGroups) {
+    const float* ptr;
+    int n;
     if (j == 0) {
-      ptr = p.astat_part, n = p.nb_a, stride = 1;
+      ptr = p.astat_part, n = p.nb_a;
     } else if (j == 1) {
-      ptr = p.astat_part + p.nb_a, n = p.nb_a, stride = 1;
+      ptr = p.astat_part + p.nb_a, n = p.nb_a;
     } else if (j == 2) {
-      ptr = p.vstat_part, n = p.nb_v, stride = 1;
+      ptr = p.vstat_part, n = p.nb_v;
     } else if (j == 3) {
-      ptr = p.sq_part, n = p.nsq_a, stride = 1;
+      ptr = p.sq_part, n = p.nsq_a;
     } else if (j == 4) {
-      ptr = p.sq_part + p.nsq_a, n = p.nsq - p.nsq_a, stride = 1;
+      ptr = p.sq_part + p.nsq_a, n = p.nsq - p.nsq_a;
     } else {
-      ptr = p.gls_part + (long long)(j - 5) * p.nb_a, n = p.nb_a, stride = 1;
+      ptr = p.gls_part + (long long)(j - 5) * p.nb_a, n = p.nb_a;
     }
-  };
-  int total = 0;
-  for (int j = 0; j < nq; ++j) {
-    const float* ptr;
-    int n, stride;
-    range(j, ptr, n, stride);
-    total += (n + kChunk - 1) / kChunk;
-  }
-  // A wavefront takes its chunks (wave, wave + 16, ...) four at a time and
-  // issues all their loads before adding: one memory latency per four chunks.
-  // Within a chunk lane l adds terms l, l + 64, ... in order.
-  constexpr int kW = kFinalizeThreads / 64, kB = 4, kPer = kChunk / 64;
-  for (int cb = wave; cb < total; cb += kW * kB) {
-    float tv[kB][kPer];
-    int len[kB];
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const int ci = cb + kW * b;
-      len[b] = 0;
-      if (ci >= total) continue;
-      int j = 0, first = 0, nch = 0;
-      const float* ptr = nullptr;
-      int n = 0, stride = 1;
-      for (;; ++j) {  // the quantity owning chunk ci (uniform over the wave)
-        range(j, ptr, n, stride);
-        nch = (n + kChunk - 1) / kChunk;
-        if (ci < first + nch) break;
-        first += nch;
-      }
-      const int c0 = (ci - first) * kChunk;
-      len[b] = min(kChunk, n - c0);
-#pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        const int i = lane + 64 * u;
-        tv[b][u] = i < len[b] ? ptr[(long long)(c0 + i) * stride] : 0.f;
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < kB; ++b) {
-      const int ci = cb + kW * b;
-      if (ci >= total) continue;
-      float v = 0.f;
-#pragma unroll
-      for (int u = 0; u < kPer; ++u)
-        if (lane + 64 * u < len[b]) v += tv[b][u];
-      v = wave_sum(v);
-      if (lane == 0) cs[ci] = v;
-    }
-  }
-  __syncthreads();
-  if (t < nq) {
-    int first = 0;
-    for (int j = 0; j < t; ++j) {
-      const float* ptr;
-      int n, stride;
-      range(j, ptr, n, stride);
-      first += (n + kChunk - 1) / kChunk;
-    }
-    const float* ptr;
-    int n, stride;
-    range(t, ptr, n, stride);
-    const int nch = (n + kChunk - 1) / kChunk;
     float v = 0.f;
-    for (int i = 0; i < nch; ++i) v += cs[first + i];
-    q[t] = v;
-    if (t >= 5) p.g_logstd[t - 5] = v;
+    for (int i0 = gln; i0 < n; i0 += 8 * 32) {
+      float tv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) tv[u] = i0 + 32 * u < n ? ptr[i0 + 32 * u] : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (i0 + 32 * u < n) v += tv[u];
+    }
+#pragma unroll
+    for (int m = 16; m > 0; m >>= 1) v = v + __shfl_xor(v, m, 32);
+    if (gln == 0) {
+      q[j] = v;
+      if (j >= 5) p.g_logstd[j - 5] = v;
+    }
   }
   __syncthreads();
   if (wave != 0) return;

@@ -7,14 +7,12 @@
 
 namespace zk {
 
-// zk_finalize: one block of 16 wavefronts; every per-block partial sum is cut
-// into chunks of kFinalizeChunk terms, at most kFinalizeMaxChunks in total.
+// zk_finalize: one block of 16 wavefronts (32 lane groups, one quantity each
+// at a time).
 constexpr int kFinalizeThreads = 1024;
 // Block sizes of zk_actor_loss (32 lane groups) and zk_reduce_all.
 constexpr int kLossThreads = 1024;
 constexpr int kReduceAllThreads = 1024;
-constexpr int kFinalizeChunk = 512;
-constexpr int kFinalizeMaxChunks = 1024;
 
 enum EpiMode : int {
   kEpiStore = 0,    // C = acc

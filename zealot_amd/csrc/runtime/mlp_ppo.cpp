@@ -776,13 +776,6 @@ zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       PassCounts pc;
       if ((s = minibatch_pass(p, v, px, perm_e, row0, pl.mb, b, cfg, pl.pp.scale, guard, &pc))) return s;
       const int nsq = pc.nsq, nsq_a = pc.nsq_a;
-      {
-        auto ch = [](long long n) { return cdiv(n, zk::kFinalizeChunk); };
-        const long long chunks = (2 + A) * ch(pc.nb_a) + ch(pc.nb_v) + ch(nsq_a) + ch(nsq - nsq_a);
-        if (chunks > zk::kFinalizeMaxChunks)
-          return fail(c, ZL_ERR_INVALID, "finalize: %lld partial chunks > %d", chunks,
-                      zk::kFinalizeMaxChunks);
-      }
       zk::FinalizeArgs fz{};
       fz.st = p->dstate;
       fz.gls_part = p->gls_part;
