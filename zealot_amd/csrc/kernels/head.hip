@@ -41,6 +41,25 @@ __device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, i
   }
 }
 
+// Sum over a row's 32 components in component order, every lane of the
+// 32-lane group getting the result: lane k stores its term in the row's LDS
+// slot k (components >= A hold 0, and adding 0 changes no sum), then each
+// lane reads the row back as 8 broadcast float4 loads. LDS instructions of
+// one wavefront execute in order, so no barrier is needed.
+__device__ __forceinline__ float row_sum_ordered(float* srow, int k, float term) {
+  srow[k] = term;
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < kHeadMaxActions / 4; ++c) {
+    const float4 v = *reinterpret_cast<const float4*>(srow + 4 * c);
+    s += v.x;
+    s += v.y;
+    s += v.z;
+    s += v.w;
+  }
+  return s;
+}
+
 __device__ void head_actor(const HeadArgs& p, float* smem) {
   const HeadNet& q = p.net[0];
   float* sx = smem;                                      // activations [R x pitch]
@@ -64,7 +83,7 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   }
 
   // Loss lanes: 8 groups of 32, lane k on action component k.
-  const int grp = t >> 5, k = t & 31, base = (t & 63) - k;
+  const int grp = t >> 5, k = t & 31;
   const bool on = k < A;
   const float ls = on ? p.log_std[k] : 0.f;
   const float sdv = expf(ls);
@@ -146,10 +165,11 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
           sd[row * kHeadDPitch + k] = 0.f;
           continue;
         }
-        const float mu = sd[row * kHeadDPitch + k];
+        float* srow = sd + row * kHeadDPitch;
+        const float mu = srow[k];
         const float act = in[j].act;
         const float dz = (act - mu) / sdv;
-        const float lp = lanes_sum_ordered<32>(on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f, base, A);
+        const float lp = row_sum_ordered(srow, k, on ? -0.5f * dz * dz - ls - kLogSqrt2Pi : 0.f);
         const float ratio = expf(lp - in[j].lpo);
         const float a = in[j].adv;
         const float surr = fminf(ratio * a, clampf(ratio, lo, hi) * a);
@@ -166,9 +186,9 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
         sacc += surr * p.scale;
         if (p.mean_old) {
           const float y = (mu - in[j].mo) * inv_sd;
-          kacc += lanes_sum_ordered<32>(on ? 0.5f * (y * y) : 0.f, base, A) * p.scale;
+          kacc += row_sum_ordered(srow, k, on ? 0.5f * (y * y) : 0.f) * p.scale;
         }
-        sd[row * kHeadDPitch + k] = on ? gm : 0.f;  // the group's own row: no other reader yet
+        srow[k] = on ? gm : 0.f;  // the group's own row: no other reader yet
       }
     }
     lds_barrier();
