@@ -19,16 +19,20 @@ namespace zk {
 // the stores drain in the background.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+constexpr int kHeadGroups = kHeadThreads / 32;  // 32-lane loss groups
 constexpr int kHeadPitch = kHeadMaxHidden + 4;  // LDS row pitch of the activation tile
 constexpr int kHeadDPitch = kHeadMaxActions + 4;
+constexpr int kHeadRed = kHeadGroups * 34 > kHeadThreads ? kHeadGroups * 34 : kHeadThreads;
 constexpr int kHeadLds =
-    kHeadRows * kHeadPitch + kHeadMaxActions * kHeadPitch + kHeadRows * kHeadDPitch + 8 * 34;
+    kHeadRows * kHeadPitch + kHeadMaxActions * kHeadPitch + kHeadRows * kHeadDPitch + kHeadRed;
+static_assert(kHeadRows == 64 && kHeadMaxHidden == 128 && kHeadMaxActions == 32,
+              "wave-to-tile mapping of zk_head");
 
 // Rows [r0, r0 + nr) of x into sx (kHeadRows x kHeadPitch), zero past nr
 // rows and past H columns (up to kHeadMaxHidden).
 __device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, int nr, float* sx) {
   constexpr int QPR = kHeadMaxHidden / 4;  // float4 quads per row
-  for (int i = threadIdx.x; i < kHeadRows * QPR; i += kThreads) {
+  for (int i = threadIdx.x; i < kHeadRows * QPR; i += kHeadThreads) {
     const int r = i / QPR, c = (i % QPR) * 4;
     float4 v = {0.f, 0.f, 0.f, 0.f};
     if (r < nr && c < q.H) {
@@ -65,12 +69,12 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   float* sx = smem;                                      // activations [R x pitch]
   float* sw = sx + kHeadRows * kHeadPitch;               // weights [32 x pitch], rows >= A zero
   float* sd = sw + kHeadMaxActions * kHeadPitch;         // means, then dL/dmean [R x dpitch]
-  float* sred = sd + kHeadRows * kHeadDPitch;            // [8 groups][34]
+  float* sred = sd + kHeadRows * kHeadDPitch;            // [groups][34]
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int A = p.A, H = q.H;
 
-  for (int i = t; i < kHeadMaxActions * (kHeadMaxHidden / 4); i += kThreads) {
+  for (int i = t; i < kHeadMaxActions * (kHeadMaxHidden / 4); i += kHeadThreads) {
     const int m = i / (kHeadMaxHidden / 4), c = (i % (kHeadMaxHidden / 4)) * 4;
     float4 v = {0.f, 0.f, 0.f, 0.f};
     if (m < A && c < H) {
@@ -82,7 +86,7 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     *reinterpret_cast<float4*>(sw + m * kHeadPitch + c) = v;
   }
 
-  // Loss lanes: 8 groups of 32, lane k on action component k.
+  // Loss lanes: 16 groups of 32, lane k on action component k.
   const int grp = t >> 5, k = t & 31;
   const bool on = k < A;
   const float ls = on ? p.log_std[k] : 0.f;
@@ -92,16 +96,16 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   const float lo = 1.0f - p.clip, hi = 1.0f + p.clip;
   float gacc = 0.f, sacc = 0.f, kacc = 0.f;
   float dbias = 0.f;  // thread t < 32: bias gradient of component t
-  floatx4 wacc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) wacc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 wacc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  // Wave-to-tile mapping: 16-row tile rt = wave % 4; forward components
+  // 16 * (wave / 4) ..; data-gradient columns 64 * (wave / 4) ..; weight
+  // gradient columns 16 * wave ...
+  const int rt = wave & 3, half = wave >> 2;
 
   struct In {
     float act, lpo, adv, mo;
   };
-  constexpr int RG = kHeadRows / 8;  // rows per loss group
+  constexpr int RG = kHeadRows / kHeadGroups;  // rows per loss group
   const long long ntiles = (p.rows + kHeadRows - 1) / kHeadRows;
   for (int tt = 0; tt < p.tiles_per_block; ++tt) {
     const long long tile = blockIdx.x + (long long)tt * gridDim.x;
@@ -109,11 +113,11 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     const long long r0 = tile * kHeadRows;
     const int nr = (int)min((long long)kHeadRows, p.rows - r0);
     // Loss inputs of the group's rows, in flight during the tile load and
-    // the forward (group g takes rows g, g + 8, ...).
+    // the forward (group g takes rows g, g + 16, ...).
     In in[RG];
 #pragma unroll
     for (int j = 0; j < RG; ++j) {
-      const int row = grp + 8 * j;
+      const int row = grp + kHeadGroups * j;
       In x{0.f, 0.f, 0.f, 0.f};
       if (row < nr) {
         const long long s = p.perm ? p.perm[p.row0 + r0 + row] : (long long)(p.row0 + r0 + row);
@@ -128,30 +132,25 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     head_load_tile(q, r0, nr, sx);
     lds_barrier();
 
-    // Head forward: wave w computes rows 16w..16w+15, components 0..31.
+    // Head forward: rows of tile rt, components 16 * half ...
     {
-      floatx4 acc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+      floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
       for (int c16 = 0; c16 < kHeadMaxHidden / 16; ++c16) {
-        const float4 af = *reinterpret_cast<const float4*>(sx + (16 * wave + lr) * kHeadPitch + 16 * c16 + 4 * lg);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const float4 bf = *reinterpret_cast<const float4*>(sw + (16 * j + lr) * kHeadPitch + 16 * c16 + 4 * lg);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc[j], 0, 0, 0);
-        }
+        const float4 af = *reinterpret_cast<const float4*>(sx + (16 * rt + lr) * kHeadPitch + 16 * c16 + 4 * lg);
+        const float4 bf = *reinterpret_cast<const float4*>(sw + (16 * half + lr) * kHeadPitch + 16 * c16 + 4 * lg);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
       }
+      const int m = 16 * half + lr;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int m = 16 * j + lr;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = 16 * wave + 4 * lg + r;
-          const float mu = m < A ? acc[j][r] + q.b[m] : 0.f;
-          sd[row * kHeadDPitch + m] = mu;
-          if (m < A && row < nr) q.out[(r0 + row) * q.ldo + m] = mu;
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * rt + 4 * lg + r;
+        const float mu = m < A ? acc[r] + q.b[m] : 0.f;
+        sd[row * kHeadDPitch + m] = mu;
+        if (m < A && row < nr) q.out[(r0 + row) * q.ldo + m] = mu;
       }
     }
     lds_barrier();
@@ -160,7 +159,7 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     {
 #pragma unroll
       for (int j = 0; j < RG; ++j) {
-        const int row = grp + 8 * j;
+        const int row = grp + kHeadGroups * j;
         if (row >= nr) {  // group-uniform
           sd[row * kHeadDPitch + k] = 0.f;
           continue;
@@ -193,18 +192,19 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     }
     lds_barrier();
 
-    // Data gradient of the head times ELU' of the activations: wave w, rows
-    // 16w..16w+15, all hidden columns.
+    // Data gradient of the head times ELU' of the activations: rows of tile
+    // rt, hidden columns 64 * half ...
     {
-      floatx4 dacc[kHeadMaxHidden / 16];
+      constexpr int NJ = kHeadMaxHidden / 32;
+      floatx4 dacc[NJ];
 #pragma unroll
-      for (int j = 0; j < kHeadMaxHidden / 16; ++j) dacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NJ; ++j) dacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c16 = 0; c16 < kHeadMaxActions / 16; ++c16) {
-        const float4 af = *reinterpret_cast<const float4*>(sd + (16 * wave + lr) * kHeadDPitch + 16 * c16 + 4 * lg);
-        const float* wr = sw + (16 * c16 + 4 * lg) * kHeadPitch + lr;
+        const float4 af = *reinterpret_cast<const float4*>(sd + (16 * rt + lr) * kHeadDPitch + 16 * c16 + 4 * lg);
+        const float* wr = sw + (16 * c16 + 4 * lg) * kHeadPitch + 64 * half + lr;
 #pragma unroll
-        for (int j = 0; j < kHeadMaxHidden / 16; ++j) {
+        for (int j = 0; j < NJ; ++j) {
           dacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, wr[16 * j], dacc[j], 0, 0, 0);
           dacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, wr[kHeadPitch + 16 * j], dacc[j], 0, 0, 0);
           dacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, wr[2 * kHeadPitch + 16 * j], dacc[j], 0, 0, 0);
@@ -212,11 +212,11 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
         }
       }
 #pragma unroll
-      for (int j = 0; j < kHeadMaxHidden / 16; ++j) {
-        const int n = 16 * j + lr;
+      for (int j = 0; j < NJ; ++j) {
+        const int n = 64 * half + 16 * j + lr;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = 16 * wave + 4 * lg + r;
+          const int row = 16 * rt + 4 * lg + r;
           if (row < nr && n < H)
             q.dz[(r0 + row) * q.ldz + n] = dacc[j][r] * elu_grad_from_act(sx[row * kHeadPitch + n]);
         }
@@ -224,25 +224,22 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     }
 
     // Weight gradient partial dW += dmean^T . x over this tile's rows: wave w
-    // takes hidden columns 32w..32w+31; the bias gradient is the column sum.
+    // takes hidden columns 16w..16w+15; the bias gradient is the column sum.
 #pragma unroll
     for (int r16 = 0; r16 < kHeadRows / 16; ++r16) {
-      float av[2][4], bv[2][4];
+      float av[2][4], bv[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int row = 16 * r16 + 4 * lg + c;
 #pragma unroll
         for (int i = 0; i < 2; ++i) av[i][c] = sd[row * kHeadDPitch + 16 * i + lr];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) bv[j][c] = sx[row * kHeadPitch + 32 * wave + 16 * j + lr];
+        bv[c] = sx[row * kHeadPitch + 16 * wave + lr];
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            wacc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][c], bv[j][c], wacc[i][j], 0, 0, 0);
+        for (int c = 0; c < 4; ++c)
+          wacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][c], bv[c], wacc[i], 0, 0, 0);
     }
     if (t < kHeadMaxActions)
       for (int row = 0; row < kHeadRows; ++row) dbias += sd[row * kHeadDPitch + t];
@@ -251,16 +248,14 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   // Partials of this block.
   const int blk = blockIdx.x, nblk = gridDim.x;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i) {
+    const int n = 16 * wave + lr;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = 32 * wave + 16 * j + lr;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 16 * i + 4 * lg + r;
-        if (m < A && n < H) q.wpart[((long long)blk * A + m) * H + n] = wacc[i][j][r];
-      }
+    for (int r = 0; r < 4; ++r) {
+      const int m = 16 * i + 4 * lg + r;
+      if (m < A && n < H) q.wpart[((long long)blk * A + m) * H + n] = wacc[i][r];
     }
+  }
   if (t < A) q.bpart[(long long)blk * A + t] = dbias;
   sred[grp * 34 + k] = gacc;
   if (k == 0) {
@@ -270,12 +265,12 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   lds_barrier();
   if (t < A) {
     float g = 0.f;
-    for (int j = 0; j < 8; ++j) g += sred[j * 34 + t];
+    for (int j = 0; j < kHeadGroups; ++j) g += sred[j * 34 + t];
     p.gls_part[(long long)t * nblk + blk] = g;
   } else if (t == 64 || t == 65) {
     const int qq = t - 64;
     float v = 0.f;
-    for (int j = 0; j < 8; ++j) v += sred[j * 34 + 32 + qq];
+    for (int j = 0; j < kHeadGroups; ++j) v += sred[j * 34 + 32 + qq];
     p.astat_part[(long long)qq * nblk + blk] = v;
   }
 }
@@ -283,21 +278,22 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
 __device__ void head_critic(const HeadArgs& p, float* smem) {
   const HeadNet& q = p.net[1];
   float* sx = smem;
-  float* sw = sx + kHeadRows * kHeadPitch;  // w[0..H)
+  float* sw = sx + kHeadRows * kHeadPitch;         // w[0..128), zero past H
   float* sdv = sw + kHeadMaxActions * kHeadPitch;  // dL/dvalue per row
   float* sred = sdv + kHeadRows * kHeadDPitch;
   const int t = threadIdx.x;
   const int H = q.H;
-  for (int i = t; i < kHeadMaxHidden; i += kThreads) sw[i] = i < H ? q.w[i] : 0.f;
+  for (int i = t; i < kHeadMaxHidden; i += kHeadThreads) sw[i] = i < H ? q.w[i] : 0.f;
   const float bias = q.b[0];
   float vacc = 0.f, dw = 0.f, db = 0.f;
   const long long ntiles = (p.rows + kHeadRows - 1) / kHeadRows;
+  constexpr int U = kHeadThreads / kHeadRows;  // lanes per row (8)
   for (int tt = 0; tt < p.tiles_per_block; ++tt) {
     const long long tile = blockIdx.x + (long long)tt * gridDim.x;
     if (tile >= ntiles) break;  // uniform
     const long long r0 = tile * kHeadRows;
     const int nr = (int)min((long long)kHeadRows, p.rows - r0);
-    const int row = t >> 2, u = t & 3;
+    const int row = t / U, u = t % U;
     float vo = 0.f, R = 0.f;  // loss inputs, in flight during the tile load
     if (u == 0 && row < nr) {
       const long long s = p.perm ? p.perm[p.row0 + r0 + row] : (long long)(p.row0 + r0 + row);
@@ -307,18 +303,23 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
     lds_barrier();
     head_load_tile(q, r0, nr, sx);
     lds_barrier();
-    // value = b + sum_k w_k x_k: four lanes per row, 32 columns each, then
-    // the four partial sums in order.
+    // value = b + sum_k w_k x_k: U lanes per row, lane u on columns u, u + U,
+    // ..., then the U partial sums in lane order.
     {
       float part = 0.f;
-      for (int c = 32 * u; c < 32 * u + 32; ++c) part += sx[row * kHeadPitch + c] * sw[c];
-      const int l0 = (t & 63) & ~3;
-      const float p0 = __shfl(part, l0, 64), p1 = __shfl(part, l0 + 1, 64);
-      const float p2 = __shfl(part, l0 + 2, 64), p3 = __shfl(part, l0 + 3, 64);
+#pragma unroll
+      for (int i = 0; i < kHeadMaxHidden / U; ++i) part += sx[row * kHeadPitch + u + U * i] * sw[u + U * i];
+      const int l0 = (t & 63) & ~(U - 1);
+      float ps[U];
+#pragma unroll
+      for (int i = 0; i < U; ++i) ps[i] = __shfl(part, l0 + i, 64);
       if (u == 0) {
         float dv = 0.f;
         if (row < nr) {
-          const float v = bias + (((p0 + p1) + p2) + p3);
+          float sum = ps[0];
+#pragma unroll
+          for (int i = 1; i < U; ++i) sum += ps[i];
+          const float v = bias + sum;
           q.out[(r0 + row) * q.ldo] = v;
           // ppo.rs:436-450, as zk_value_loss.
           const float vc = vo + clampf(v - vo, -p.clip, p.clip);
@@ -339,27 +340,44 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
       }
     }
     lds_barrier();
-    for (int e = t; e < kHeadRows * kHeadMaxHidden; e += kThreads) {
-      const int row = e / kHeadMaxHidden, n = e % kHeadMaxHidden;
-      if (row < nr && n < H)
-        q.dz[(r0 + row) * q.ldz + n] = (sdv[row] * sw[n]) * elu_grad_from_act(sx[row * kHeadPitch + n]);
+    // dL/dz = (dv * w) * ELU'(x), four columns per thread (the dz rows are
+    // 16-byte aligned: ldz is a multiple of 4).
+    for (int e = t; e < kHeadRows * (kHeadMaxHidden / 4); e += kHeadThreads) {
+      const int rr = e / (kHeadMaxHidden / 4), n = (e % (kHeadMaxHidden / 4)) * 4;
+      if (rr < nr && n < H) {
+        const float d = sdv[rr];
+        const float* xr = sx + rr * kHeadPitch + n;
+        float4 o;
+        o.x = (d * sw[n]) * elu_grad_from_act(xr[0]);
+        o.y = (d * sw[n + 1]) * elu_grad_from_act(xr[1]);
+        o.z = (d * sw[n + 2]) * elu_grad_from_act(xr[2]);
+        o.w = (d * sw[n + 3]) * elu_grad_from_act(xr[3]);
+        float* dst = q.dz + (r0 + rr) * q.ldz + n;
+        if (n + 4 <= H) {
+          *reinterpret_cast<float4*>(dst) = o;
+        } else {
+          dst[0] = o.x;
+          if (n + 1 < H) dst[1] = o.y;
+          if (n + 2 < H) dst[2] = o.z;
+        }
+      }
     }
     if (t < kHeadMaxHidden) {
-      for (int row = 0; row < kHeadRows; ++row) dw += sdv[row] * sx[row * kHeadPitch + t];
-    } else if (t == kThreads - 1) {
-      for (int row = 0; row < kHeadRows; ++row) db += sdv[row];
+      for (int rr = 0; rr < kHeadRows; ++rr) dw += sdv[rr] * sx[rr * kHeadPitch + t];
+    } else if (t == kHeadThreads - 1) {
+      for (int rr = 0; rr < kHeadRows; ++rr) db += sdv[rr];
     }
   }
   const int blk = blockIdx.x;
   if (t < H) q.wpart[(long long)blk * H + t] = dw;
-  if (t == kThreads - 1) q.bpart[blk] = db;
-  const float tot = block_sum(vacc, sred);
+  if (t == kHeadThreads - 1) q.bpart[blk] = db;
+  const float tot = block_sum<kHeadThreads>(vacc, sred);
   if (t == 0) p.vstat_part[blk] = tot;
 }
 
 }  // namespace zk
 
-extern "C" __global__ __launch_bounds__(256) void zk_head(zk::HeadArgs p) {
+extern "C" __global__ __launch_bounds__(zk::kHeadThreads) void zk_head(zk::HeadArgs p) {
   __shared__ __align__(16) float smem[zk::kHeadLds];
   if (p.guard && *p.guard == 0) return;
   if (blockIdx.z == 0)

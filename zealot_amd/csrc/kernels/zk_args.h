@@ -157,6 +157,7 @@ struct ValueLossArgs {
 // strided over the blocks of a net; the last hidden width is at most
 // kHeadMaxHidden and the action dim at most kHeadMaxActions.
 constexpr int kHeadRows = 64;
+constexpr int kHeadThreads = 512;  // 8 wavefronts per block
 constexpr int kHeadMaxBlocks = 512;
 constexpr int kHeadMaxHidden = 128;
 constexpr int kHeadMaxActions = 32;

@@ -674,7 +674,7 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     h.astat_part = p->astat_part;
     h.vstat_part = p->vstat_part;
     h.guard = guard;
-    if ((s = launch(c, K_HEAD, (unsigned)head_blocks, 1, 2, h))) return s;
+    if ((s = launch(c, K_HEAD, (unsigned)head_blocks, 1, 2, h, 0, zk::kHeadThreads))) return s;
     pc->nb_a = pc->nb_v = head_blocks;
   } else {
     const LossShape lsh = actor_loss_shape(rows, A);
