@@ -283,23 +283,51 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
   const int rs_m = tid % BM, rs_g = tid / BM;
   const bool rs_on = rowsum && tid < BM * RSG;
 
+  // Column bias of the batch-major forward epilogue, read before the k-loop
+  // so that its latency is hidden behind the MFMAs.
+  float bpre[TN];
+  if (p.epi == kEpiBiasN) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + (wn * TN + j) * 16 + lr;
+      bpre[j] = n < p.N ? p.bias[n] : 0.f;
+    }
+  }
+
+  // Pipeline. Registers hold the global loads of k-tile t + 1 while the MFMAs
+  // of k-tile t run; they are written to the free LDS buffer at the start of
+  // iteration t, and the loads of k-tile t + 2 are issued right after. The
+  // single barrier of an iteration sits before the group's last 16-wide
+  // chunk: the fragments of that chunk are read before it, and the first
+  // chunk of k-tile t + 1 is read after it while the last chunk's MFMAs run,
+  // so no wave waits on an LDS read right after the barrier.
+  //   LDS buffer (t + 1) & 1 is written in iteration t: its previous contents
+  //   (k-tile t - 1) were last read before the barrier of iteration t - 1.
+  //   Its reads happen after the barrier of iteration t.
   if (kt0 < kt1) {
     ta.fetch_rows(kt0 * BK);
     tb.fetch_rows(kt0 * BK);
     ta.load(kt0 * BK);
     tb.load(kt0 * BK);
+    ta.store(sA(0), kt0 * BK);
+    tb.store(sB(0), kt0 * BK);
     if (kt0 + 1 < kt1) {
       ta.fetch_rows((kt0 + 1) * BK);
       tb.fetch_rows((kt0 + 1) * BK);
+      ta.load((kt0 + 1) * BK);
+      tb.load((kt0 + 1) * BK);
+      if (kt0 + 2 < kt1) {
+        ta.fetch_rows((kt0 + 2) * BK);
+        tb.fetch_rows((kt0 + 2) * BK);
+      }
     }
-    ta.store(sA(0), kt0 * BK);
-    tb.store(sB(0), kt0 * BK);
   }
   __syncthreads();
 
   // YPRE variants (data gradients): the ELU' operand is read into registers
-  // two k-tiles before the end, so its latency overlaps the last MFMAs
-  // instead of the epilogue waiting for it.
+  // at the start of the last k-tile (which has no tile loads left to issue),
+  // so its latency overlaps the last MFMAs instead of the epilogue waiting
+  // for it.
   const bool elu_grad = YPRE && p.epi == kEpiEluGrad && kg == 0;
   float ypre[YPRE ? TM : 1][YPRE ? TN : 1][4];
   auto prefetch_y = [&]() {
@@ -315,47 +343,72 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
         }
       }
   };
-  if (elu_grad && kt1 - kt0 <= 2) prefetch_y();
 
-  for (int kt = kt0; kt < kt1; ++kt) {
+  // This group's 16-wide chunks of a k-tile: q = kg * QPG + qi.
+  constexpr int QPG = BK / 16 / KG;
+  struct Frags {
+    float4 a[TM], b[TN];
+  };
+  auto read_chunk = [&](Frags& f, const float* as, const float* bs, int qi) {
+    const int q = kg * QPG + qi;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) f.a[i] = TA::frag(as, (wm * TM + i) * 16 + lr, q, lg);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) f.b[j] = TB::frag(bs, (wn * TN + j) * 16 + lr, q, lg);
+  };
+  auto mma_chunk = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i].x, f.b[j].x, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i].y, f.b[j].y, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i].z, f.b[j].z, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[i].w, f.b[j].w, acc[i][j], 0, 0, 0);
+      }
+  };
+  // One iteration; `first` holds chunk 0 of k-tile kt on entry (its MFMAs
+  // run before the barrier) and receives chunk 0 of k-tile kt + 1 after it.
+  // With a single chunk per group nothing is left to run after the barrier:
+  // the next iteration's LDS stores and global loads are issued while that
+  // read is in flight.
+  Frags fr[QPG];
+  auto iteration = [&](int kt, Frags& first) {
     const int cur = (kt - kt0) & 1;
-    const bool more = kt + 1 < kt1;
-    if (elu_grad && kt1 - kt0 > 2 && kt == kt1 - 2) prefetch_y();
-    if (more) {
-      ta.load((kt + 1) * BK);
-      tb.load((kt + 1) * BK);
-      if (kt + 2 < kt1) {
-        ta.fetch_rows((kt + 2) * BK);
-        tb.fetch_rows((kt + 2) * BK);
+    if (kt + 1 < kt1) {
+      ta.store(sA(cur ^ 1), (kt + 1) * BK);
+      tb.store(sB(cur ^ 1), (kt + 1) * BK);
+    }
+    if (kt + 2 < kt1) {
+      ta.load((kt + 2) * BK);
+      tb.load((kt + 2) * BK);
+      if (kt + 3 < kt1) {
+        ta.fetch_rows((kt + 3) * BK);
+        tb.fetch_rows((kt + 3) * BK);
       }
     }
     const float* as = sA(cur);
     const float* bs = sB(cur);
 #pragma unroll
-    for (int q = kg * (BK / 16 / KG); q < (kg + 1) * (BK / 16 / KG); ++q) {
-      float4 af[TM], bf[TN];
+    for (int qi = 1; qi < QPG; ++qi) read_chunk(fr[qi], as, bs, qi);
+    mma_chunk(first);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = TA::frag(as, (wm * TM + i) * 16 + lr, q, lg);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = TB::frag(bs, (wn * TN + j) * 16 + lr, q, lg);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
-        }
-    }
+    for (int qi = 1; qi + 1 < QPG; ++qi) mma_chunk(fr[qi]);
     if (rs_on) {
       for (int kk = rs_g; kk < BK; kk += RSG) rs += TA::at(as, rs_m, kk);
     }
-    if (more) {
-      ta.store(sA(cur ^ 1), (kt + 1) * BK);
-      tb.store(sB(cur ^ 1), (kt + 1) * BK);
-    }
     __syncthreads();
+    if (kt + 1 < kt1) read_chunk(first, sA(cur ^ 1), sB(cur ^ 1), 0);
+    if constexpr (QPG > 1) mma_chunk(fr[QPG - 1]);
+  };
+  // The last k-tile is peeled off the loop, so that the ELU' operand read
+  // before it is not held in registers across the loop.
+  Frags f0;
+  if (kt0 < kt1) read_chunk(f0, sA(0), sB(0), 0);
+  for (int kt = kt0; kt + 1 < kt1; ++kt) iteration(kt, f0);
+  if (kt0 < kt1) {
+    if (elu_grad) prefetch_y();
+    iteration(kt1 - 1, f0);
   }
 
   if (rowsum) {
@@ -405,7 +458,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
         if (m < p.M && n < p.N) {
           float v = acc[i][j][r];
           if (p.epi == kEpiBiasN) {
-            v = v + p.bias[n];
+            v = v + bpre[j];
             if (p.act) v = elu(v);
           } else if (p.epi == kEpiBiasM) {
             v = v + p.bias[(long long)m * p.bias_stride];
