@@ -700,6 +700,7 @@ ZK_GEMM(zk_gemm_am_bn_64x128x16_w24, false, false, 64, 128, 16, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_am_bn_64x128x32_w22k2, false, false, 64, 128, 32, 2, 2, 2, true)
 ZK_GEMM(zk_gemm_am_bn_128x128x16_w24, false, false, 128, 128, 16, 2, 4, 1, true)
+ZK_GEMM(zk_gemm_am_bn_128x128x32_w24, false, false, 128, 128, 32, 2, 4, 1, true)
 ZK_GEMM(zk_gemm_am_bn_128x128x32_w22k2, false, false, 128, 128, 32, 2, 2, 2, true)
 ZK_GEMM(zk_gemm_am_bn_64x64x16_w22, false, false, 64, 64, 16, 2, 2, 1, true)
 ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, 1, true)

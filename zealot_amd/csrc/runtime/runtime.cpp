@@ -50,6 +50,7 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512, true},
     {"zk_gemm_am_bn_64x128x32_w22k2", false, false, 64, 128, 32, 512, true},
     {"zk_gemm_am_bn_128x128x16_w24", false, false, 128, 128, 16, 512, true},
+    {"zk_gemm_am_bn_128x128x32_w24", false, false, 128, 128, 32, 512, true},
     {"zk_gemm_am_bn_128x128x32_w22k2", false, false, 128, 128, 32, 512, true},
     {"zk_gemm_am_bn_64x64x16_w22", false, false, 64, 64, 16, 256, true},
     {"zk_gemm_am_bn_32x128x16_w14", false, false, 32, 128, 16, 256, true},
@@ -140,8 +141,9 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // exact multiple of the 256 CUs with 96-row tiles, so the row-major layer
 // GEMMs use them; the narrow output layers use narrow-N tiles. The weight
 // gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
-// 512- and 256-wide layers, 64 x 128 for the 128-wide one and 32 x 128 for
-// the narrow heads (measured on gfx950 at 24,576 rows).
+// 512- and 256-wide layers, 64 x 128 for the 128-wide one (both with 32-row
+// k-tiles, so that the k-loop's barrier sits between two chunks) and
+// 32 x 128 for the narrow heads (measured on gfx950 at 24,576 rows).
 int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec, int epi) {
   const int lay = layout_of(a_kc, b_kc);
   const bool forced = c && c->force_gemm[lay] >= 0;
@@ -192,9 +194,9 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
       break;
     case L_AM_BN:
       if (M >= 256)
-        name = "zk_gemm_am_bn_128x128x16_w24";
+        name = "zk_gemm_am_bn_128x128x32_w24";
       else if (M >= 96)
-        name = "zk_gemm_am_bn_64x128x16_w24";
+        name = "zk_gemm_am_bn_64x128x32_w24";
       else
         name = "zk_gemm_am_bn_32x128x16_w14";
       break;
