@@ -446,33 +446,47 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
           acc[i][j][r] = acc[i][j][r] + xch[(((wave * TM + i) * TN + j) * 4 + r) * 64 + lane];
   }
 
+  // Epilogue. The kind (and ELU flag) is uniform, so each kind runs its own
+  // straight-line element loop; tiles wholly inside C skip the bounds tests.
   float* C = p.C + (long long)split * p.split_stride;
+  const bool full_tile = m0 + BM <= p.M && n0 + BN <= p.N;
+  auto emit = [&](auto f) {
+    auto run = [&](auto full) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + (wn * TN + j) * 16 + lr;
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + (wm * TM + i) * 16 + lg * 4 + r;
+          float* crow = C + (long long)m * p.ldc;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + (wm * TM + i) * 16 + lg * 4 + r;
-        if (m < p.M && n < p.N) {
-          float v = acc[i][j][r];
-          if (p.epi == kEpiBiasN) {
-            v = v + bpre[j];
-            if (p.act) v = elu(v);
-          } else if (p.epi == kEpiBiasM) {
-            v = v + p.bias[(long long)m * p.bias_stride];
-            if (p.act) v = elu(v);
-          } else if (p.epi == kEpiEluGrad) {
-            if constexpr (YPRE)
-              v = v * elu_grad_from_act(ypre[i][j][r]);
-            else
-              v = v * elu_grad_from_act(p.Y[(long long)m * p.ldy + n]);
+          for (int j = 0; j < TN; ++j) {
+            const int n = n0 + (wn * TN + j) * 16 + lr;
+            if (decltype(full)::value || (m < p.M && n < p.N)) crow[n] = f(acc[i][j][r], i, j, r, m, n);
           }
-          C[(long long)m * p.ldc + n] = v;
         }
-      }
-    }
+    };
+    if (full_tile)
+      run(std::true_type{});
+    else
+      run(std::false_type{});
+  };
+  if (p.epi == kEpiBiasN) {
+    if (p.act)
+      emit([&](float v, int, int j, int, int, int) { return elu(v + bpre[j]); });
+    else
+      emit([&](float v, int, int j, int, int, int) { return v + bpre[j]; });
+  } else if (p.epi == kEpiBiasM) {
+    if (p.act)
+      emit([&](float v, int, int, int, int m, int) { return elu(v + p.bias[(long long)m * p.bias_stride]); });
+    else
+      emit([&](float v, int, int, int, int m, int) { return v + p.bias[(long long)m * p.bias_stride]; });
+  } else if (p.epi == kEpiEluGrad) {
+    if constexpr (YPRE)
+      emit([&](float v, int i, int j, int r, int, int) { return v * elu_grad_from_act(ypre[i][j][r]); });
+    else
+      emit([&](float v, int, int, int, int m, int n) { return v * elu_grad_from_act(p.Y[(long long)m * p.ldy + n]); });
+  } else {
+    emit([&](float v, int, int, int, int, int) { return v; });
   }
 }
 
