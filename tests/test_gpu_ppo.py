@@ -393,19 +393,24 @@ def test_update_deterministic_and_replay(ctx):
     gac.close()
 
 
-def test_values_and_actor_mean(ctx):
-    """Config 2 (actor inference over 4096 rows) and critic values."""
+@pytest.mark.parametrize("n", [4096, 3500, 2500, 1024, 1000])
+def test_values_and_actor_mean(ctx, n):
+    """Config 2 (actor inference over 4096 rows) and critic values. With
+    1024-row buffers the critic's chunks run in pairs (the second in the
+    actor's buffers): n = 3500 ends in a short pair, 2500 in a lone short
+    chunk, 1024 and 1000 are a single chunk."""
     c2 = synth.config2()
+    obs = c2["obs"][:n]
     critic = synth.kaiming_uniform_net(synth.rng(2, 1), synth.CRITIC_DIMS)
     gac = GpuActorCritic(ctx, synth.ACTOR_DIMS, synth.CRITIC_DIMS, 1024)
     gac.set_params(c2["actor"], critic, c2["log_std"], 1e-3)
-    dobs = ctx.to_device(c2["obs"])
-    mean = ctx.alloc((4096, 29))
-    vals = ctx.alloc(4096)
-    gac.actor_mean(dobs, 4096, mean)
-    gac.values(dobs, 4096, vals)
-    rm = zo.mlp_forward(synth.ACTOR_DIMS, c2["actor"], c2["obs"])[-1]
-    rv = zo.mlp_forward(synth.CRITIC_DIMS, critic, c2["obs"])[-1][:, 0]
+    dobs = ctx.to_device(obs)
+    mean = ctx.alloc((n, 29))
+    vals = ctx.alloc(n)
+    gac.actor_mean(dobs, n, mean)
+    gac.values(dobs, n, vals)
+    rm = zo.mlp_forward(synth.ACTOR_DIMS, c2["actor"], obs)[-1]
+    rv = zo.mlp_forward(synth.CRITIC_DIMS, critic, obs)[-1][:, 0]
     assert rel_amax(mean.numpy(), rm) <= TOL
     assert rel_amax(vals.numpy(), rv) <= TOL
     gac.close()
