@@ -137,6 +137,29 @@ def test_gemm_narrow_shapes(ctx, case):
     assert err <= FWD_BWD_TOL, (case, err)
 
 
+@pytest.fixture(scope="module")
+def tiled_ctx():
+    """A context with the register-resident narrow kernels switched off
+    (ZL_NARROW=0, read at zl_init): N <= 32 then runs the 256 x 16 / 128 x 32
+    tiles and K <= 32 / M <= 32 the general tiles."""
+    import os
+
+    from zealot_amd import Context
+
+    os.environ["ZL_NARROW"] = "0"
+    try:
+        c = Context(0)
+    finally:
+        del os.environ["ZL_NARROW"]
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("case", NARROW_CASES)
+def test_gemm_narrow_shapes_tiled(tiled_ctx, case):
+    test_gemm_narrow_shapes(tiled_ctx, case)
+
+
 def test_gemm_narrow_bias_elu(ctx):
     """K <= 32 with the strided bias column + ELU epilogue of gemm_bias_act."""
     m, n, k = 300, 100, 20

@@ -232,34 +232,27 @@ struct Tile {
   }
 };
 
-// KG > 1 splits every staged k-tile between KG groups of WM x WN waves (group
-// g runs the 16-wide chunks [g, g+1) * BK/16/KG); the groups' accumulators are
-// added in LDS in group order before the epilogue, so a tile gets KG times
-// the waves without any global split-K partials.
-template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, int KG, bool VEC,
+template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, bool VEC,
           bool YPRE = false>
 __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
-  constexpr int NT = 64 * WM * WN * KG;
+  constexpr int NT = 64 * WM * WN;
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
   static_assert(TM >= 1 && TN >= 1 && TM * WM * 16 == BM && TN * WN * 16 == BN, "wave tiling");
-  static_assert(BK % (16 * KG) == 0, "16-wide chunks per group");
-  static_assert(KG == 1 || KG == 2, "one LDS exchange round");
+  static_assert(BK % 16 == 0, "16-wide chunks");
   constexpr int RSG = NT / BM >= 1 ? NT / BM : 1;  // threads per A row in the row sums
   using TA = Tile<BM, AK, BK, NT, VEC>;
   using TB = Tile<BN, BKC, BK, NT, VEC>;
   constexpr int SMEM = 2 * (TA::SIZE + TB::SIZE);
-  static_assert(KG == 1 || SMEM >= BM * BN, "LDS holds one group's accumulator tile");
   static_assert(SMEM >= NT, "LDS holds one float per thread for the row sums");
   // One allocation: [A buf 0][A buf 1][B buf 0][B buf 1], reused after the
-  // k-loop for the row-sum and k-group exchanges.
+  // k-loop for the row-sum exchange.
   __shared__ __align__(16) float smem[SMEM];
   auto sA = [&](int b) { return smem + b * TA::SIZE; };
   auto sB = [&](int b) { return smem + 2 * TA::SIZE + b * TB::SIZE; };
 
   if (p.guard && *p.guard == 0) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave_all = tid >> 6;
-  const int kg = wave_all / (WM * WN), wave = wave_all % (WM * WN);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
   const int lr = lane & 15, lg = lane >> 4;
   const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
@@ -328,7 +321,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
   // at the start of the last k-tile (which has no tile loads left to issue),
   // so its latency overlaps the last MFMAs instead of the epilogue waiting
   // for it.
-  const bool elu_grad = YPRE && p.epi == kEpiEluGrad && kg == 0;
+  const bool elu_grad = YPRE && p.epi == kEpiEluGrad;
   float ypre[YPRE ? TM : 1][YPRE ? TN : 1][4];
   auto prefetch_y = [&]() {
 #pragma unroll
@@ -344,13 +337,13 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
       }
   };
 
-  // This group's 16-wide chunks of a k-tile: q = kg * QPG + qi.
-  constexpr int QPG = BK / 16 / KG;
+  // 16-wide chunks per k-tile.
+  constexpr int QPG = BK / 16;
   struct Frags {
     float4 a[TM], b[TN];
   };
   auto read_chunk = [&](Frags& f, const float* as, const float* bs, int qi) {
-    const int q = kg * QPG + qi;
+    const int q = qi;
 #pragma unroll
     for (int i = 0; i < TM; ++i) f.a[i] = TA::frag(as, (wm * TM + i) * 16 + lr, q, lg);
 #pragma unroll
@@ -421,29 +414,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
       if (m0 + tid < p.M) p.rowsumA[(long long)split * p.M + m0 + tid] = tot;
     }
     __syncthreads();
-  }
-
-  if constexpr (KG > 1) {
-    // Group 1 hands its accumulators to group 0 through LDS (free after the
-    // k-loop and the row-sum barrier).
-    float* xch = smem;
-    if (kg == 1) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xch[(((wave * TM + i) * TN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
-    }
-    __syncthreads();
-    if (kg != 0) return;
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          acc[i][j][r] = acc[i][j][r] + xch[(((wave * TM + i) * TN + j) * 4 + r) * 64 + lane];
   }
 
   // Epilogue. The kind (and ELU flag) is uniform, so each kind runs its own
@@ -672,57 +642,40 @@ __device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
 
 }  // namespace zk
 
-#define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, KG, VEC)                                   \
-  extern "C" __global__ __launch_bounds__(64 * WM * WN * KG) void NAME(zk::GemmBatch b) {      \
-    const int prob = blockIdx.z / b.zper;                                                      \
-    if (prob >= b.count) return;                                                               \
-    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, KG, VEC>(b.g[prob], blockIdx.z % b.zper);       \
+#define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC)                                 \
+  extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(zk::GemmBatch b) {      \
+    const int prob = blockIdx.z / b.zper;                                                 \
+    if (prob >= b.count) return;                                                          \
+    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, VEC>(b.g[prob], blockIdx.z % b.zper);      \
   }
 
 // Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous,
-// then BMxBNxBK, the wave grid WMxWN, (k2) two k-groups per tile and (_s)
-// scalar global loads for operands that are not 16-byte aligned row by row.
-ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22, true, true, 64, 128, 16, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_96x128x16_w24, true, true, 96, 128, 16, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_96x128x32_w22k2, true, true, 96, 128, 32, 2, 2, 2, true)
-ZK_GEMM(zk_gemm_ak_bk_128x128x32_w24, true, true, 128, 128, 32, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_128x128x32_w22, true, true, 128, 128, 32, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_128x128x16_w22, true, true, 128, 128, 16, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_64x64x32_w22, true, true, 64, 64, 32, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_32x64x32_w12, true, true, 32, 64, 32, 1, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_96x32x32_w21, true, true, 96, 32, 32, 2, 1, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, 1, true)
-ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_ak_bn_96x128x16_w24, true, false, 96, 128, 16, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_ak_bn_96x128x32_w22k2, true, false, 96, 128, 32, 2, 2, 2, true)
+// then BMxBNxBK, the wave grid WMxWN and (_s) scalar global loads for
+// operands that are not 16-byte aligned row by row.
+ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22, true, true, 64, 128, 16, 2, 2, true)
+ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, true)
+ZK_GEMM(zk_gemm_ak_bk_64x64x32_w22, true, true, 64, 64, 32, 2, 2, true)
+ZK_GEMM(zk_gemm_ak_bk_32x64x32_w12, true, true, 32, 64, 32, 1, 2, true)
+ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, true)
+ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, true)
+ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, true)
 // Data-gradient variant (ELU' operand prefetched), held to 4 waves per SIMD
 // so that two 8-wave blocks stay resident per CU.
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
 void zk_gemm_ak_bn_96x128x32_w24_dg(zk::GemmBatch b) {
   const int prob = blockIdx.z / b.zper;
   if (prob >= b.count) return;
-  zk::gemm_body<true, false, 96, 128, 32, 2, 4, 1, true, true>(b.g[prob], blockIdx.z % b.zper);
+  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true>(b.g[prob], blockIdx.z % b.zper);
 }
-ZK_GEMM(zk_gemm_ak_bn_128x128x32_w24, true, false, 128, 128, 32, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_ak_bn_128x128x32_w22, true, false, 128, 128, 32, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bn_128x128x16_w22, true, false, 128, 128, 16, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_am_bn_64x128x16_w22, false, false, 64, 128, 16, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_am_bn_64x128x16_w24, false, false, 64, 128, 16, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_am_bn_64x128x32_w22k2, false, false, 64, 128, 32, 2, 2, 2, true)
-ZK_GEMM(zk_gemm_am_bn_128x128x16_w24, false, false, 128, 128, 16, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_am_bn_128x128x32_w24, false, false, 128, 128, 32, 2, 4, 1, true)
-ZK_GEMM(zk_gemm_am_bn_128x128x32_w22k2, false, false, 128, 128, 32, 2, 2, 2, true)
-ZK_GEMM(zk_gemm_am_bn_64x64x16_w22, false, false, 64, 64, 16, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, 1, true)
-ZK_GEMM(zk_gemm_am_bk_64x128x16_w22, false, true, 64, 128, 16, 2, 2, 1, true)
-ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22_s, true, true, 64, 128, 16, 2, 2, 1, false)
-ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22_s, true, false, 64, 128, 16, 2, 2, 1, false)
-ZK_GEMM(zk_gemm_am_bn_64x128x16_w22_s, false, false, 64, 128, 16, 2, 2, 1, false)
-ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, 1, false)
+ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, true)
+ZK_GEMM(zk_gemm_am_bn_128x128x32_w24, false, false, 128, 128, 32, 2, 4, true)
+ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, true)
+ZK_GEMM(zk_gemm_am_bk_64x128x16_w22, false, true, 64, 128, 16, 2, 2, true)
+ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22_s, true, true, 64, 128, 16, 2, 2, false)
+ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22_s, true, false, 64, 128, 16, 2, 2, false)
+ZK_GEMM(zk_gemm_am_bn_64x128x16_w22_s, false, false, 64, 128, 16, 2, 2, false)
+ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, false)
 
 extern "C" __global__ __launch_bounds__(256) void zk_splitk_reduce(zk::SplitReduceArgs p) {
   zk::splitk_reduce_body(p);

@@ -27,32 +27,15 @@ const char* const kFixedNames[K_GEMM_BASE] = {
 const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bk_64x128x16_w22", true, true, 64, 128, 16, 256, true},
     {"zk_gemm_ak_bk_96x128x32_w24", true, true, 96, 128, 32, 512, true},
-    {"zk_gemm_ak_bk_96x128x16_w24", true, true, 96, 128, 16, 512, true},
-    {"zk_gemm_ak_bk_96x128x32_w22k2", true, true, 96, 128, 32, 512, true},
-    {"zk_gemm_ak_bk_128x128x32_w24", true, true, 128, 128, 32, 512, true},
-    {"zk_gemm_ak_bk_128x128x32_w22", true, true, 128, 128, 32, 256, true},
-    {"zk_gemm_ak_bk_128x128x16_w22", true, true, 128, 128, 16, 256, true},
     {"zk_gemm_ak_bk_64x64x32_w22", true, true, 64, 64, 32, 256, true},
     {"zk_gemm_ak_bk_32x64x32_w12", true, true, 32, 64, 32, 128, true},
     {"zk_gemm_ak_bk_128x32x16_w41", true, true, 128, 32, 16, 256, true},
-    {"zk_gemm_ak_bk_96x32x32_w21", true, true, 96, 32, 32, 128, true},
     {"zk_gemm_ak_bk_256x16x16_w41", true, true, 256, 16, 16, 256, true},
     {"zk_gemm_ak_bn_64x128x16_w22", true, false, 64, 128, 16, 256, true},
     {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512, true},
-    {"zk_gemm_ak_bn_96x128x16_w24", true, false, 96, 128, 16, 512, true},
-    {"zk_gemm_ak_bn_96x128x32_w22k2", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w24_dg", true, false, 96, 128, 32, 512, true},
-    {"zk_gemm_ak_bn_128x128x32_w24", true, false, 128, 128, 32, 512, true},
-    {"zk_gemm_ak_bn_128x128x32_w22", true, false, 128, 128, 32, 256, true},
-    {"zk_gemm_ak_bn_128x128x16_w22", true, false, 128, 128, 16, 256, true},
-    {"zk_gemm_am_bn_64x128x16_w22", false, false, 64, 128, 16, 256, true},
-    {"zk_gemm_am_bn_64x128x16_w24", false, false, 64, 128, 16, 512, true},
     {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512, true},
-    {"zk_gemm_am_bn_64x128x32_w22k2", false, false, 64, 128, 32, 512, true},
-    {"zk_gemm_am_bn_128x128x16_w24", false, false, 128, 128, 16, 512, true},
     {"zk_gemm_am_bn_128x128x32_w24", false, false, 128, 128, 32, 512, true},
-    {"zk_gemm_am_bn_128x128x32_w22k2", false, false, 128, 128, 32, 512, true},
-    {"zk_gemm_am_bn_64x64x16_w22", false, false, 64, 64, 16, 256, true},
     {"zk_gemm_am_bn_32x128x16_w14", false, false, 32, 128, 16, 256, true},
     {"zk_gemm_am_bk_64x128x16_w22", false, true, 64, 128, 16, 256, true},
     {"zk_gemm_ak_bk_64x128x16_w22_s", true, true, 64, 128, 16, 256, false},
