@@ -1,8 +1,8 @@
 """ctypes binding of the CPU oracle (oracle/libzl_oracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py as the checker / CPU baseline, never by the
-product path. The oracle restates zealot-rl (zealot-rl/src/{rng,net,ppo}.rs)
+cpu_baseline leg of bench.py as the parity reference / CPU baseline, never
+by the product path. The oracle restates zealot-rl (zealot-rl/src/{rng,net,ppo}.rs)
 and the GPU trainer's update semantics (src/bin/biped_train_gpu.rs:1164-1553)
 in scalar C++; see zl_oracle.hpp for the line-by-line citations.
 """

@@ -25,7 +25,7 @@ from zealot_amd.rl import DeviceBatch, GpuActorCritic, PpoConfig
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-4
-NTHREADS = min(os.cpu_count() or 1, 16)  # the GPU box gives one GPU 16 host cores
+NTHREADS = min(os.cpu_count() or 1, 16)  # at most 16 host threads per GPU
 
 
 def per_tensor_err(dims, got, ref):
