@@ -255,12 +255,25 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
   const int lr = lane & 15, lg = lane >> 4;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  // Tile of this block. Workgroups go to the 8 XCDs round robin (linear id
+  // mod 8), each XCD with its own L2. When the tile count allows, the tiles
+  // are renumbered so that every XCD gets a contiguous run of them ordered
+  // column-tile fastest: the column tiles that read the same A row block then
+  // run on one XCD at the same time and share its L2.
+  const int ntl = (int)gridDim.y, ntiles = (int)gridDim.x * ntl;
+  int mt = blockIdx.x, nt = blockIdx.y;
+  if (ntiles % 8 == 0) {
+    const int bid = blockIdx.x + gridDim.x * blockIdx.y;
+    const int t = (bid % 8) * (ntiles / 8) + bid / 8;
+    mt = t / ntl;
+    nt = t % ntl;
+  }
+  const int m0 = mt * BM, n0 = nt * BN;
   if (m0 >= p.M || n0 >= p.N || split >= p.nsplit) return;  // outside this problem (uniform)
   const int KT = (p.K + BK - 1) / BK;
   const int kt0 = split * p.kt_per_split;
   const int kt1 = min(KT, kt0 + p.kt_per_split);
-  const bool rowsum = p.rowsumA != nullptr && blockIdx.y == 0;
+  const bool rowsum = p.rowsumA != nullptr && nt == 0;
 
   floatx4 acc[TM][TN];
 #pragma unroll
