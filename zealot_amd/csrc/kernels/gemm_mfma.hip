@@ -232,9 +232,36 @@ struct Tile {
   }
 };
 
+// Tile (mt, nt) and z index (problem x split-K slice) of this block.
+// Workgroups reach the 8 XCDs round robin by linear id, and every XCD has its
+// own L2, so blocks that read the same rows should sit on one XCD at the same
+// time. With a multiple of 8 z slices (the split-K weight gradients) all tiles
+// of a slice go to one XCD, slice after slice; otherwise, with a multiple of 8
+// tiles, every XCD gets a contiguous run of tiles of its slice, column tile
+// fastest (the column tiles that read one A row block together). Both are
+// bijections of the launch grid.
+struct BlockTile {
+  int mt, nt, z;
+};
+__device__ __forceinline__ BlockTile block_tile() {
+  const int ntl = (int)gridDim.y, ntiles = (int)gridDim.x * ntl, nz = (int)gridDim.z;
+  const int b = blockIdx.x + gridDim.x * blockIdx.y;
+  if (nz % 8 == 0) {
+    const long long g = b + (long long)ntiles * blockIdx.z;
+    const long long k = g / 8;
+    const int t = (int)(k % ntiles);
+    return {t / ntl, t % ntl, (int)(g % 8) + 8 * (int)(k / ntiles)};
+  }
+  if (ntiles % 8 == 0) {
+    const int t = (b % 8) * (ntiles / 8) + b / 8;
+    return {t / ntl, t % ntl, (int)blockIdx.z};
+  }
+  return {(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+}
+
 template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, bool VEC,
           bool YPRE = false>
-__device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
+__device__ __forceinline__ void gemm_body(const GemmArgs& p, int split, int mt, int nt) {
   constexpr int NT = 64 * WM * WN;
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
@@ -255,19 +282,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave % WM, wn = wave / WM;
   const int lr = lane & 15, lg = lane >> 4;
-  // Tile of this block. Workgroups go to the 8 XCDs round robin (linear id
-  // mod 8), each XCD with its own L2. When the tile count allows, the tiles
-  // are renumbered so that every XCD gets a contiguous run of them ordered
-  // column-tile fastest: the column tiles that read the same A row block then
-  // run on one XCD at the same time and share its L2.
-  const int ntl = (int)gridDim.y, ntiles = (int)gridDim.x * ntl;
-  int mt = blockIdx.x, nt = blockIdx.y;
-  if (ntiles % 8 == 0) {
-    const int bid = blockIdx.x + gridDim.x * blockIdx.y;
-    const int t = (bid % 8) * (ntiles / 8) + bid / 8;
-    mt = t / ntl;
-    nt = t % ntl;
-  }
   const int m0 = mt * BM, n0 = nt * BN;
   if (m0 >= p.M || n0 >= p.N || split >= p.nsplit) return;  // outside this problem (uniform)
   const int KT = (p.K + BK - 1) / BK;
@@ -657,9 +671,10 @@ __device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
 
 #define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC)                                 \
   extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(zk::GemmBatch b) {      \
-    const int prob = blockIdx.z / b.zper;                                                 \
+    const zk::BlockTile bt = zk::block_tile();                                            \
+    const int prob = bt.z / b.zper;                                                       \
     if (prob >= b.count) return;                                                          \
-    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, VEC>(b.g[prob], blockIdx.z % b.zper);      \
+    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, VEC>(b.g[prob], bt.z % b.zper, bt.mt, bt.nt); \
   }
 
 // Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous,
@@ -677,9 +692,10 @@ ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, true)
 // so that two 8-wave blocks stay resident per CU.
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
 void zk_gemm_ak_bn_96x128x32_w24_dg(zk::GemmBatch b) {
-  const int prob = blockIdx.z / b.zper;
+  const zk::BlockTile bt = zk::block_tile();
+  const int prob = bt.z / b.zper;
   if (prob >= b.count) return;
-  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true>(b.g[prob], blockIdx.z % b.zper);
+  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true>(b.g[prob], bt.z % b.zper, bt.mt, bt.nt);
 }
 ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, true)
 ZK_GEMM(zk_gemm_am_bn_128x128x32_w24, false, false, 128, 128, 32, 2, 4, true)
