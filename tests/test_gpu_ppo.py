@@ -156,7 +156,9 @@ def test_minibatch_grads_with_perm(ctx, hidden, n, start, mb):
 
 
 @pytest.mark.parametrize("ad,cd", [([37, 64, 160, 40], [37, 64, 160, 1]),   # H > 128, A > 32
-                                   ([37, 96, 30, 3], [37, 96, 30, 1])])      # H = 30: padded tile
+                                   ([37, 96, 30, 3], [37, 96, 30, 1]),       # H = 30: padded tile
+                                   ([37, 64, 128, 48], [37, 64, 128, 1]),    # the largest action dim
+                                   ([37, 64, 128, 32], [37, 64, 128, 1])])   # the fused head's largest
 def test_minibatch_grads_head_variants(ctx, ad, cd):
     """Output layers outside the fused head kernel's range (last hidden width
     > 128 or more than 32 actions: separate head GEMMs and loss kernels) and
@@ -181,6 +183,13 @@ def test_minibatch_grads_head_variants(ctx, ad, cd):
     assert abs(st["surrogate"] - rst[0]) <= 1e-4 * max(1, abs(rst[0]))
     assert abs(st["value_loss"] - rst[1]) <= 1e-4 * max(1, abs(rst[1]))
     gac.close()
+
+
+def test_action_dim_limit(ctx):
+    """zl_ppo_create refuses more than 48 actions, its stated maximum (the
+    48-action net above is accepted)."""
+    with pytest.raises(ZealotError):
+        GpuActorCritic(ctx, [37, 64, 49], [37, 64, 1], 256)
 
 
 def _param_delta_report(p0, pg, pc, lr, steps):
