@@ -739,7 +739,10 @@ struct Plan {
 
 zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg, const Plan& pl) {
   zl_ctx* c = p->c;
-  const int* guard = &p->dstate->active;
+  // Kernels after a KL early stop are skipped through the device flag
+  // `active`; only the early stop clears it, so without one the kernels get
+  // no flag and skip the dependent load of it at their start.
+  const int* guard = pl.pp.early_stop ? &p->dstate->active : nullptr;
   const int A = p->A;
   zl_status s = ZL_OK;
   if (cfg->normalize_adv) {
