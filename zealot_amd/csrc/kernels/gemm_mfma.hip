@@ -9,9 +9,9 @@
 // B + n*ldb) or N-contiguous (row k at B + k*ldb). Each operand tile is staged
 // in LDS in its global orientation (float4 global loads -> ds_write_b128). A
 // workgroup is WM x WN wave64s; each wave owns TM x TN 16x16 accumulator
-// tiles. K is walked in BK-wide k-tiles, double-buffered in LDS with the next
-// k-tile's global loads in flight during the MFMAs. BK = 32 makes every
-// K-contiguous row segment a full 128-byte line.
+// tiles. K is walked in BK-wide k-tiles, double-buffered in LDS, with the
+// global loads two k-tiles ahead in registers (see gemm_body). BK = 32 makes
+// every K-contiguous row segment a full 128-byte line.
 //
 // Reduction-index assignment. v_mfma_f32_16x16x4f32 takes A[i][s] from lane
 // i + 16 s and B[s][j] from lane j + 16 s. Within each 16-wide chunk q of a
@@ -38,11 +38,11 @@ namespace zk {
 //
 // Global loads are issued unconditionally from clamped, always-valid
 // addresses and every bounds / padding mask is applied when the registers are
-// written to LDS, after the MFMAs of the current k-tile: nothing between the
-// load and the store needs the loaded values, so the loads of k-tile t+1 stay
-// in flight during the MFMAs of k-tile t. Storage rows gathered through
-// `perm` are resolved once per block for a K-contiguous operand (its rows do
-// not change along K) and one k-tile ahead for the other orientation.
+// written to LDS, one iteration later: nothing between the load and the store
+// needs the loaded values, so the loads stay in flight during a k-tile's
+// MFMAs. Storage rows gathered through `perm` are resolved once per block for
+// a K-contiguous operand (its rows do not change along K) and one k-tile
+// ahead of the loads for the other orientation.
 template <int EXT, bool KC, int BK, int NT, bool VEC>
 struct Tile {
   // Row length in LDS (see the file header): conflict-free fragment reads
