@@ -444,10 +444,12 @@ zl_status reduce_rows(zl_ctx* c, const float* part, int width, int blocks, float
 }
 
 
-// Split lanes for `splits` slices: enough that each thread adds at most ~8.
+// Split lanes for `splits` slices: enough that each thread adds at most 32
+// (fewer, longer lanes measured faster than 8 slices per lane for the update's
+// 32- and 64-slice weight gradients: 23.6 vs 25.3 us per minibatch).
 static int reduce_lanes(int splits) {
   int sl = 1;
-  while (sl < 64 && sl * 8 < splits) sl <<= 1;
+  while (sl < 64 && sl * 32 < splits) sl <<= 1;
   return sl;
 }
 
