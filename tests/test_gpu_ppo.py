@@ -306,6 +306,43 @@ def test_update_actor_critic_semantics(ctx, rule):
     gac.close()
 
 
+def test_update_actor_critic_full_size(ctx):
+    """ActorCritic::update at the headline shapes: 98,304 rows, 5 epochs x 4
+    shuffled minibatches of 24,576 rows (the observation gather fused into the
+    first layer's loads and the first weight gradient), per-net clip, log_std
+    Adam with clamp, on the well-posed construction at lr 1e-5 (see
+    test_update_config5_full_size)."""
+    ad, cd = synth.ACTOR_DIMS, synth.CRITIC_DIMS
+    n, lr0 = 98304, 1e-5
+    actor, critic, log_std, batch = _well_posed_problem(43, n, ad, cd)
+    ac = zo.ActorCritic(ad, cd, 1.0, lr0, 1)
+    ac.set(actor, critic, log_std, lr0)
+    cfg_o = zo.PpoCfg(0.99, 0.95, WELL_POSED_CLIP, 0.01, 1.0, 5, 4, 1.0, 0.01, 1e-6, 1e-2, 0)
+    stats_o, adv_o = ac.update(batch, cfg_o, nthreads=NTHREADS, normalize_obs=False)
+    ao, co, lso, lro, to = ac.get()
+
+    gac = GpuActorCritic(ctx, ad, cd, n // 4)
+    gac.set_params(actor, critic, log_std, lr0)
+    db = DeviceBatch(ctx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
+                     batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
+    st = gac.update(db, PpoConfig(epochs=5, minibatches=4, clip=WELL_POSED_CLIP, adaptive_lr=False,
+                                  desired_kl=0.01, lr_min=1e-6, lr_max=1e-2, shuffle=True,
+                                  normalize_adv=True, clamp_log_std=True))
+    ag, cg, lsg, lrg = gac.get_params()
+    t, _ = gac.counters()
+    reps = dict(actor=_param_delta_report(actor, ag, ao, lr0, 20),
+                critic=_param_delta_report(critic, cg, co, lr0, 20),
+                log_std=_param_delta_report(log_std, lsg, lso, lr0, 20))
+    print(f"[gpu] AC update full size: {reps} stats gpu {st} cpu {stats_o}", flush=True)
+    assert t == to == 20 and lrg == pytest.approx(lro, rel=1e-6)
+    assert np.allclose(db.adv.numpy(), adv_o, rtol=1e-5, atol=1e-6)
+    _assert_tight(reps)
+    for k, gv in zip(("kl", "surrogate", "value_loss", "entropy"), (st.kl, st.surrogate, st.value_loss, st.entropy)):
+        ov = stats_o[["kl", "surrogate", "value_loss", "entropy"].index(k)]
+        assert abs(gv - ov) <= 1e-3 * max(abs(ov), 1e-2), (k, gv, ov)
+    gac.close()
+
+
 def test_update_clipped_regime(ctx):
     """ActorCritic::update at clip 0.2 on config-4 style data, where the
     surrogate and value clips are taken throughout. The regime is chaotic in
