@@ -680,7 +680,6 @@ __device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
 // Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous,
 // then BMxBNxBK, the wave grid WMxWN and (_s) scalar global loads for
 // operands that are not 16-byte aligned row by row.
-ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22, true, true, 64, 128, 16, 2, 2, true)
 ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, true)
 ZK_GEMM(zk_gemm_ak_bk_64x64x32_w22, true, true, 64, 64, 32, 2, 2, true)
 ZK_GEMM(zk_gemm_ak_bk_32x64x32_w12, true, true, 32, 64, 32, 1, 2, true)
