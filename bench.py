@@ -36,7 +36,7 @@ HBM_PEAK = 8.0e12  # bytes/s
 # readings of a 256 MiB copy kernel (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0) and
 # averaged over an update's launch mix; reported as roofline.traffic for the
 # dominant kernel when it is one of these.
-MEASURED_TRAFFIC = {"zk_gemm_ak_bk_96x128x32_w24": 123.3e6}
+MEASURED_TRAFFIC = {"zk_gemm_ak_bk_96x128x32_w24": 123.2e6}
 
 
 def cpu_baseline(ro, actor, critic, log_std, mean_old, action, logp_old, values, adv):
