@@ -650,11 +650,19 @@ __device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
     if (matrix) {
       if (idx < nq) {
         const float o[4] = {v.x, v.y, v.z, v.w};
+        // Row and column of the quad's first element by one division; the
+        // next three follow by stepping the column.
+        long long r = 4 * idx / p.cols;
+        int col = (int)(4 * idx - r * p.cols);
         for (int c = 0; c < 4; ++c) {
           const long long i = 4 * idx + c;
           if (i < p.mn) {
-            if (p.part) p.out[(i / p.cols) * p.ldo + i % p.cols] = o[c];
+            if (p.part) p.out[r * p.ldo + col] = o[c];
             sq += o[c] * o[c];
+          }
+          if (++col == p.cols) {
+            col = 0;
+            ++r;
           }
         }
       }
