@@ -23,7 +23,12 @@
 // differences (tests/test_oracle.py); the normaliser (Normalizer::update,
 // PendingNorm::push, norm_commit, normalize; ppo.rs:104-206) by the float64
 // Chan-merge closed forms, the unit-prior identity, the variance floor and
-// the f32 count saturation at 2^24.
+// the f32 count saturation at 2^24; the GPU trainer's optimiser branch
+// (trainer_update: global clip over actor + critic + log_std, bias correction
+// from the epoch's shared gstep) and the minibatch / epoch statistics
+// (surrogate, value loss, mean-only KL, entropy) by a float64 restatement of
+// the epoch built from tests/np_ref.py, which also shows that log_std left out
+// of the norm, a per-net clip or a per-minibatch Adam t fail the check.
 #pragma once
 #include <cmath>
 #include <cstddef>

@@ -589,3 +589,162 @@ def test_norm_count_saturates_like_f32():
     st[2 * dim] = np.float32(2 ** 24 - 2)
     out = zo.norm_update(st, _obs_rows(8, 5, dim))
     assert out[2 * dim] == np.float32(2 ** 24)
+
+
+# ---- the GPU trainer's optimiser branch and the minibatch statistics, pinned
+# by a float64 restatement built only from np_ref (no oracle code).
+
+def _trainer_epoch_f64(ad, cd, actor, critic, log_std, batch, n_mb, lr, max_norm, clip, ent, vcoef,
+                       variant="ref"):
+    """One epoch of src/bin/biped_train_gpu.rs:1164-1461 in float64: contiguous
+    minibatches, the gradient of each from np_ref at the current parameters,
+    ONE norm over actor + critic + log_std gradients (:1368-1452), scale
+    max/norm when the norm exceeds max, then Adam on all three with the bias
+    corrections of t = gstep = n_mb, shared by every minibatch of the epoch
+    (:1165-1167, :1453-1461). `variant` restates a plausible misreading:
+    'no_logstd' (log_std left out of the norm), 'per_net' (each net clipped
+    by its own norm, log_std unclipped: ActorCritic semantics) or 'per_step_t'
+    (bias correction advanced per minibatch)."""
+    n = batch["obs"].shape[0]
+    mb = n // n_mb
+    p = [np.asarray(x, np.float64).copy() for x in (actor, critic, log_std)]
+    m = [np.zeros_like(x) for x in p]
+    v = [np.zeros_like(x) for x in p]
+    norms, stats = [], []
+    for k in range(n_mb):
+        idx = np.arange(k * mb, (k + 1) * mb)
+        ga, gc, gl, st = np_ref.minibatch_grads(ad, cd, p[0], p[1], p[2], batch, idx, clip, ent, vcoef)
+        entropy = float(np.sum(p[2] + 0.5 + np_ref.LOG_SQRT_2PI))
+        stats.append([st[0], st[1], st[2], entropy])
+        g = [ga, gc, gl]
+        sq = [float(np.sum(x * x)) for x in g]
+        if variant == "per_net":
+            sc = [min(1.0, max_norm / np.sqrt(sq[0])), min(1.0, max_norm / np.sqrt(sq[1])), 1.0]
+            norms.append(np.sqrt(sum(sq)))
+        else:
+            tot = sq[0] + sq[1] + (0.0 if variant == "no_logstd" else sq[2])
+            norm = np.sqrt(tot)
+            norms.append(np.sqrt(sum(sq)))
+            s = max_norm / norm if norm > max_norm else 1.0
+            sc = [s, s, s]
+        t = k + 1 if variant == "per_step_t" else n_mb
+        bc1, bc2 = 1.0 - 0.9 ** t, 1.0 - 0.999 ** t
+        for i in range(3):
+            gi = g[i] * sc[i]
+            m[i] = 0.9 * m[i] + 0.1 * gi
+            v[i] = 0.999 * v[i] + 0.001 * gi * gi
+            p[i] = p[i] - lr * (m[i] / bc1) / (np.sqrt(v[i] / bc2) + 1e-8)
+    return p, m, v, np.array(norms), np.array(stats)
+
+
+def _trainer_case(seed):
+    ad, cd, actor, critic, log_std, batch = _ppo_tiny(seed, v_shift=0.05)
+    g = np.random.default_rng(seed + 100)
+    n = 48  # three contiguous minibatches of 16 rows
+    obs = g.standard_normal((n, 3)).astype(np.float32)
+    means = np_ref.forward(ad, actor, obs)[-1].astype(np.float32)
+    vals = np_ref.forward(cd, critic, obs)[-1][:, 0].astype(np.float32)
+    action = (means + 0.7 * g.standard_normal((n, 2))).astype(np.float32)
+    lp = np.sum(-0.5 * ((action - means) / np.exp(log_std)) ** 2 - log_std - 0.9189385, axis=1)
+    batch = dict(obs=obs, critic_obs=obs, action=action,
+                 mean_old=(means + 0.1 * g.standard_normal((n, 2))).astype(np.float32),
+                 logp_old=(lp + 0.02 * g.standard_normal(n)).astype(np.float32),
+                 value_old=(vals + 0.05).astype(np.float32),
+                 adv=zo.adv_normalize(g.standard_normal(n).astype(np.float32)),
+                 ret=g.standard_normal(n).astype(np.float32))
+    return ad, cd, actor, critic, log_std, batch
+
+
+def test_trainer_global_clip_and_shared_bias_correction():
+    """The GPU trainer's optimiser branch of the oracle (global clip over actor
+    + critic + log_std, gstep-shared bias correction; src/bin/biped_train_gpu.rs:
+    1165-1167, 1368-1461) against a float64 restatement that shares no code with
+    it. The clip fires on every minibatch; the Adam moments (linear in the
+    clipped gradient: they expose the clip scale, to which Adam's step is
+    nearly blind) and the parameter changes (which expose the bias correction)
+    both match. Each plausible misreading — log_std left out of the norm, a
+    per-net clip, a per-minibatch Adam t — moves them far outside the bound."""
+    ad, cd, actor, critic, log_std, batch = _trainer_case(31)
+    # Value and entropy coefficients chosen so that the three gradient groups
+    # have norms of one order (log_std's from the entropy term).
+    n_mb, lr, max_norm, clip, ent, vcoef = 3, 1e-2, 0.05, 0.2, 0.3, 0.2
+    tr = zo.Trainer(ad, cd, actor, critic, log_std, lr)
+    so = tr.update(batch, zo.TrainerCfg(clip, ent, vcoef, 1, n_mb, max_norm, 0.01, 1e-5, 1.0, 0, 0, 0))
+    a1, c1, l1, lr1, gstep = tr.get()
+    ma, va, mc, vc, mls, vls = tr.moments()
+    assert gstep == n_mb and int(so[5]) == 1 and lr1 == pytest.approx(lr)
+    got_p = [a1, c1, l1]
+    got_m = [ma, mc, mls]
+    got_v = [va, vc, vls]
+    p0 = [actor, critic, log_std]
+
+    def dist(res):
+        p, m, v = res[0], res[1], res[2]
+        dm = max(rel_amax(got_m[i], m[i]) for i in range(3))
+        dv = max(rel_amax(got_v[i], v[i]) for i in range(3))
+        dp = max(rel_amax(got_p[i].astype(np.float64) - p0[i], p[i] - p0[i]) for i in range(3))
+        return dm, dv, dp
+
+    ref = _trainer_epoch_f64(ad, cd, actor, critic, log_std, batch, n_mb, lr, max_norm, clip, ent, vcoef)
+    assert np.all(ref[3] > 2 * max_norm), ref[3]  # the clip really fires, every minibatch
+    # log_std's share of the norm is large enough that leaving it out matters.
+    gl0 = np_ref.minibatch_grads(ad, cd, actor, critic, log_std, batch, np.arange(16), clip, ent, vcoef)[2]
+    assert np.sum(gl0 ** 2) > 0.2 * ref[3][0] ** 2
+    dm, dv, dp = dist(ref)
+    assert dm < 1e-4 and dv < 2e-4 and dp < 1e-3, (dm, dv, dp)
+    for variant in ("no_logstd", "per_net", "per_step_t"):
+        alt = _trainer_epoch_f64(ad, cd, actor, critic, log_std, batch, n_mb, lr, max_norm, clip, ent,
+                                 vcoef, variant)
+        am, av, ap = dist(alt)
+        assert max(am, av, ap) > 2e-2, (variant, am, av, ap)
+
+
+def test_trainer_epoch_statistics_float64():
+    """The trainer's epoch statistics are the means over the epoch's
+    minibatches of the clipped surrogate, the clipped value loss, the mean-only
+    KL (ActorCritic::kl, zealot-rl/src/ppo.rs:327-334, live log_std) and the
+    entropy (ppo.rs:308-311), each at the parameters the minibatch saw
+    (ppo.rs:374-381): against the float64 restatement above."""
+    ad, cd, actor, critic, log_std, batch = _trainer_case(37)
+    n_mb, lr = 3, 1e-2
+    tr = zo.Trainer(ad, cd, actor, critic, log_std, lr)
+    so = tr.update(batch, zo.TrainerCfg(0.2, 0.1, 1.0, 1, n_mb, 0.05, 0.01, 1e-5, 1.0, 0, 0, 0))
+    ref = _trainer_epoch_f64(ad, cd, actor, critic, log_std, batch, n_mb, lr, 0.05, 0.2, 0.1, 1.0)
+    want = ref[4].mean(axis=0)  # surrogate, value loss, kl, entropy
+    got = {"surrogate": so[1], "value_loss": so[2], "kl": so[0], "entropy": so[3]}
+    for name, w in zip(("surrogate", "value_loss", "kl", "entropy"), want):
+        assert abs(got[name] - w) <= 1e-4 * max(abs(w), 1e-3), (name, got[name], w)
+    # The statistics move with the parameters: minibatches 2 and 3 saw updated
+    # nets, so the statistics of the initial parameters alone do not match.
+    assert np.max(np.abs(ref[4][2, :3] - ref[4][0, :3])) > 1e-2
+
+
+@pytest.mark.parametrize("seed", [3, 11])
+def test_minibatch_statistics_float64(seed):
+    """The oracle's per-minibatch statistics (ppo.rs:417 surrogate, :448 value
+    loss, :452 mean-only KL, all scaled by 1/count) and ActorCritic::
+    minibatch_step's returned statistics (with the entropy, ppo.rs:308-311)
+    against np_ref's float64 values, with the value clamp active on part of
+    the rows. Swapping the KL's log_std for exp(-2 log_std), dropping the
+    clamp branch or the surrogate's min would each fail by far more."""
+    ad, cd, actor, critic, log_std, batch = _ppo_tiny(seed, v_shift=0.3)
+    n = batch["obs"].shape[0]
+    idx = np.arange(n)
+    _, _, _, st = zo.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
+    _, _, _, ref = np_ref.minibatch_grads(ad, cd, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
+    assert rel_amax(st, ref) < 1e-5, (st, ref)
+    ac = zo.ActorCritic(ad, cd, 1.0, 1e-3, 1)
+    ac.set(actor, critic, log_std, 1e-3)
+    cfg = zo.PpoCfg(0.99, 0.95, 0.2, 0.01, 1.0, 1, 1, 1.0, 0.01, 1e-5, 1e-2, 0)
+    s = ac.minibatch_step(batch, idx, cfg, nthreads=1, normalize_obs=False)
+    ent = float(np.sum(log_std.astype(np.float64) + 0.5 + np_ref.LOG_SQRT_2PI))
+    for got, want in ((s[0], ref[2]), (s[1], ref[0]), (s[2], ref[1]), (s[3], ent)):
+        assert abs(got - want) <= 1e-5 * max(abs(want), 1e-3), (got, want)
+    # Misreadings, evaluated in float64, land far from the oracle's values.
+    mean = np_ref.forward(ad, actor, batch["obs"])[-1]
+    mo = batch["mean_old"].astype(np.float64)
+    kl_var = float(np.sum(0.5 * (mean - mo) ** 2 * np.exp(-2 * log_std) ** 2) / n)
+    assert abs(kl_var - ref[2]) > 1e-2 * abs(ref[2])
+    v = np_ref.forward(cd, critic, batch["critic_obs"])[-1][:, 0]
+    vl_plain = float(np.mean((v - batch["ret"]) ** 2))
+    assert abs(vl_plain - ref[1]) > 1e-3 * abs(ref[1])
