@@ -121,19 +121,23 @@ zl_status zl_row_sum(zl_ctx* ctx, float* out, const float* x, int m, int n);
 
 /* ------------------------------------- operators (vortx kernels) ---- */
 
-/* Actor half of the PPO loss for `rows` samples, batch-major:
- * d_mean(rows x A) = dL/dmean, d_log_std[A] = summed dL/dlog_std (with the
- * entropy term), stats_dev[2] = {sum of scaled surrogate, sum of scaled
- * mean-only KL} (mean_old may be NULL: KL = 0). Semantics of
- * zealot-rl/src/ppo.rs:411-432,452; replaces vortx Ppo::actor_grad + the dls
- * row_sum (src/bin/biped_train_gpu.rs:1257-1271,1350-1357). All pointers are
- * device pointers. */
+/* Actor half of the PPO loss for `rows` samples:
+ * d_mean = dL/dmean, d_log_std[A] = summed dL/dlog_std (with the entropy
+ * term), stats_dev[2] = {sum of scaled surrogate, sum of scaled mean-only KL}
+ * (mean_old may be NULL: KL = 0). Semantics of zealot-rl/src/ppo.rs:411-432,
+ * 452; replaces vortx Ppo::actor_grad + the dls row_sum
+ * (src/bin/biped_train_gpu.rs:1257-1271,1350-1357). All pointers are device
+ * pointers. feature_major == 0: mean, action, mean_old and d_mean are
+ * batch-major [rows x A] with row strides ld_*; feature_major != 0: they are
+ * the trainer's [A x rows] tensors (element (sample r, component k) at
+ * ptr[k * ld + r], ld >= rows, e.g. the actor output a[L] and f_act of
+ * src/bin/biped_train_gpu.rs:692-694,1055). */
 zl_status zl_ppo_actor_grad(zl_ctx* ctx, const float* mean, int ld_mean, const float* action,
                             int ld_action, const float* log_std, const float* adv,
                             const float* logp_old, const float* mean_old, int ld_mean_old,
                             int rows, int action_dim, float clip, float entropy_coef,
                             float scale, float* d_mean, int ld_d_mean, float* d_log_std,
-                            float* stats_dev);
+                            float* stats_dev, int feature_major);
 
 /* Critic half: d_v[r] = value_coef * dv * scale with the clipped value loss
  * (zealot-rl/src/ppo.rs:436-450); stats_dev[1] = sum of scaled value loss.
@@ -151,6 +155,42 @@ zl_status zl_adam_step(zl_ctx* ctx, float* p, const float* g, float* m, float* v
 /* out_dev[0] = sum of squares of x[0..n) (deterministic two-pass).
  * Replaces vortx Reduce::SqNorm (src/bin/biped_train_gpu.rs:1377-1397). */
 zl_status zl_grad_sqnorm(zl_ctx* ctx, const float* x, size_t n, float* out_dev);
+
+/* A device tensor of n floats (one gradient tensor of the trainer's
+ * per-tensor buffers: net.dw[l], net.db[l], dls). */
+typedef struct zl_tensor {
+  const float* ptr;
+  size_t n;
+} zl_tensor;
+
+/* The trainer's global grad-norm clip without the host round trip
+ * (src/bin/biped_train_gpu.rs:1368-1452: Reduce::SqNorm per tensor, the
+ * readback, the norm, OpAssign::Mul): norm = sqrt(sum over the `count`
+ * tensors of their sums of squares), fixed summation order;
+ * scale_dev[0] = max_norm / norm when max_norm > 0 and norm > max_norm, else
+ * 1; norm_dev[0] = norm (norm_dev may be NULL). Gradients are not modified:
+ * zl_adam_multi applies the scale. count <= 48. Asynchronous; device
+ * outputs. */
+zl_status zl_grad_clip_scale(zl_ctx* ctx, const zl_tensor* tensors, int count, float max_norm,
+                             float* scale_dev, float* norm_dev);
+
+/* One Adam parameter tensor with its gradient and moments (device, n floats each). */
+typedef struct zl_adam_tensor {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  size_t n;
+} zl_adam_tensor;
+
+/* One Adam step over `count` tensors in one launch (vortx Adam::step per
+ * tensor with AdamParams, src/bin/biped_train_gpu.rs:501-538,1453-1461;
+ * element update of zealot-rl/src/net.rs:240-245), each gradient multiplied
+ * by clip_scale_dev[0] first (a device scalar, e.g. from zl_grad_clip_scale;
+ * NULL: 1). count <= 48. Asynchronous. */
+zl_status zl_adam_multi(zl_ctx* ctx, const zl_adam_tensor* tensors, int count, float lr,
+                        float beta1, float beta2, float eps, float bc1, float bc2,
+                        const float* clip_scale_dev);
 
 /* GAE(lambda) for N independent trajectories of length T, one lane per env
  * (zealot-rl/src/ppo.rs:681-703, run per env by
@@ -253,10 +293,23 @@ typedef struct zl_ppo_config {
   int clamp_log_std;   /* ACTOR_CRITIC: [-1.6, 1.0] each step; GPU_TRAINER: [-1.6, 0.0] after */
 } zl_ppo_config;
 
+/* Layout bits of zl_batch.feature_major: the field is the trainer's
+ * feature-major [dim x n] tensor (element (sample i, feature k) at
+ * ptr[k * ld + i], ld >= n: f_obs / f_cobs / f_act of
+ * src/bin/biped_train_gpu.rs:1029-1030,1053-1056) instead of batch-major
+ * [n x dim] rows (ptr[i * ld + k]). */
+#define ZL_FM_OBS 1u
+#define ZL_FM_CRITIC_OBS 2u
+#define ZL_FM_ACTION 4u
+#define ZL_FM_MEAN_OLD 8u
+
 /* One rollout batch, structure of arrays, all DEVICE pointers, n samples in
- * batch order (sample i = row i). obs and critic_obs are the already
+ * batch order (sample i = column / row i). obs and critic_obs are the already
  * normalised observations (the trainer stages normalised obs,
- * src/bin/biped_train_gpu.rs:1021-1030). */
+ * src/bin/biped_train_gpu.rs:1021-1030). The update copies the batch into
+ * its own buffers at its start (inside the same graph replay), so the
+ * buffers may change from call to call without a re-capture; they must stay
+ * valid until the call returns. */
 typedef struct zl_batch {
   long long n;
   const float* obs;        int ld_obs;       /* [n x actor_dims[0]] */
@@ -267,6 +320,7 @@ typedef struct zl_batch {
   const float* value_old;                    /* [n] */
   float* adv;                                /* [n], normalised in place if requested */
   const float* ret;                          /* [n] */
+  unsigned feature_major;                    /* ZL_FM_* bits; 0 = all batch-major */
 } zl_batch;
 
 /* PpoStats (zealot-rl/src/ppo.rs:90-102) plus the trainer's epoch count. */
@@ -302,9 +356,15 @@ zl_status zl_ppo_get_counters(zl_ppo* ppo, int* t, unsigned long long* gstep);
  * src/bin/biped_train_gpu.rs:1164-1553 per config->semantics). */
 zl_status zl_ppo_update(zl_ppo* ppo, const zl_batch* batch, const zl_ppo_config* config,
                         zl_ppo_stats* stats);
+/* Captured update graphs of this handle so far and the host time of the last
+ * capture + instantiation (milliseconds). A graph is re-captured only when the
+ * update's shapes, strides, layouts or configuration change, or when a buffer
+ * it uses had to grow; new batch pointers alone never re-capture. */
+zl_status zl_ppo_graph_info(zl_ppo* ppo, long long* captures, double* last_capture_ms);
 /* Gradients of one minibatch without stepping: forward, PPO losses and
  * backward over batch rows [row0, row0 + rows) (or rows perm_dev[row0 + r] when
- * perm_dev, a device int array, is non-NULL), leaving the summed gradients in
+ * perm_dev, a device int array whose entries are in [0, n), is non-NULL;
+ * row0 + rows <= n either way), leaving the summed gradients in
  * the flat gradient buffer (read them with zl_ppo_get_grads) and
  * stats[3] = {surrogate, value_loss, kl} (host). The accumulation of
  * zealot-rl/src/ppo.rs:406-462 before clip / Adam. Blocks until done. */

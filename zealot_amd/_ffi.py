@@ -63,7 +63,22 @@ class zl_batch(C.Structure):
         ("value_old", vp),
         ("adv", vp),
         ("ret", vp),
+        ("feature_major", C.c_uint),
     ]
+
+
+ZL_FM_OBS = 1
+ZL_FM_CRITIC_OBS = 2
+ZL_FM_ACTION = 4
+ZL_FM_MEAN_OLD = 8
+
+
+class zl_tensor(C.Structure):
+    _fields_ = [("ptr", vp), ("n", C.c_size_t)]
+
+
+class zl_adam_tensor(C.Structure):
+    _fields_ = [("p", vp), ("g", vp), ("m", vp), ("v", vp), ("n", C.c_size_t)]
 
 
 class zl_ppo_stats(C.Structure):
@@ -121,7 +136,7 @@ SIGNATURES = {
     "zl_ppo_actor_grad": (
         C.c_int,
         [vp, vp, C.c_int, vp, C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int,
-         C.c_float, C.c_float, C.c_float, vp, C.c_int, vp, vp],
+         C.c_float, C.c_float, C.c_float, vp, C.c_int, vp, vp, C.c_int],
     ),
     "zl_ppo_value_grad": (
         C.c_int,
@@ -133,6 +148,12 @@ SIGNATURES = {
          C.c_float, C.c_float],
     ),
     "zl_grad_sqnorm": (C.c_int, [vp, vp, C.c_size_t, vp]),
+    "zl_grad_clip_scale": (C.c_int, [vp, C.POINTER(zl_tensor), C.c_int, C.c_float, vp, vp]),
+    "zl_adam_multi": (
+        C.c_int,
+        [vp, C.POINTER(zl_adam_tensor), C.c_int, C.c_float, C.c_float, C.c_float, C.c_float,
+         C.c_float, C.c_float, vp],
+    ),
     "zl_gae": (
         C.c_int,
         [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_longlong, C.c_longlong, C.c_longlong,
@@ -184,6 +205,7 @@ SIGNATURES = {
         [vp, C.POINTER(zl_batch), C.POINTER(zl_ppo_config), C.c_longlong, C.c_int, vp, fp],
     ),
     "zl_ppo_get_grads": (C.c_int, [vp, vp, vp, vp]),
+    "zl_ppo_graph_info": (C.c_int, [vp, C.POINTER(C.c_longlong), C.POINTER(C.c_double)]),
     "zl_ppo_values": (C.c_int, [vp, vp, C.c_int, C.c_longlong, vp]),
     "zl_ppo_actor_mean": (C.c_int, [vp, vp, C.c_int, C.c_longlong, vp, C.c_int]),
 }

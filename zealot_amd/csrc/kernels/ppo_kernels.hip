@@ -71,11 +71,11 @@ __device__ void actor_loss_body(const ActorLossArgs& p) {
   auto fetch = [&](int rr) {
     In x;
     const long long s = p.perm ? p.perm[p.row0 + rr] : (long long)(p.row0 + rr);
-    x.mu = on ? p.mean[(long long)rr * p.ldm + k] : 0.f;
-    x.act = on ? p.action[s * p.ldact + k] : 0.f;
+    x.mu = on ? p.mean[(long long)rr * p.ldm + (long long)k * p.cm] : 0.f;
+    x.act = on ? p.action[s * p.ldact + (long long)k * p.cact] : 0.f;
     x.lpo = p.logp_old[s];
     x.adv = p.adv[s];
-    x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
+    x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + (long long)k * p.cmo] : 0.f;
     return x;
   };
   // Rows per group whose loads are issued together (two for 64-lane groups,
@@ -110,7 +110,7 @@ __device__ void actor_loss_body(const ActorLossArgs& p) {
       }
       c += -p.entropy_coef * p.scale;
       if (on) {
-        p.delta[(long long)r * p.ldd + k] = gm;
+        p.delta[(long long)r * p.ldd + (long long)k * p.cdd] = gm;
         gacc += c;
       }
       sacc += surr * p.scale;
@@ -517,7 +517,12 @@ __device__ void adv_norm_body(const AdvNormArgs& p) {
     if (threadIdx.x == 0) p.part2[blockIdx.x] = tot;
   } else {
     const float mean = bc[0], sd = bc[1];
-    for (long long i = lo + threadIdx.x; i < hi; i += kThreads) p.x[i] = (p.x[i] - mean) / sd;
+    float* const wb = p.wb ? *p.wb : nullptr;
+    for (long long i = lo + threadIdx.x; i < hi; i += kThreads) {
+      const float y = (p.x[i] - mean) / sd;
+      p.x[i] = y;
+      if (wb) wb[i] = y;
+    }
   }
 }
 
@@ -619,6 +624,175 @@ __device__ void sample_body(const SampleArgs& p) {
   p.logp[r] = lp;
 }
 
+// Batch staging (see StageArgs): every field of a rollout batch copied into
+// library-owned batch-major buffers with 16-byte aligned, zero-padded rows;
+// feature-major sources ([dim x n], the reference trainer's staging layout,
+// src/bin/biped_train_gpu.rs:1029-1068) are transposed through LDS.
+__device__ void stage_body(const StageArgs& p) {
+  __shared__ float tile[kStageRows][kStageCols + 1];
+  if (p.guard && *p.guard == 0) return;
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < p.njobs && b >= p.job[j + 1].blk0) ++j;
+  const StageJob& jb = p.job[j];
+  const int lb = b - jb.blk0;
+  if (lb >= jb.blocks) return;
+  const int t = threadIdx.x;
+  if (jb.vec) {
+    const float* src = p.ptrs->vec[jb.slot];
+    const long long base = (long long)lb * kStageVec;
+#pragma unroll
+    for (int u = 0; u < kStageVec / kThreads; ++u) {
+      const long long r = base + u * kThreads + t;
+      if (r < p.rows) {
+        const long long sr = p.perm ? (long long)p.perm[p.row0 + r] : p.row0 + r;
+        jb.dst[r] = src[sr];
+      }
+    }
+    return;
+  }
+  const float* src = p.ptrs->mat[jb.slot];
+  const long long r0 = (long long)(lb / jb.tiles_c) * kStageRows;
+  const int c0 = (lb % jb.tiles_c) * kStageCols;
+  if (jb.fm) {
+    // Read along samples (coalesced in a feature row), write along features.
+    const int rr = t % kStageRows, cq = t / kStageRows;
+    const long long r = r0 + rr;
+    long long sr = 0;
+    if (r < p.rows) sr = p.perm ? (long long)p.perm[p.row0 + r] : p.row0 + r;
+#pragma unroll
+    for (int u = 0; u < kStageCols / (kThreads / kStageRows); ++u) {
+      const int c = cq + u * (kThreads / kStageRows);
+      const int cg = c0 + c;
+      tile[rr][c] = (r < p.rows && cg < jb.cols) ? src[(long long)cg * jb.ld + sr] : 0.f;
+    }
+    __syncthreads();
+    const int c = t % kStageCols, rq = t / kStageCols;
+    const int cg = c0 + c;
+#pragma unroll
+    for (int u = 0; u < kStageRows / (kThreads / kStageCols); ++u) {
+      const int rr2 = rq + u * (kThreads / kStageCols);
+      const long long r2 = r0 + rr2;
+      if (r2 < p.rows && cg < jb.ldd) jb.dst[r2 * jb.ldd + cg] = tile[rr2][c];
+    }
+  } else {
+    const int c = t % kStageCols, rq = t / kStageCols;
+    const int cg = c0 + c;
+#pragma unroll
+    for (int u = 0; u < kStageRows / (kThreads / kStageCols); ++u) {
+      const long long r = r0 + rq + u * (kThreads / kStageCols);
+      if (r >= p.rows || cg >= jb.ldd) continue;
+      float v = 0.f;
+      if (cg < jb.cols) {
+        const long long sr = p.perm ? (long long)p.perm[p.row0 + r] : p.row0 + r;
+        v = src[sr * jb.ld + cg];
+      }
+      jb.dst[r * jb.ldd + cg] = v;
+    }
+  }
+}
+
+// Per-block sums of squares over a list of tensors (Reduce::SqNorm of every
+// gradient tensor, src/bin/biped_train_gpu.rs:1377-1397): block b covers
+// chunk b - blk0[j] of tensor j; partial b = its sum (fixed in-block tree).
+__device__ void sumsq_multi_body(const SumsqMultiArgs& p) {
+  __shared__ float red[kThreads];
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < p.count && b >= p.blk0[j + 1]) ++j;
+  const long long lo = (long long)(b - p.blk0[j]) * p.chunk;
+  const long long hi = min(p.n[j], lo + p.chunk);
+  const float* x = p.x[j];
+  float s = 0.f;
+  if (((uintptr_t)x & 15u) == 0) {
+    const long long hi4 = lo + ((hi - lo) & ~3LL);
+    for (long long i = lo + 4 * threadIdx.x; i < hi4; i += 4 * kThreads) {
+      const float4 v = *reinterpret_cast<const float4*>(x + i);
+      s += v.x * v.x;
+      s += v.y * v.y;
+      s += v.z * v.z;
+      s += v.w * v.w;
+    }
+    for (long long i = hi4 + threadIdx.x; i < hi; i += kThreads) s += x[i] * x[i];
+  } else {
+    for (long long i = lo + threadIdx.x; i < hi; i += kThreads) s += x[i] * x[i];
+  }
+  const float tot = block_sum(s, red);
+  if (threadIdx.x == 0) p.part[b] = tot;
+}
+
+// One wavefront: the norm from the partials in block order, and the clip
+// scale of the trainer's global clip (src/bin/biped_train_gpu.rs:1398-1404):
+// max_norm / norm when norm > max_norm, else 1.
+__device__ void clip_scale_body(const ClipScaleArgs& p) {
+  if (threadIdx.x >= 64) return;
+  const float sq = wave_sum_strided(p.part, p.nparts, 1);
+  if (threadIdx.x != 0) return;
+  const float norm = sqrtf(sq);
+  float s = 1.0f;
+  if (p.max_norm > 0.0f && norm > p.max_norm) s = p.max_norm / norm;
+  *p.scale = s;
+  if (p.norm) *p.norm = norm;
+}
+
+// Adam element update of zealot-rl/src/net.rs:240-245 over a list of tensors
+// (vortx Adam::step per tensor, src/bin/biped_train_gpu.rs:501-538,
+// 1453-1461), the clip scale read from the device.
+__device__ void adam_multi_body(const AdamMultiArgs& p) {
+  const int b = blockIdx.x;
+  int j = 0;
+  while (j + 1 < p.count && b >= p.blk0[j + 1]) ++j;
+  const AdamTensor& T = p.t[j];
+  const long long i0 = ((long long)(b - p.blk0[j]) * kThreads + threadIdx.x) * 4;
+  if (i0 >= T.n) return;
+  const float sc = p.scale ? *p.scale : 1.0f;
+  const float b1 = p.beta1, b2 = p.beta2, eps = p.eps, lr = p.lr, bc1 = p.bc1, bc2 = p.bc2;
+  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+  const bool quad = i0 + 4 <= T.n &&
+                    ((((uintptr_t)T.p | (uintptr_t)T.g | (uintptr_t)T.m | (uintptr_t)T.v) & 15u) == 0);
+  float x[4], g[4], m[4], v[4];
+  if (quad) {
+    const float4 x4 = *reinterpret_cast<const float4*>(T.p + i0);
+    const float4 g4 = *reinterpret_cast<const float4*>(T.g + i0);
+    const float4 m4 = *reinterpret_cast<const float4*>(T.m + i0);
+    const float4 v4 = *reinterpret_cast<const float4*>(T.v + i0);
+    x[0] = x4.x, x[1] = x4.y, x[2] = x4.z, x[3] = x4.w;
+    g[0] = g4.x, g[1] = g4.y, g[2] = g4.z, g[3] = g4.w;
+    m[0] = m4.x, m[1] = m4.y, m[2] = m4.z, m[3] = m4.w;
+    v[0] = v4.x, v[1] = v4.y, v[2] = v4.z, v[3] = v4.w;
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const bool in = i0 + u < T.n;
+      x[u] = in ? T.p[i0 + u] : 0.f;
+      g[u] = in ? T.g[i0 + u] : 0.f;
+      m[u] = in ? T.m[i0 + u] : 0.f;
+      v[u] = in ? T.v[i0 + u] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float gr = g[u] * sc;
+    m[u] = b1 * m[u] + omb1 * gr;
+    v[u] = b2 * v[u] + omb2 * gr * gr;
+    x[u] = x[u] - lr * (m[u] / bc1) / (sqrtf(v[u] / bc2) + eps);
+  }
+  if (quad) {
+    *reinterpret_cast<float4*>(T.m + i0) = make_float4(m[0], m[1], m[2], m[3]);
+    *reinterpret_cast<float4*>(T.v + i0) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(T.p + i0) = make_float4(x[0], x[1], x[2], x[3]);
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (i0 + u < T.n) {
+        T.m[i0 + u] = m[u];
+        T.v[i0 + u] = v[u];
+        T.p[i0 + u] = x[u];
+      }
+    }
+  }
+}
+
 __device__ void clamp_body(const ClampArgs& p) {
   const int i = blockIdx.x * kThreads + threadIdx.x;
   if (i < p.n) p.x[i] = clampf(p.x[i], p.lo, p.hi);
@@ -655,3 +829,7 @@ ZK_KERNEL(zk_sample, SampleArgs, sample_body)
 extern "C" __global__ __launch_bounds__(256) void zk_sample_g32(zk::SampleArgs p) { zk::sample_lanes_body<32>(p); }
 extern "C" __global__ __launch_bounds__(256) void zk_sample_g64(zk::SampleArgs p) { zk::sample_lanes_body<64>(p); }
 ZK_KERNEL(zk_clamp, ClampArgs, clamp_body)
+ZK_KERNEL(zk_stage, StageArgs, stage_body)
+ZK_KERNEL(zk_sumsq_multi, SumsqMultiArgs, sumsq_multi_body)
+ZK_KERNEL(zk_clip_scale, ClipScaleArgs, clip_scale_body)
+ZK_KERNEL(zk_adam_multi, AdamMultiArgs, adam_multi_body)

@@ -133,7 +133,11 @@ struct ActorLossArgs {
   float* gls_part;        // [A x blocks] log_std gradient partials (component-major)
   float* stat_part;       // [2 x blocks] surrogate, kl partials
   const int* guard;
+  // Element (row r, component k) of mean / action / mean_old / delta is at
+  // r * ld + k * c: batch-major (c = 1) or feature-major (ld = 1, c = the
+  // feature stride).
   int ldm, ldact, ldmo, ldd;
+  int cm, cact, cmo, cdd;
   int row0, rows, A;
   int rows_per_block;  // samples handled by one block
   int group;           // lanes per sample: 32 (A <= 32) or 64 (A <= 64)
@@ -274,6 +278,7 @@ struct AdvNormArgs {
   int nparts;
   int chunk;     // elements per block
   int phase;     // 0: sums, 1: squared deviations, 2: apply
+  float* const* wb;  // nullable: phase 2 also writes the result to *wb (device-resident pointer)
 };
 
 struct EluBwdArgs {
@@ -334,6 +339,84 @@ struct ClampArgs {
   int n;
   float lo, hi;
   const int* guard;
+};
+
+// The caller's pointers of one rollout batch, uploaded to device memory with
+// every update so that a captured update graph reads them at replay time
+// instead of baking them in (zk_stage, and the advantage write-back).
+struct BatchPtrs {
+  const float* mat[4];  // obs, critic_obs, action, mean_old (nullable)
+  const float* vec[4];  // logp_old, value_old, adv, ret
+  float* adv_out;       // the caller's adv: normalised advantages are written back
+};
+
+// zk_stage: copies batch fields into library-owned batch-major buffers.
+// A matrix job moves tiles of kStageRows samples x kStageCols features; a
+// feature-major source (element (sample i, feature k) at k * ld + i) is
+// transposed through LDS, a batch-major one (i * ld + k) copied row by row;
+// columns [cols, ldd) of the destination are written as zeros. A vector job
+// moves kStageVec elements per block. Blocks [blk0, blk0 + blocks) of the
+// 1-D grid belong to a job.
+constexpr int kStageRows = 64;
+constexpr int kStageCols = 32;
+constexpr int kStageVec = 2048;
+constexpr int kMaxStageJobs = 8;
+struct StageJob {
+  float* dst;    // [rows x ldd]
+  long long ld;  // source stride (row stride, or feature stride when fm)
+  int cols, ldd;
+  int fm;        // source is feature-major
+  int slot;      // BatchPtrs::mat[slot] (matrix job) or vec[slot] (vector job)
+  int vec;
+  int tiles_c;   // column tiles of a matrix job
+  int blk0, blocks;
+};
+struct StageArgs {
+  const BatchPtrs* ptrs;
+  const int* perm;  // source row of staged row r = perm ? perm[row0 + r] : row0 + r
+  const int* guard;
+  long long rows, row0;
+  StageJob job[kMaxStageJobs];
+  int njobs;
+};
+
+// Sum of squares over a list of tensors (zk_sumsq_multi): blocks [blk0[j],
+// blk0[j + 1]) cover tensor j in chunks of `chunk` elements, one partial per
+// block; zk_clip_scale then adds the partials in block order, takes the norm
+// and the clip scale.
+constexpr int kMaxNormTensors = 48;
+struct SumsqMultiArgs {
+  const float* x[kMaxNormTensors];
+  long long n[kMaxNormTensors];
+  int blk0[kMaxNormTensors + 1];
+  int count, chunk;
+  float* part;  // one partial per block
+};
+struct ClipScaleArgs {
+  const float* part;
+  int nparts;
+  float max_norm;  // <= 0: scale 1
+  float* scale;    // [1] max_norm / norm when norm > max_norm, else 1
+  float* norm;     // [1] nullable
+};
+
+// Adam over a list of tensors in one launch (zk_adam_multi): blocks
+// [blk0[j], blk0[j + 1]) cover tensor j, 4 elements per thread; the gradient
+// is multiplied by *scale first when scale is set.
+constexpr int kMaxAdamTensors = 48;
+struct AdamTensor {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  long long n;
+};
+struct AdamMultiArgs {
+  AdamTensor t[kMaxAdamTensors];
+  int blk0[kMaxAdamTensors + 1];
+  int count;
+  const float* scale;  // nullable
+  float lr, bc1, bc2, beta1, beta2, eps;
 };
 
 }  // namespace zk

@@ -42,6 +42,10 @@ enum KernelId : int {
   K_NORM_COMMIT,
   K_SAMPLE_G32,
   K_SAMPLE_G64,
+  K_STAGE,
+  K_SUMSQ_MULTI,
+  K_CLIP_SCALE,
+  K_ADAM_MULTI,
   K_GEMM_BASE
 };
 

@@ -12,7 +12,9 @@
 // zero Adam update). Activations are batch-major [rows x ld] with ld the
 // feature count rounded up to 4.
 #include <algorithm>
+#include <chrono>
 #include <cmath>
+#include <cstddef>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -22,9 +24,7 @@
 namespace zl {
 
 zl_status adv_normalize_into(zl_ctx* c, float* adv, long long n, float* scratch, int nparts,
-                             int chunk, const int* guard);
-
-static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+                             int chunk, const int* guard, float* const* wb);
 
 // Offsets of one MLP's tensors inside the flat buffer.
 struct NetLayout {
@@ -527,10 +527,18 @@ struct zl_ppo {
   size_t pws_cap = 0;
   PartialPlan pplan;
   size_t adv_part_cap = 0;
+  // Device scalars of an update followed by the caller's batch pointers
+  // (UpdateIn), uploaded together before every update.
   zk::DevState* dstate = nullptr;
+  zk::BatchPtrs* bptrs = nullptr;
   float* ls_old = nullptr;
   float* stat_out = nullptr;  // [8] scratch for zl_ppo_minibatch_grads
-  // Observation staging (padded, 16-byte aligned rows) and shuffle orders.
+  // The staged batch (zk_stage): actor obs [n x odp], critic obs [n x cdp],
+  // action [n x A], mean_old [n x A], then logp_old, value_old, adv, ret [n].
+  float* stg[8] = {};
+  size_t stg_cap[8] = {};
+  // Observation staging of the rollout step and the chunked forwards
+  // (padded, 16-byte aligned rows) and shuffle orders.
   float* obs_pad = nullptr;
   size_t obs_pad_floats = 0;
   float* cobs_pad = nullptr;
@@ -539,16 +547,26 @@ struct zl_ppo {
   size_t perm_cap = 0;
   std::vector<int> perm_host;
   zk::DevState hstate{};
+  // Bumped whenever a device buffer of this handle is reallocated: a captured
+  // graph is only replayed while every buffer it references is still alive.
+  unsigned long long gen = 0;
   // Captured update graph and the signature it was captured for.
   hipGraphExec_t gexec = nullptr;
   std::string gkey;
+  long long captures = 0;
+  double capture_ms = 0.0;
 };
 
 namespace {
 
-zl_status grow(zl_ctx* c, void** p, size_t* cap, size_t bytes) {
+// Grow a device buffer of the handle (outside graph capture: may synchronize).
+// A reallocation bumps the handle's buffer generation, which is part of the
+// captured update graph's key.
+zl_status grow(zl_ppo* pp, void** p, size_t* cap, size_t bytes) {
+  zl_ctx* c = pp->c;
   if (bytes <= *cap) return ZL_OK;
   ZL_HIP(c, hipStreamSynchronize(c->stream));
+  pp->gen += 1;
   if (*p) ZL_HIP(c, hipFree(*p));
   *p = nullptr;
   *cap = 0;
@@ -557,13 +575,19 @@ zl_status grow(zl_ctx* c, void** p, size_t* cap, size_t bytes) {
   return ZL_OK;
 }
 
+// Host image of the device block at zl_ppo::dstate.
+struct UpdateIn {
+  zk::DevState st;
+  zk::BatchPtrs ptrs;
+};
+
 // Lay out the weight-gradient partial regions for minibatches of `rows` rows
 // and grow their buffer (outside graph capture: may synchronize).
 zl_status ensure_partials(zl_ppo* p, int rows) {
   const NetLayout* nls[2] = {&p->actor, &p->critic};
   p->pplan.build(p->c, nls, rows, p->fused_head);
   size_t cap = p->pws_cap * 4;
-  zl_status s = grow(p->c, (void**)&p->pws, &cap, p->pplan.total * 4 + 4);
+  zl_status s = grow(p, (void**)&p->pws, &cap, p->pplan.total * 4 + 4);
   p->pws_cap = cap / 4;
   return s;
 }
@@ -687,6 +711,7 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     al.logp_old = b->logp_old;
     al.mean_old = b->mean_old;
     al.ldmo = b->ld_mean_old;
+    al.cm = al.cact = al.cmo = al.cdd = 1;
     al.log_std = p->params + p->ls_off;
     al.perm = perm;
     al.row0 = row0;
@@ -729,35 +754,146 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
 struct Plan {
   int mode, mb, n_mb, epochs;
   long long n;
-  bool stage_obs, stage_cobs, share_cobs, shuffle;
+  bool share_cobs, shuffle;
   const float* X;
   int ldx;
   const float* XC;
   int ldxc;
+  zl_batch sb;  // the staged batch: batch-major rows in the handle's buffers
+  zk::StageArgs stage;
+  int stage_blocks;
   zk::PpoParams pp;
 };
 
-zl_status enqueue_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg, const Plan& pl) {
+// A batch field with element (sample i, feature k) at i * ld + k (batch-major)
+// or k * ld + i (feature-major) over n samples of `cols` features.
+bool field_ok(long long n, int cols, int ld, bool fm) { return fm ? ld >= n : ld >= cols; }
+
+zl_status check_batch(zl_ppo* p, const zl_batch* b, const char* who) {
+  zl_ctx* c = p->c;
+  if (!b->obs || !b->critic_obs || !b->action || !b->logp_old || !b->value_old || !b->adv ||
+      !b->ret)
+    return fail(c, ZL_ERR_INVALID, "%s: null batch pointer", who);
+  if (b->n < 0 || b->n > (1LL << 31) - 1)
+    return fail(c, ZL_ERR_INVALID, "%s: n = %lld out of range", who, b->n);
+  const unsigned fm = b->feature_major;
+  if (fm & ~(ZL_FM_OBS | ZL_FM_CRITIC_OBS | ZL_FM_ACTION | ZL_FM_MEAN_OLD))
+    return fail(c, ZL_ERR_INVALID, "%s: unknown feature_major bits 0x%x", who, fm);
+  if (!field_ok(b->n, p->actor.dims[0], b->ld_obs, fm & ZL_FM_OBS) ||
+      !field_ok(b->n, p->critic.dims[0], b->ld_critic_obs, fm & ZL_FM_CRITIC_OBS) ||
+      !field_ok(b->n, p->A, b->ld_action, fm & ZL_FM_ACTION) ||
+      (b->mean_old && !field_ok(b->n, p->A, b->ld_mean_old, fm & ZL_FM_MEAN_OLD)))
+    return fail(c, ZL_ERR_INVALID, "%s: a stride is smaller than the row (or, feature-major, than n)",
+                who);
+  return ZL_OK;
+}
+
+// Lay out the staged copy of `rows` batch samples (source sample perm[row0 + r],
+// or row0 + r) in the handle's buffers, growing them as needed: the zk_stage
+// launch reading the caller's pointers from p->bptrs, and the staged batch
+// view (batch-major rows; observation rows padded to a multiple of 4 floats
+// and zero-filled, 16-byte aligned for the layer-0 GEMM loads).
+zl_status plan_stage(zl_ppo* p, const zl_batch* b, long long rows, const int* perm, long long row0,
+                     zk::StageArgs* st, int* blocks, zl_batch* sb, bool* share_out) {
+  const int od = p->actor.dims[0], cd = p->critic.dims[0], A = p->A;
+  const int odp = (int)round_up(od, 4), cdp = (int)round_up(cd, 4);
+  const unsigned fm = b->feature_major;
+  const bool share = b->critic_obs == b->obs && b->ld_critic_obs == b->ld_obs && od == cd &&
+                     ((fm & ZL_FM_OBS) != 0) == ((fm & ZL_FM_CRITIC_OBS) != 0);
+  const bool has_mo = b->mean_old != nullptr;
+  const long long need[8] = {rows * odp, share ? 0 : rows * cdp, rows * A, has_mo ? rows * A : 0,
+                             rows, rows, rows, rows};
+  for (int i = 0; i < 8; ++i) {
+    if (need[i] <= 0) continue;
+    zl_status s = grow(p, (void**)&p->stg[i], &p->stg_cap[i], (size_t)need[i] * 4);
+    if (s) return s;
+  }
+  *st = zk::StageArgs{};
+  st->ptrs = p->bptrs;
+  st->perm = perm;
+  st->rows = rows;
+  st->row0 = row0;
+  int blk = 0, nj = 0;
+  auto mat = [&](int slot, int cols, int ld, int ldd, bool f) {
+    zk::StageJob& j = st->job[nj++];
+    j.dst = p->stg[slot];
+    j.ld = ld;
+    j.cols = cols;
+    j.ldd = ldd;
+    j.fm = f ? 1 : 0;
+    j.slot = slot;
+    j.vec = 0;
+    j.tiles_c = (int)cdiv(ldd, zk::kStageCols);
+    j.blk0 = blk;
+    j.blocks = (int)(cdiv(rows, zk::kStageRows) * j.tiles_c);
+    blk += j.blocks;
+  };
+  mat(0, od, b->ld_obs, odp, fm & ZL_FM_OBS);
+  if (!share) mat(1, cd, b->ld_critic_obs, cdp, fm & ZL_FM_CRITIC_OBS);
+  mat(2, A, b->ld_action, A, fm & ZL_FM_ACTION);
+  if (has_mo) mat(3, A, b->ld_mean_old, A, fm & ZL_FM_MEAN_OLD);
+  for (int v = 0; v < 4; ++v) {
+    zk::StageJob& j = st->job[nj++];
+    j.dst = p->stg[4 + v];
+    j.ld = 1;
+    j.cols = 1;
+    j.ldd = 1;
+    j.slot = v;
+    j.vec = 1;
+    j.blk0 = blk;
+    j.blocks = (int)cdiv(rows, zk::kStageVec);
+    blk += j.blocks;
+  }
+  st->njobs = nj;
+  *blocks = rows > 0 ? blk : 0;
+  *sb = zl_batch{};
+  sb->n = rows;
+  sb->obs = p->stg[0];
+  sb->ld_obs = odp;
+  sb->critic_obs = share ? p->stg[0] : p->stg[1];
+  sb->ld_critic_obs = share ? odp : cdp;
+  sb->action = p->stg[2];
+  sb->ld_action = A;
+  sb->mean_old = has_mo ? p->stg[3] : nullptr;
+  sb->ld_mean_old = A;
+  sb->logp_old = p->stg[4];
+  sb->value_old = p->stg[5];
+  sb->adv = p->stg[6];
+  sb->ret = p->stg[7];
+  *share_out = share;
+  return ZL_OK;
+}
+
+zk::BatchPtrs batch_ptrs(const zl_batch* b) {
+  zk::BatchPtrs h{};
+  h.mat[0] = b->obs;
+  h.mat[1] = b->critic_obs;
+  h.mat[2] = b->action;
+  h.mat[3] = b->mean_old;
+  h.vec[0] = b->logp_old;
+  h.vec[1] = b->value_old;
+  h.vec[2] = b->adv;
+  h.vec[3] = b->ret;
+  h.adv_out = b->adv;
+  return h;
+}
+
+zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
   zl_ctx* c = p->c;
   // Kernels after a KL early stop are skipped through the device flag
   // `active`; only the early stop clears it, so without one the kernels get
   // no flag and skip the dependent load of it at their start.
   const int* guard = pl.pp.early_stop ? &p->dstate->active : nullptr;
   const int A = p->A;
-  zl_status s = ZL_OK;
+  const zl_batch* b = &pl.sb;
+  zl_status s = launch(c, K_STAGE, (unsigned)pl.stage_blocks, 1, 1, pl.stage);
+  if (s) return s;
   if (cfg->normalize_adv) {
+    // In place in the staged copy, and written back to the caller's adv
+    // (ActorCritic::update normalises the batch it was given, ppo.rs:343-348).
     const int nparts = (int)cdiv(pl.n, zl_ppo::kAdvChunk);
-    s = adv_normalize_into(c, b->adv, pl.n, p->adv_part, nparts, zl_ppo::kAdvChunk, guard);
-    if (s) return s;
-  }
-  if (pl.stage_obs) {
-    s = copy_rows(c, p->obs_pad, pl.ldx, b->obs, b->ld_obs, p->actor.dims[0], pl.n, nullptr, 0,
-                  guard, true);
-    if (s) return s;
-  }
-  if (pl.stage_cobs && !pl.share_cobs) {
-    s = copy_rows(c, p->cobs_pad, pl.ldxc, b->critic_obs, b->ld_critic_obs, p->critic.dims[0],
-                  pl.n, nullptr, 0, guard, true);
+    s = adv_normalize_into(c, b->adv, pl.n, p->adv_part, nparts, zl_ppo::kAdvChunk, guard,
+                           &p->bptrs->adv_out);
     if (s) return s;
   }
   const int La = p->actor.L;
@@ -909,7 +1045,8 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
       p->sq_cap += (int)(cdiv(cdiv((long long)nl->dims[l + 1] * nl->dims[l], 4), min_per_block) +
                          cdiv(nl->dims[l + 1], min_per_block));
   dalloc((void**)&p->sq_part, (size_t)p->sq_cap * 4);
-  dalloc((void**)&p->dstate, sizeof(zk::DevState));
+  dalloc((void**)&p->dstate, sizeof(UpdateIn));
+  if (!s) p->bptrs = (zk::BatchPtrs*)((char*)p->dstate + offsetof(UpdateIn, ptrs));
   dalloc((void**)&p->ls_old, (size_t)p->A * 4);
   dalloc((void**)&p->stat_out, 8 * 4);
   if (!s && hipStreamSynchronize(c->stream) != hipSuccess)
@@ -935,6 +1072,8 @@ void zl_ppo_destroy(zl_ppo* p) {
                   (void*)p->kl_part, (void*)p->sq_part, (void*)p->adv_part, (void*)p->dstate,
                   (void*)p->ls_old, (void*)p->obs_pad, (void*)p->cobs_pad, (void*)p->perm,
                   (void*)p->stat_out, (void*)p->pws})
+    if (b) hipFree(b);
+  for (float* b : p->stg)
     if (b) hipFree(b);
   delete p;
 }
@@ -1011,15 +1150,10 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
   const int mode = cfg->semantics;
   if (mode != ZL_SEMANTICS_ACTOR_CRITIC && mode != ZL_SEMANTICS_GPU_TRAINER)
     return fail(c, ZL_ERR_INVALID, "zl_ppo_update: unknown semantics %d", mode);
-  if (!b->obs || !b->critic_obs || !b->action || !b->logp_old || !b->value_old || !b->adv ||
-      !b->ret)
-    return fail(c, ZL_ERR_INVALID, "zl_ppo_update: null batch pointer");
+  zl_status s = check_batch(p, b, "zl_ppo_update");
+  if (s) return s;
   if (cfg->epochs < 0 || cfg->minibatches < 1 || b->n < cfg->minibatches)
     return fail(c, ZL_ERR_INVALID, "zl_ppo_update: n %lld < minibatches %d", b->n, cfg->minibatches);
-  if (b->ld_obs < p->actor.dims[0] || b->ld_critic_obs < p->critic.dims[0] ||
-      b->ld_action < p->A || (b->mean_old && b->ld_mean_old < p->A))
-    return fail(c, ZL_ERR_INVALID, "zl_ppo_update: row stride smaller than the row");
-  if (b->n > (1LL << 31) - 1) return fail(c, ZL_ERR_INVALID, "zl_ppo_update: n too large");
   Plan pl{};
   pl.mode = mode;
   pl.n = b->n;
@@ -1030,47 +1164,20 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
     return fail(c, ZL_ERR_INVALID, "zl_ppo_update: minibatch of %d rows > capacity %d", pl.mb,
                 p->mb_cap);
   pl.shuffle = mode == ZL_SEMANTICS_ACTOR_CRITIC && cfg->shuffle;
-  // Observation staging: layer-0 operands need 16-byte aligned rows.
-  const int od = p->actor.dims[0], cd = p->critic.dims[0];
-  const int odp = (int)round_up(od, 4), cdp = (int)round_up(cd, 4);
-  pl.stage_obs = !(aligned16(b->obs) && b->ld_obs % 4 == 0);
-  pl.stage_cobs = !(aligned16(b->critic_obs) && b->ld_critic_obs % 4 == 0);
-  pl.share_cobs = pl.stage_obs && pl.stage_cobs && b->critic_obs == b->obs &&
-                  b->ld_critic_obs == b->ld_obs && od == cd;
-  zl_status s = ZL_OK;
-  if (pl.stage_obs) {
-    size_t cap = p->obs_pad_floats * 4;
-    if ((s = grow(c, (void**)&p->obs_pad, &cap, (size_t)pl.n * odp * 4))) return s;
-    p->obs_pad_floats = cap / 4;
-    pl.X = p->obs_pad;
-    pl.ldx = odp;
-  } else {
-    pl.X = b->obs;
-    pl.ldx = b->ld_obs;
-  }
-  if (pl.stage_cobs) {
-    if (pl.share_cobs) {
-      pl.XC = p->obs_pad;
-      pl.ldxc = odp;
-    } else {
-      size_t cap = p->cobs_pad_floats * 4;
-      if ((s = grow(c, (void**)&p->cobs_pad, &cap, (size_t)pl.n * cdp * 4))) return s;
-      p->cobs_pad_floats = cap / 4;
-      pl.XC = p->cobs_pad;
-      pl.ldxc = cdp;
-    }
-  } else {
-    pl.XC = b->critic_obs;
-    pl.ldxc = b->ld_critic_obs;
-  }
+  if ((s = plan_stage(p, b, pl.n, nullptr, 0, &pl.stage, &pl.stage_blocks, &pl.sb, &pl.share_cobs)))
+    return s;
+  pl.X = pl.sb.obs;
+  pl.ldx = pl.sb.ld_obs;
+  pl.XC = pl.sb.critic_obs;
+  pl.ldxc = pl.sb.ld_critic_obs;
   if (cfg->normalize_adv) {
     size_t need = (size_t)2 * cdiv(pl.n, zl_ppo::kAdvChunk) * 4;
-    if ((s = grow(c, (void**)&p->adv_part, &p->adv_part_cap, need))) return s;
+    if ((s = grow(p, (void**)&p->adv_part, &p->adv_part_cap, need))) return s;
   }
   if ((s = ensure_partials(p, pl.mb))) return s;
   if (pl.shuffle) {
     size_t cap = p->perm_cap * 4;
-    if ((s = grow(c, (void**)&p->perm, &cap, (size_t)pl.epochs * pl.n * 4 + 4))) return s;
+    if ((s = grow(p, (void**)&p->perm, &cap, (size_t)pl.epochs * pl.n * 4 + 4))) return s;
     p->perm_cap = cap / 4;
     // Per-epoch Fisher-Yates with Lcg::new(t_logstd + 1) (zealot-rl/src/ppo.rs:357-363);
     // t_logstd advances once per minibatch, so epoch e starts at t + e*minibatches.
@@ -1105,23 +1212,22 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
   pp.beta2 = 0.999f;
   pp.eps = 1e-8f;
 
-  // The launch sequence depends only on these; everything that changes per
-  // update (scalars, orders, batch contents) lives in device memory.
-  char key[1024];
+  // The launch sequence depends only on these: shapes, strides, layouts, the
+  // configuration and the generation of the handle's buffers. The caller's
+  // pointers reach the graph through p->bptrs, the per-update scalars through
+  // p->dstate.
+  char key[512];
   snprintf(key, sizeof(key),
-           "%d|%lld|%d|%d|%d|%p|%d|%p|%d|%p|%d|%p|%d|%p|%p|%p|%p|%d%d%d|%a|%a|%a|%a|%a|%a|%a|%d|%d|"
-           "%d|%d|%d|%p|%p|%p",
-           mode, pl.n, pl.mb, pl.n_mb, pl.epochs, (const void*)b->obs, b->ld_obs,
-           (const void*)b->critic_obs, b->ld_critic_obs, (const void*)b->action, b->ld_action,
-           (const void*)b->mean_old, b->ld_mean_old, (const void*)b->logp_old,
-           (const void*)b->value_old, (const void*)b->adv, (const void*)b->ret, (int)pl.stage_obs,
-           (int)pl.stage_cobs, (int)pl.shuffle, (double)cfg->clip, (double)cfg->entropy_coef,
-           (double)cfg->value_coef, (double)cfg->max_grad_norm, (double)cfg->desired_kl,
-           (double)cfg->lr_min, (double)cfg->lr_max, cfg->adaptive_lr, cfg->early_stop,
-           cfg->normalize_adv, cfg->clamp_log_std, cfg->shuffle, (void*)p->obs_pad,
-           (void*)p->perm, (void*)p->pws);
+           "%d|%lld|%d|%d|%d|%d|%d|%d|%d|%u|%d|%d|%d|%a|%a|%a|%a|%a|%a|%a|%d|%d|%d|%d|%d|%llu",
+           mode, pl.n, pl.mb, pl.n_mb, pl.epochs, b->ld_obs, b->ld_critic_obs, b->ld_action,
+           b->ld_mean_old, b->feature_major, (int)pl.share_cobs, (int)(b->mean_old != nullptr),
+           (int)pl.shuffle, (double)cfg->clip, (double)cfg->entropy_coef, (double)cfg->value_coef,
+           (double)cfg->max_grad_norm, (double)cfg->desired_kl, (double)cfg->lr_min,
+           (double)cfg->lr_max, cfg->adaptive_lr, cfg->early_stop, cfg->normalize_adv,
+           cfg->clamp_log_std, cfg->shuffle, p->gen);
   const bool eager = c->timing_kernel != -1;
   if (!eager && (!p->gexec || p->gkey != key)) {
+    const auto t0 = std::chrono::steady_clock::now();
     if (p->gexec) {
       hipGraphExecDestroy(p->gexec);
       p->gexec = nullptr;
@@ -1129,7 +1235,7 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
     p->gkey.clear();
     ZL_HIP(c, hipStreamSynchronize(c->stream));
     ZL_HIP(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    s = enqueue_update(p, b, cfg, pl);
+    s = enqueue_update(p, cfg, pl);
     hipGraph_t graph = nullptr;
     hipError_t e = hipStreamEndCapture(c->stream, &graph);
     if (s) {
@@ -1145,9 +1251,15 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
       return fail(c, ZL_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
     }
     p->gkey = key;
+    p->captures += 1;
+    p->capture_ms =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   }
-  // Per-update device scalars: persistent lr / t / gstep, everything else reset.
-  zk::DevState st = p->hstate;
+  // Per-update device scalars: persistent lr / t / gstep, everything else
+  // reset; the caller's batch pointers beside them.
+  UpdateIn in{};
+  zk::DevState& st = in.st;
+  st = p->hstate;
   st.active = 1;
   st.epochs_run = 0;
   st.mb_in_epoch = 0;
@@ -1161,14 +1273,15 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
     st.bc1 = 1.f;
     st.bc2 = 1.f;
   }
-  ZL_HIP(c, hipMemcpyAsync(p->dstate, &st, sizeof(st), hipMemcpyHostToDevice, c->stream));
+  in.ptrs = batch_ptrs(b);
+  ZL_HIP(c, hipMemcpyAsync(p->dstate, &in, sizeof(in), hipMemcpyHostToDevice, c->stream));
   ZL_HIP(c, hipMemcpyAsync(p->ls_old, p->params + p->ls_off, (size_t)p->A * 4,
                            hipMemcpyDeviceToDevice, c->stream));
   if (pl.shuffle)
     ZL_HIP(c, hipMemcpyAsync(p->perm, p->perm_host.data(), p->perm_host.size() * 4,
                              hipMemcpyHostToDevice, c->stream));
   if (eager) {
-    if ((s = enqueue_update(p, b, cfg, pl))) return s;
+    if ((s = enqueue_update(p, cfg, pl))) return s;
   } else {
     ZL_HIP(c, hipGraphLaunch(p->gexec, c->stream));
   }
@@ -1192,6 +1305,13 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
   return ZL_OK;
 }
 
+zl_status zl_ppo_graph_info(zl_ppo* p, long long* captures, double* last_capture_ms) {
+  if (!p) return ZL_ERR_INVALID;
+  if (captures) *captures = p->captures;
+  if (last_capture_ms) *last_capture_ms = p->capture_ms;
+  return ZL_OK;
+}
+
 zl_status zl_ppo_get_grads(zl_ppo* p, float* actor, float* critic, float* log_std) {
   if (!p) return ZL_ERR_INVALID;
   zl_ctx* c = p->c;
@@ -1208,32 +1328,26 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
                                  long long row0, int rows, const int* perm_dev, float* stats) {
   if (!p || !b || !cfg) return ZL_ERR_INVALID;
   zl_ctx* c = p->c;
-  if (!b->obs || !b->critic_obs || !b->action || !b->logp_old || !b->value_old || !b->adv ||
-      !b->ret || rows < 1 || rows > p->mb_cap || row0 < 0 || (!perm_dev && row0 + rows > b->n) ||
-      b->ld_obs < p->actor.dims[0] || b->ld_critic_obs < p->critic.dims[0] ||
-      b->ld_action < p->A || (b->mean_old && b->ld_mean_old < p->A))
-    return fail(c, ZL_ERR_INVALID, "zl_ppo_minibatch_grads: bad argument");
-  // Layer-0 operands need 16-byte aligned rows: stage the rows of this call.
-  const int od = p->actor.dims[0], cd = p->critic.dims[0];
-  const int odp = (int)round_up(od, 4), cdp = (int)round_up(cd, 4);
-  zl_status s = ZL_OK;
-  size_t cap = p->obs_pad_floats * 4;
-  if ((s = grow(c, (void**)&p->obs_pad, &cap, (size_t)rows * odp * 4))) return s;
-  p->obs_pad_floats = cap / 4;
-  cap = p->cobs_pad_floats * 4;
-  if ((s = grow(c, (void**)&p->cobs_pad, &cap, (size_t)rows * cdp * 4))) return s;
-  p->cobs_pad_floats = cap / 4;
-  if ((s = copy_rows(c, p->obs_pad, odp, b->obs, b->ld_obs, od, rows, perm_dev, (int)row0, nullptr,
-                     true)))
+  zl_status s = check_batch(p, b, "zl_ppo_minibatch_grads");
+  if (s) return s;
+  if (rows < 1 || rows > p->mb_cap || row0 < 0 || row0 + rows > b->n)
+    return fail(c, ZL_ERR_INVALID, "zl_ppo_minibatch_grads: rows [%lld, %lld) outside [0, %lld) or "
+                "more than %d", row0, row0 + rows, b->n, p->mb_cap);
+  // The minibatch's samples are staged as rows 0 .. rows-1 (gathered through
+  // perm_dev when given), batch-major and aligned for the layer-0 GEMMs.
+  Plan pl{};
+  if ((s = plan_stage(p, b, rows, perm_dev, row0, &pl.stage, &pl.stage_blocks, &pl.sb,
+                      &pl.share_cobs)))
     return s;
-  if ((s = copy_rows(c, p->cobs_pad, cdp, b->critic_obs, b->ld_critic_obs, cd, rows, perm_dev,
-                     (int)row0, nullptr, true)))
-    return s;
+  const zk::BatchPtrs hp = batch_ptrs(b);
+  ZL_HIP(c, hipMemcpyAsync(p->bptrs, &hp, sizeof(hp), hipMemcpyHostToDevice, c->stream));
+  if ((s = launch(c, K_STAGE, (unsigned)pl.stage_blocks, 1, 1, pl.stage))) return s;
   const int A = p->A;
   if ((s = ensure_partials(p, rows))) return s;
-  const NetView v[2] = {{&p->actor, &p->ab, p->obs_pad, odp}, {&p->critic, &p->cb, p->cobs_pad, cdp}};
+  const NetView v[2] = {{&p->actor, &p->ab, pl.sb.obs, pl.sb.ld_obs},
+                        {&p->critic, &p->cb, pl.sb.critic_obs, pl.sb.ld_critic_obs}};
   PassCounts pc;
-  if ((s = minibatch_pass(p, v, nullptr, perm_dev, (int)row0, rows, b, cfg, 1.0f / (float)rows,
+  if ((s = minibatch_pass(p, v, nullptr, nullptr, 0, rows, &pl.sb, cfg, 1.0f / (float)rows,
                           nullptr, &pc)))
     return s;
   // Fixed-order sums of the per-block partials.
@@ -1334,12 +1448,12 @@ zl_status zl_ppo_act(zl_ppo* p, const float* obs_norm, const float* obs, int ld_
   zl_status s = ZL_OK;
   if (obs_norm) {
     size_t cap = p->obs_pad_floats * 4;
-    if ((s = grow(c, (void**)&p->obs_pad, &cap, (size_t)chunk * odp * 4))) return s;
+    if ((s = grow(p, (void**)&p->obs_pad, &cap, (size_t)chunk * odp * 4))) return s;
     p->obs_pad_floats = cap / 4;
   }
   if (critic_norm) {
     size_t cap = p->cobs_pad_floats * 4;
-    if ((s = grow(c, (void**)&p->cobs_pad, &cap, (size_t)chunk * cdp * 4))) return s;
+    if ((s = grow(p, (void**)&p->cobs_pad, &cap, (size_t)chunk * cdp * 4))) return s;
     p->cobs_pad_floats = cap / 4;
   }
   const int La = p->actor.L, Lc = p->critic.L;

@@ -21,6 +21,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_clamp",         "zk_reduce_all",  "zk_actor_loss_g64", "zk_head",       "zk_norm_set",
     "zk_norm_apply",
     "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
+    "zk_stage",         "zk_sumsq_multi", "zk_clip_scale",  "zk_adam_multi",
 };
 
 // {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
@@ -952,11 +953,14 @@ zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const flo
                             int ld_action, const float* log_std, const float* adv,
                             const float* logp_old, const float* mean_old, int ld_mean_old,
                             int rows, int A, float clip, float entropy_coef, float scale,
-                            float* d_mean, int ld_d_mean, float* d_log_std, float* stats_dev) {
+                            float* d_mean, int ld_d_mean, float* d_log_std, float* stats_dev,
+                            int feature_major) {
   if (!c) return ZL_ERR_INVALID;
+  // Batch-major rows need ld >= A; feature-major component rows need ld >= rows.
+  const int min_ld = feature_major ? rows : A;
   if (!mean || !action || !log_std || !adv || !logp_old || !d_mean || !d_log_std || !stats_dev ||
-      rows < 0 || A < 1 || A > 48 || ld_mean < A || ld_action < A || ld_d_mean < A ||
-      (mean_old && ld_mean_old < A))
+      rows < 0 || A < 1 || A > 48 || ld_mean < min_ld || ld_action < min_ld || ld_d_mean < min_ld ||
+      (mean_old && ld_mean_old < min_ld))
     return fail(c, ZL_ERR_INVALID, "zl_ppo_actor_grad: bad argument (rows=%d A=%d)", rows, A);
   const LossShape sh = actor_loss_shape(rows, A);
   const int nb = sh.blocks;
@@ -973,10 +977,19 @@ zl_status zl_ppo_actor_grad(zl_ctx* c, const float* mean, int ld_mean, const flo
   a.delta = d_mean;
   a.gls_part = c->ws;
   a.stat_part = c->ws + (size_t)nb * A;
-  a.ldm = ld_mean;
-  a.ldact = ld_action;
-  a.ldmo = ld_mean_old;
-  a.ldd = ld_d_mean;
+  if (feature_major) {
+    a.ldm = a.ldact = a.ldmo = a.ldd = 1;
+    a.cm = ld_mean;
+    a.cact = ld_action;
+    a.cmo = ld_mean_old;
+    a.cdd = ld_d_mean;
+  } else {
+    a.ldm = ld_mean;
+    a.ldact = ld_action;
+    a.ldmo = ld_mean_old;
+    a.ldd = ld_d_mean;
+    a.cm = a.cact = a.cmo = a.cdd = 1;
+  }
   a.row0 = 0;
   a.rows = rows;
   a.A = A;
@@ -1060,6 +1073,69 @@ zl_status zl_grad_sqnorm(zl_ctx* c, const float* x, size_t n, float* out_dev) {
   return reduce_partials(c, c->ws, nb, 1, out_dev);
 }
 
+zl_status zl_grad_clip_scale(zl_ctx* c, const zl_tensor* tensors, int count, float max_norm,
+                             float* scale_dev, float* norm_dev) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!tensors || !scale_dev || count < 1 || count > zk::kMaxNormTensors)
+    return fail(c, ZL_ERR_INVALID, "zl_grad_clip_scale: bad argument (count %d)", count);
+  zk::SumsqMultiArgs a{};
+  const int chunk = 2048;
+  int blk = 0;
+  for (int j = 0; j < count; ++j) {
+    if (!tensors[j].ptr && tensors[j].n)
+      return fail(c, ZL_ERR_INVALID, "zl_grad_clip_scale: tensor %d is NULL", j);
+    a.x[j] = tensors[j].ptr;
+    a.n[j] = (long long)tensors[j].n;
+    a.blk0[j] = blk;
+    blk += (int)std::max<long long>(1, cdiv((long long)tensors[j].n, chunk));
+  }
+  a.blk0[count] = blk;
+  a.count = count;
+  a.chunk = chunk;
+  zl_status s = ensure_ws(c, (size_t)blk);
+  if (s) return s;
+  a.part = c->ws;
+  if ((s = launch(c, K_SUMSQ_MULTI, (unsigned)blk, 1, 1, a))) return s;
+  zk::ClipScaleArgs cs{};
+  cs.part = c->ws;
+  cs.nparts = blk;
+  cs.max_norm = max_norm;
+  cs.scale = scale_dev;
+  cs.norm = norm_dev;
+  return launch(c, K_CLIP_SCALE, 1, 1, 1, cs, 0, 64);
+}
+
+zl_status zl_adam_multi(zl_ctx* c, const zl_adam_tensor* tensors, int count, float lr, float beta1,
+                        float beta2, float eps, float bc1, float bc2, const float* clip_scale_dev) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!tensors || count < 1 || count > zk::kMaxAdamTensors)
+    return fail(c, ZL_ERR_INVALID, "zl_adam_multi: bad argument (count %d)", count);
+  zk::AdamMultiArgs a{};
+  int blk = 0;
+  for (int j = 0; j < count; ++j) {
+    const zl_adam_tensor& t = tensors[j];
+    if (t.n && (!t.p || !t.g || !t.m || !t.v))
+      return fail(c, ZL_ERR_INVALID, "zl_adam_multi: tensor %d has a NULL pointer", j);
+    a.t[j].p = t.p;
+    a.t[j].g = t.g;
+    a.t[j].m = t.m;
+    a.t[j].v = t.v;
+    a.t[j].n = (long long)t.n;
+    a.blk0[j] = blk;
+    blk += (int)cdiv((long long)t.n, 4 * kThreads);
+  }
+  a.blk0[count] = blk;
+  a.count = count;
+  a.scale = clip_scale_dev;
+  a.lr = lr;
+  a.bc1 = bc1;
+  a.bc2 = bc2;
+  a.beta1 = beta1;
+  a.beta2 = beta2;
+  a.eps = eps;
+  return launch(c, K_ADAM_MULTI, (unsigned)blk, 1, 1, a);
+}
+
 zl_status zl_gae(zl_ctx* c, const float* rewards, const float* values, const uint8_t* dones,
                  const float* last_values, int T, int N, long long in_ts, long long in_es,
                  long long out_ts, long long out_es, float gamma, float lam, float* adv,
@@ -1088,10 +1164,12 @@ zl_status zl_gae(zl_ctx* c, const float* rewards, const float* values, const uin
 }  // extern "C"
 
 namespace zl {
-// Three-launch deterministic normalisation with caller scratch (2*nparts floats).
+// Three-launch deterministic normalisation with caller scratch (2*nparts
+// floats); the last phase also writes the result to *wb when wb is set.
 zl_status adv_normalize_into(zl_ctx* c, float* adv, long long n, float* scratch, int nparts,
-                             int chunk, const int* guard) {
+                             int chunk, const int* guard, float* const* wb) {
   zk::AdvNormArgs a{};
+  a.wb = wb;
   a.x = adv;
   a.part = scratch;
   a.part2 = scratch + nparts;
@@ -1117,7 +1195,7 @@ zl_status zl_adv_normalize(zl_ctx* c, float* adv, size_t n) {
   const int nparts = (int)cdiv((long long)n, chunk);
   zl_status s = ensure_ws(c, (size_t)2 * nparts);
   if (s) return s;
-  return adv_normalize_into(c, adv, (long long)n, c->ws, nparts, chunk, nullptr);
+  return adv_normalize_into(c, adv, (long long)n, c->ws, nparts, chunk, nullptr, nullptr);
 }
 
 zl_status zl_sample_actions(zl_ctx* c, const float* mean, int ld_mean, const float* log_std,

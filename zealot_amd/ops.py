@@ -5,6 +5,7 @@ from __future__ import annotations
 
 import ctypes as C
 
+from . import _ffi
 from .device import Context, DeviceBuffer
 
 
@@ -32,12 +33,18 @@ def row_sum(ctx: Context, out, x, m, n):
 
 def ppo_actor_grad(ctx: Context, mean, action, log_std, adv, logp_old, mean_old, rows, A, clip,
                    entropy_coef, scale, d_mean, d_log_std, stats, ld_mean=None, ld_action=None,
-                   ld_d_mean=None):
+                   ld_d_mean=None, ld_mean_old=None, feature_major=False):
+    """Vortx Ppo::actor_grad + the dls row sum (src/bin/biped_train_gpu.rs:1257-1271,
+    1350-1357). Batch-major [rows x A] operands by default (row strides ld_*,
+    default A); feature_major: the trainer's [A x rows] tensors (feature
+    strides ld_*, default rows)."""
+    dflt = rows if feature_major else A
     ctx.check(
         ctx.lib.zl_ppo_actor_grad(
-            ctx.h, mean.p, ld_mean or A, action.p, ld_action or A, log_std.p, adv.p, logp_old.p,
-            mean_old.p if mean_old is not None else None, A, rows, A, clip, entropy_coef, scale,
-            d_mean.p, ld_d_mean or A, d_log_std.p, stats.p,
+            ctx.h, mean.p, ld_mean or dflt, action.p, ld_action or dflt, log_std.p, adv.p,
+            logp_old.p, mean_old.p if mean_old is not None else None, ld_mean_old or dflt, rows, A,
+            clip, entropy_coef, scale, d_mean.p, ld_d_mean or dflt, d_log_std.p, stats.p,
+            int(bool(feature_major)),
         ),
         "zl_ppo_actor_grad",
     )
@@ -56,6 +63,29 @@ def adam_step(ctx: Context, p, g, m, v, n, lr, bc1, bc2, beta1=0.9, beta2=0.999,
 
 def grad_sqnorm(ctx: Context, x, n, out):
     ctx.check(ctx.lib.zl_grad_sqnorm(ctx.h, x.p, n, out.p), "zl_grad_sqnorm")
+
+
+def _ptr(x):
+    return x.p if isinstance(x, DeviceBuffer) else x
+
+
+def grad_clip_scale(ctx: Context, tensors, max_norm, scale_out, norm_out=None):
+    """The trainer's global grad-norm clip on the device (src/bin/biped_train_gpu.rs:
+    1368-1452): tensors = [(buffer or pointer, n), ...]; scale_out[0] = the clip
+    scale, norm_out[0] = the global norm."""
+    arr = (_ffi.zl_tensor * len(tensors))(*[_ffi.zl_tensor(_ptr(t), int(n)) for t, n in tensors])
+    ctx.check(ctx.lib.zl_grad_clip_scale(ctx.h, arr, len(tensors), max_norm, _ptr(scale_out),
+                                         _ptr(norm_out) if norm_out is not None else None),
+              "zl_grad_clip_scale")
+
+
+def adam_multi(ctx: Context, tensors, lr, bc1, bc2, clip_scale=None, beta1=0.9, beta2=0.999, eps=1e-8):
+    """Adam over [(p, g, m, v, n), ...] in one launch, gradients times *clip_scale."""
+    arr = (_ffi.zl_adam_tensor * len(tensors))(
+        *[_ffi.zl_adam_tensor(_ptr(p), _ptr(g), _ptr(m), _ptr(v), int(n)) for p, g, m, v, n in tensors])
+    ctx.check(ctx.lib.zl_adam_multi(ctx.h, arr, len(tensors), lr, beta1, beta2, eps, bc1, bc2,
+                                    _ptr(clip_scale) if clip_scale is not None else None),
+              "zl_adam_multi")
 
 
 def gae(ctx: Context, rewards, values, dones, last_values, T, N, adv, ret, gamma=0.99, lam=0.95,

@@ -357,6 +357,12 @@ class GpuActorCritic:
         return PpoStats(st.kl, st.surrogate, st.value_loss, st.entropy, st.lr, st.epochs_run,
                         st.last_kl, tuple(st.grad_norm))
 
+    def graph_info(self):
+        """(captured update graphs so far, host ms of the last capture + instantiation)."""
+        n, ms = C.c_longlong(), C.c_double()
+        self.ctx.check(self.ctx.lib.zl_ppo_graph_info(self.h, C.byref(n), C.byref(ms)), "graph_info")
+        return int(n.value), float(ms.value)
+
     def minibatch_grads(self, batch: "DeviceBatch", cfg: PpoConfig, row0: int, rows: int,
                         perm: DeviceBuffer | None = None):
         """Gradients of one minibatch (no clip / Adam): returns
@@ -414,26 +420,39 @@ class GpuActorCritic:
 
 
 class DeviceBatch:
-    """A rollout batch resident on the device (structure of arrays, batch order)."""
+    """A rollout batch resident on the device (structure of arrays, batch
+    order). Host arrays are [n x dim]; with feature_major=True the matrix
+    fields are stored as the reference trainer stages them, [dim x n]
+    (src/bin/biped_train_gpu.rs:1029-1030,1053-1056), with stride n."""
 
-    def __init__(self, ctx: Context, obs, critic_obs, action, mean_old, logp_old, value_old, adv, ret):
+    def __init__(self, ctx: Context, obs, critic_obs, action, mean_old, logp_old, value_old, adv, ret,
+                 feature_major: bool = False):
         self.ctx = ctx
         self.n = int(np.asarray(obs).shape[0])
-        self.obs = ctx.to_device(obs, np.float32)
-        self.critic_obs = self.obs if critic_obs is obs else ctx.to_device(critic_obs, np.float32)
-        self.action = ctx.to_device(action, np.float32)
-        self.mean_old = ctx.to_device(mean_old, np.float32) if mean_old is not None else None
+        self.feature_major = bool(feature_major)
+
+        def mat(x):
+            x = np.asarray(x, np.float32)
+            return ctx.to_device(np.ascontiguousarray(x.T) if feature_major else x, np.float32)
+
+        self.obs = mat(obs)
+        self.critic_obs = self.obs if critic_obs is obs else mat(critic_obs)
+        self.action = mat(action)
+        self.mean_old = mat(mean_old) if mean_old is not None else None
         self.logp_old = ctx.to_device(logp_old, np.float32)
         self.value_old = ctx.to_device(value_old, np.float32)
         self.adv = ctx.to_device(adv, np.float32)
         self.ret = ctx.to_device(ret, np.float32)
-        self.od = self.obs.shape[1]
-        self.cd = self.critic_obs.shape[1]
-        self.ad = self.action.shape[1]
+        self.od = np.asarray(obs).shape[1]
+        self.cd = np.asarray(critic_obs).shape[1]
+        self.ad = np.asarray(action).shape[1]
 
     def to_c(self) -> _ffi.zl_batch:
+        fm = self.feature_major
+        ld = (lambda d: self.n) if fm else (lambda d: d)
+        bits = (_ffi.ZL_FM_OBS | _ffi.ZL_FM_CRITIC_OBS | _ffi.ZL_FM_ACTION | _ffi.ZL_FM_MEAN_OLD) if fm else 0
         return _ffi.zl_batch(
-            self.n, self.obs.ptr, self.od, self.critic_obs.ptr, self.cd, self.action.ptr, self.ad,
-            self.mean_old.ptr if self.mean_old is not None else None, self.ad,
-            self.logp_old.ptr, self.value_old.ptr, self.adv.ptr, self.ret.ptr,
+            self.n, self.obs.ptr, ld(self.od), self.critic_obs.ptr, ld(self.cd), self.action.ptr,
+            ld(self.ad), self.mean_old.ptr if self.mean_old is not None else None, ld(self.ad),
+            self.logp_old.ptr, self.value_old.ptr, self.adv.ptr, self.ret.ptr, bits,
         )
