@@ -121,6 +121,77 @@ def aux_measurements(ctx, gac, ro, d_obs, ld, n):
     }
 
 
+def gemm_flop_per_row(ad, cd):
+    """Layer-GEMM FLOP per minibatch row of one update step: forward and
+    weight gradient of every layer, data gradient of every layer above the
+    first, both nets."""
+    f = 0
+    for dims in (ad, cd):
+        mac = [dims[l] * dims[l + 1] for l in range(len(dims) - 1)]
+        f += 2 * (2 * sum(mac) + sum(mac[1:]))
+    return f
+
+
+def trainer_nets_measurement(ctx, steps):
+    """The reference trainer's own networks (src/bin/biped_train_gpu.rs:604-610):
+    actor 265-256-256-128-12 on the policy observation, critic 64-512-256-128-1
+    on a separate critic observation, over a 4096 x 24 rollout staged
+    feature-major ([dim x n], as the trainer stages f_obs / f_cobs / f_act),
+    GPU-trainer semantics at the headline settings. Wall time per update
+    (critic values + GAE + update) over `steps` updates."""
+    from zealot_amd import ops, synth
+    from zealot_amd.rl import GpuActorCritic, PpoConfig, _ffi
+
+    ad, cd = [265, 256, 256, 128, 12], [64, 512, 256, 128, 1]
+    N, T = N_ENVS, T_STEPS
+    n, mb = N * T, N * T // MINIBATCHES
+    g = synth.rng(5, 1)
+    obs = synth.obs(g, n, ad[0])
+    cobs = synth.obs(g, n, cd[0])
+    boot = synth.obs(g, N, cd[0])
+    gac = GpuActorCritic(ctx, ad, cd, mb)
+    gac.set_params(synth.kaiming_uniform_net(g, ad), synth.kaiming_uniform_net(g, cd),
+                   np.full(ad[-1], -0.5, np.float32), 1e-3)
+    d_obs, d_cobs, d_boot = ctx.to_device(obs), ctx.to_device(cobs), ctx.to_device(boot)
+    d_mean, d_act, d_logp = ctx.alloc((n, ad[-1])), ctx.alloc((n, ad[-1])), ctx.alloc(n)
+    gac.actor_mean(d_obs, n, d_mean)
+    ops.sample_actions(ctx, d_mean, ctx.to_device(np.full(ad[-1], -0.5, np.float32)),
+                       ctx.to_device(synth.normal(g, (n, ad[-1]))), n, ad[-1], d_act, d_logp)
+    # The trainer's feature-major staging of the same batch.
+    fm_obs, fm_cobs = ctx.to_device(np.ascontiguousarray(obs.T)), ctx.to_device(np.ascontiguousarray(cobs.T))
+    fm_act = ctx.to_device(np.ascontiguousarray(d_act.numpy().T))
+    fm_mean = ctx.to_device(np.ascontiguousarray(d_mean.numpy().T))
+    d_rew = ctx.to_device(synth.normal(g, (T, N)))
+    d_done = ctx.to_device((g.random((T, N)) < 0.02).astype(np.uint8))
+    d_val, d_last, d_adv, d_ret = ctx.alloc(n), ctx.alloc(N), ctx.alloc(n), ctx.alloc(n)
+    fm = _ffi.ZL_FM_OBS | _ffi.ZL_FM_CRITIC_OBS | _ffi.ZL_FM_ACTION | _ffi.ZL_FM_MEAN_OLD
+    batch = _ffi.zl_batch(n, fm_obs.ptr, n, fm_cobs.ptr, n, fm_act.ptr, n, fm_mean.ptr, n, d_logp.ptr,
+                          d_val.ptr, d_adv.ptr, d_ret.ptr, fm)
+    cfg = PpoConfig.gpu_trainer(epochs=EPOCHS, minibatches=MINIBATCHES, clip=0.2, entropy_coef=0.005,
+                                value_coef=1.0, max_grad_norm=1.0, adaptive_lr=False, early_stop=False,
+                                normalize_adv=True, clamp_log_std=True).to_c()
+    stats = _ffi.zl_ppo_stats()
+
+    def step():
+        gac.values(d_cobs, n, d_val)
+        gac.values(d_boot, N, d_last)
+        ops.gae(ctx, d_rew, d_val, d_done, d_last, T, N, d_adv, d_ret, 0.99, 0.95)
+        ctx.check(ctx.lib.zl_ppo_update(gac.h, C.byref(batch), C.byref(cfg), C.byref(stats)), "update")
+
+    t = _timed(ctx, step, steps)
+    flop = gemm_flop_per_row(ad, cd) * n * EPOCHS
+    gac.close()
+    return {
+        "workload": f"trainer nets actor {'-'.join(map(str, ad))} / critic {'-'.join(map(str, cd))} "
+                    f"(separate critic obs), {N} envs x {T} steps, feature-major batch, critic values + "
+                    f"GAE + {EPOCHS} x {MINIBATCHES} minibatches of {mb} rows, global clip 1.0, lr 1e-3",
+        "ms_per_update": t * 1e3,
+        "samples_per_s": EPOCHS * n / t,
+        "update_gemm_tflops": flop / t / 1e12,
+        "fp32_mfma_frac": flop / t / FP32_MFMA_PEAK,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +260,7 @@ def main():
     ctx.synchronize()
     t_step = (time.perf_counter() - t0) / args.steps
 
+    captures, capture_ms = gac.graph_info()
     # Per-kernel HIP-event timing: one instrumented step (eager launches),
     # every launch bracketed by events on the context stream.
     ctx.check(ctx.lib.zl_timing_begin(ctx.h, b"*"), "timing_begin")
@@ -273,7 +345,11 @@ def main():
             "launches_per_step": dom_cnt,
         },
     }
+    out["update_graph"] = {"captures": captures, "capture_instantiate_ms": capture_ms,
+                           "note": "the update graph is captured once per shape / configuration; "
+                                   "new batch buffers are read through a device pointer block"}
     out["aux"] = aux_measurements(ctx, gac, ro, d_obs, LD, n)
+    out["aux"]["trainer_nets_update"] = trainer_nets_measurement(ctx, max(2, min(args.steps, 5)))
     if not args.no_cpu_baseline:
         mean_old = d_mean.numpy()
         action = d_act.numpy()

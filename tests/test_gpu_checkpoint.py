@@ -168,3 +168,27 @@ def test_optimizer_state_roundtrip(ctx):
     assert all(not np.any(x) for x in r.get_moments())
     gac.close()
     r.close()
+
+
+@pytest.mark.parametrize("field,value", [("adam.t", -1), ("adam.t", 2 ** 31), ("adam.gstep", -5)])
+def test_out_of_range_counters_rejected(ctx, field, value):
+    """An image whose Adam counters cannot be a real step count (t outside
+    [0, 2^31 - 1], the i32 exponent of the bias correction; a negative gstep)
+    is refused with ZL_ERR_INVALID before any state of the handle changes."""
+    gac, ad, cd = _stepped_handle(ctx)
+    tensors = dict(safetensors_numpy.load(gac.save_bytes(with_optimizer=True)))
+    tensors[field] = np.array([value], np.int64)
+    bad = safetensors_numpy.save(tensors)
+    r = GpuActorCritic(ctx, ad, cd, 256)
+    before = r.get_params(), r.get_moments(), r.counters()
+    with pytest.raises(ZealotError) as ei:
+        r.load_into(bad, restore_optimizer=True)
+    assert ei.value.status == 1
+    after = r.get_params(), r.get_moments(), r.counters()
+    for x, y in zip(before[0][:3], after[0][:3]):
+        assert np.array_equal(x, y)
+    for x, y in zip(before[1], after[1]):
+        assert np.array_equal(x, y)
+    assert before[2] == after[2]
+    gac.close()
+    r.close()

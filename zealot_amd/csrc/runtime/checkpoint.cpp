@@ -11,6 +11,7 @@
 // serializer uses, so a reference-layout checkpoint is byte-identical to the
 // one the reference writes for the same values.
 #include <cstdio>
+#include <climits>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -426,6 +427,7 @@ zl_status load_image(zl_ppo* p, float* obs_norm, float* critic_norm, int restore
   // Optional optimizer state: all of it or none.
   bool have_opt = restore_opt && m.count("adam.t") && m.count("adam.gstep");
   std::vector<float> ma, va, mc, vc, mls, vls;
+  long long opt_t = 0, opt_gstep = 0;
   if (have_opt) {
     std::vector<int> d;
     std::vector<const Entry*> w[4], b[4];
@@ -443,18 +445,22 @@ zl_status load_image(zl_ppo* p, float* obs_norm, float* critic_norm, int restore
     const Entry& eg = m.at("adam.gstep");
     if (et.dt != DT_I64 || et.nbytes != 8 || eg.dt != DT_I64 || eg.nbytes != 8)
       return fail(c, ZL_ERR_INVALID, "checkpoint: adam counters are not I64 [1]");
+    std::memcpy(&opt_t, et.data, 8);
+    std::memcpy(&opt_gstep, eg.data, 8);
+    // The step count feeds powi(beta, t) (an i32 exponent) and gstep the
+    // trainer's bias correction: out-of-range values are a corrupt image.
+    if (opt_t < 0 || opt_t > INT_MAX || opt_gstep < 0)
+      return fail(c, ZL_ERR_INVALID, "checkpoint: adam counters out of range (t %lld, gstep %lld)",
+                  opt_t, opt_gstep);
   }
   std::vector<float> actor((size_t)packed_count(ad)), critic((size_t)packed_count(cd));
   get_net(aw, ab, actor.data());
   get_net(cw, cb, critic.data());
   if ((s = zl_ppo_set_params(p, actor.data(), critic.data(), ls.data(), lr[0]))) return s;
   if (have_opt) {
-    long long t = 0, g = 0;
-    std::memcpy(&t, m.at("adam.t").data, 8);
-    std::memcpy(&g, m.at("adam.gstep").data, 8);
     if ((s = ppo_set_moments(p, ma.data(), va.data(), mc.data(), vc.data(), mls.data(), vls.data())))
       return s;
-    ppo_set_counters(p, (int)t, (unsigned long long)g);
+    ppo_set_counters(p, (int)opt_t, (unsigned long long)opt_gstep);
   } else if ((s = zl_ppo_reset_optimizer(p))) {  // ppo.rs:625-636: fresh Adam state
     return s;
   }
