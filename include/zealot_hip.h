@@ -174,6 +174,18 @@ typedef struct zl_tensor {
 zl_status zl_grad_clip_scale(zl_ctx* ctx, const zl_tensor* tensors, int count, float max_norm,
                              float* scale_dev, float* norm_dev);
 
+/* zl_grad_clip_scale without any allocation: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, serving or training loops that forbid hipMalloc). Same results,
+ * bit for bit, as zl_grad_clip_scale. Its partial sums live in one static
+ * device array per GPU of 16,384 floats (64 KiB, held until the process
+ * ends): one partial per 2,048 elements of each tensor (at least one per
+ * tensor), so about 33.5 M gradient elements per call at most; larger inputs
+ * are refused with ZL_ERR_INVALID. Calls on one GPU share that array: calls
+ * that overlap in time on one GPU (other streams or contexts) race. */
+zl_status zl_grad_clip_scale_noalloc(zl_ctx* ctx, const zl_tensor* tensors, int count,
+                                     float max_norm, float* scale_dev, float* norm_dev);
+
 /* One Adam parameter tensor with its gradient and moments (device, n floats each). */
 typedef struct zl_adam_tensor {
   float* p;

@@ -149,6 +149,7 @@ SIGNATURES = {
     ),
     "zl_grad_sqnorm": (C.c_int, [vp, vp, C.c_size_t, vp]),
     "zl_grad_clip_scale": (C.c_int, [vp, C.POINTER(zl_tensor), C.c_int, C.c_float, vp, vp]),
+    "zl_grad_clip_scale_noalloc": (C.c_int, [vp, C.POINTER(zl_tensor), C.c_int, C.c_float, vp, vp]),
     "zl_adam_multi": (
         C.c_int,
         [vp, C.POINTER(zl_adam_tensor), C.c_int, C.c_float, C.c_float, C.c_float, C.c_float,

@@ -149,6 +149,10 @@ struct zl_ctx {
   // off) and the block count their row slices aim at (ZL_NARROW_TARGET).
   bool narrow = true;
   int narrow_target = 256;
+  // Device address of the allocation-free scratch array on this context's
+  // device (zl_grad_clip_scale_noalloc), set at zl_init.
+  float* noalloc_scratch = nullptr;
+  hipError_t noalloc_err = hipSuccess;
 };
 
 namespace zl {
@@ -239,6 +243,10 @@ zl_status ensure_ws(zl_ctx* c, size_t floats);
 zl_status reduce_rows(zl_ctx* c, const float* part, int width, int blocks, float* out);
 // Sampling + logp (zk_sample_g32 / _g64 for A <= 32 / 64, else zk_sample).
 zl_status launch_sample(zl_ctx* c, const zk::SampleArgs& a);
+
+// Looks up the allocation-free scratch array's address on the context's
+// device (defined in noalloc.hip; the device must be current).
+void noalloc_setup(zl_ctx* c);
 
 // zl_ppo internals for the checkpoint code (defined in mlp_ppo.cpp).
 zl_ctx* ppo_ctx(zl_ppo* p);

@@ -720,6 +720,7 @@ zl_status zl_init(int device, zl_ctx** out) {
     delete c;
     return ZL_ERR_HIP;
   }
+  noalloc_setup(c);
   double worst = 0.0;
   zl_status s = self_test(c, &worst);
   if (s) {
