@@ -16,7 +16,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "libzl_oracle.so")
+# ZL_ORACLE_LIBRARY selects another build (e.g. the sanitizer build, oracle/_asan/).
+LIB = os.environ.get("ZL_ORACLE_LIBRARY") or os.path.join(HERE, "libzl_oracle.so")
 
 vp = C.c_void_p
 fl = C.c_float

@@ -93,3 +93,28 @@ def test_malformed_images_rejected(case):
         img = _image(hdr, data + b"\0" * 40)
     with pytest.raises(ZealotError):
         checkpoint_dims(img)
+
+
+def test_mutated_images_never_crash():
+    """Seeded byte mutations of a valid image (header and data): every one
+    parses to dims or comes back as an error status, never a crash or an
+    out-of-bounds read (run under AddressSanitizer by tests/sanitize.sh)."""
+    ad, cd = [7, 16, 8, 3], [5, 16, 1]
+    good = safetensors_numpy.save(reference_tensors(ad, cd))
+    g = np.random.default_rng(2024)
+    hlen = struct.unpack("<Q", good[:8])[0]
+    ok = bad = 0
+    for i in range(400):
+        b = bytearray(good)
+        for _ in range(int(g.integers(1, 4))):
+            # Mostly inside the 8-byte length and the JSON header.
+            pos = int(g.integers(0, 8 + hlen)) if g.random() < 0.9 else int(g.integers(0, len(b)))
+            b[pos] = int(g.integers(0, 256))
+        if i % 50 == 0:
+            b = b[: int(g.integers(0, len(b)))]  # truncations
+        try:
+            checkpoint_dims(bytes(b))
+            ok += 1
+        except ZealotError:
+            bad += 1
+    assert ok + bad == 400 and bad > 100

@@ -11,7 +11,9 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(_HERE, "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libzealot_hip.so")
+# ZL_LIBRARY selects another build of the library (e.g. the sanitizer build
+# of the host runtime, zealot_amd/lib/asan/libzealot_hip.so).
+LIB_PATH = os.environ.get("ZL_LIBRARY") or os.path.join(LIB_DIR, "libzealot_hip.so")
 CODE_OBJECT_PATH = os.path.join(LIB_DIR, "zealot_kernels.hsaco")
 
 ZL_OK = 0
@@ -223,7 +225,7 @@ def load_library() -> C.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()')"
         )
-    if not os.path.exists(CODE_OBJECT_PATH):
+    if not os.environ.get("ZL_LIBRARY") and not os.path.exists(CODE_OBJECT_PATH):
         raise RuntimeError(f"{CODE_OBJECT_PATH} (gfx950 code object) is missing: build it first")
     lib = C.CDLL(LIB_PATH)
     for name, (res, args) in SIGNATURES.items():

@@ -20,6 +20,24 @@
 
 using namespace zl;
 
+// A tensor name from an image, fit for an error message: bytes outside
+// printable ASCII escaped as \xHH, at most 64 characters kept.
+static std::string printable(const std::string& raw) {
+  std::string out;
+  for (size_t i = 0; i < raw.size() && out.size() < 64; ++i) {
+    const unsigned char ch = (unsigned char)raw[i];
+    if (ch >= 0x20 && ch < 0x7f) {
+      out += (char)ch;
+    } else {
+      char b[5];
+      snprintf(b, sizeof(b), "\\x%02x", ch);
+      out += b;
+    }
+  }
+  if (out.size() >= 64) out += "...";
+  return out;
+}
+
 namespace {
 
 enum Dt { DT_F32 = 0, DT_I64 = 1 };
@@ -238,7 +256,7 @@ zl_status parse(zl_ctx* c, const unsigned char* buf, size_t size, std::map<std::
     const Json* of = t.get("data_offsets");
     if (t.kind != Json::OBJ || !dt || dt->kind != Json::STR || !sh || sh->kind != Json::ARR || !of ||
         of->kind != Json::ARR || of->arr.size() != 2 || of->arr[0].num < 0 || of->arr[1].num < 0)
-      return fail(c, ZL_ERR_INVALID, "checkpoint: malformed entry '%s'", kv.first.c_str());
+      return fail(c, ZL_ERR_INVALID, "checkpoint: malformed entry '%s'", printable(kv.first).c_str());
     size_t esize = 0;
     Entry en{};
     if (dt->str == "F32") {
@@ -254,14 +272,14 @@ zl_status parse(zl_ctx* c, const unsigned char* buf, size_t size, std::map<std::
     long long count = 1;
     for (const Json& d : sh->arr) {
       if (d.num < 0 || (d.num > 0 && count > (1LL << 40) / d.num))
-        return fail(c, ZL_ERR_INVALID, "checkpoint: bad shape of '%s'", kv.first.c_str());
+        return fail(c, ZL_ERR_INVALID, "checkpoint: bad shape of '%s'", printable(kv.first).c_str());
       en.shape.push_back(d.num);
       count *= d.num;
     }
     const size_t b = (size_t)of->arr[0].num, e = (size_t)of->arr[1].num;
     if (b > e || e > dsize || (esize && (e - b) != (size_t)count * esize))
       return fail(c, ZL_ERR_INVALID, "checkpoint: data offsets of '%s' do not match its shape",
-                  kv.first.c_str());
+                  printable(kv.first).c_str());
     ranges.emplace_back(b, e);
     if (esize) {
       en.data = data + b;

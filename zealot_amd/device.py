@@ -77,13 +77,13 @@ class Context:
         h = C.c_void_p()
         st = self.lib.zl_init(device, C.byref(h))
         if st != _ffi.ZL_OK:
-            raise ZealotError(st, self.lib.zl_global_error().decode())
+            raise ZealotError(st, self.lib.zl_global_error().decode(errors="replace"))
         self.h = h
         self.self_test_error = float(self.lib.zl_self_test_error(h))
 
     def check(self, status: int, what: str = ""):
         if status != _ffi.ZL_OK:
-            raise ZealotError(status, f"{what}: {self.lib.zl_last_error(self.h).decode()}")
+            raise ZealotError(status, f"{what}: {self.lib.zl_last_error(self.h).decode(errors='replace')}")
 
     def alloc(self, shape, dtype=np.float32) -> DeviceBuffer:
         shape = (shape,) if isinstance(shape, int) else tuple(shape)

@@ -251,7 +251,7 @@ def checkpoint_dims(data: bytes):
     na, nc = C.c_int(), C.c_int()
     st = lib.zl_checkpoint_dims(data, len(data), ad, C.byref(na), cd, C.byref(nc), cap)
     if st != _ffi.ZL_OK:
-        raise ZealotError(st, "zl_checkpoint_dims: " + lib.zl_global_error().decode())
+        raise ZealotError(st, "zl_checkpoint_dims: " + lib.zl_global_error().decode(errors="replace"))
     return list(ad[:na.value]), list(cd[:nc.value])
 
 
