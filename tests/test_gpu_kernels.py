@@ -104,6 +104,32 @@ def test_gemm_large_ragged(ctx, case):
     assert err <= FWD_BWD_TOL, (case, err)
 
 
+# Shapes whose tiles and k-tiles are all full, which run the exact-fit
+# kernels (no clamps or masks): the 96 x 128 forward tile, and split-K
+# weight gradients on 128 x 128 and 64 x 128 tiles.
+EXACT_CASES = [
+    (6144, 512, 128, False, True),
+    (256, 512, 6144, True, False),
+    (128, 256, 6144, True, False),
+]
+
+
+@pytest.mark.parametrize("case", EXACT_CASES)
+def test_gemm_exact_fit(ctx, case):
+    m, n, k, lt, rt = case
+    g = np.random.default_rng(m + 7 * n + 11 * k)
+    L = g.standard_normal((m, k)).astype(np.float32)
+    R = g.standard_normal((k, n)).astype(np.float32)
+    ref = L.astype(np.float64) @ R.astype(np.float64)
+    dl = ctx.to_device(L.T.copy() if lt else L)
+    dr = ctx.to_device(R.T.copy() if rt else R)
+    out = ctx.alloc((m, n))
+    ops.gemm(ctx, out, dl, lt, dr, rt, m, n, k)
+    err = rel_amax(out.numpy(), ref)
+    print(f"[gpu] exact-fit gemm {case}: rel err {err:.2e}", flush=True)
+    assert err <= FWD_BWD_TOL, (case, err)
+
+
 # Shapes routed to the register-resident narrow kernels (one dimension <= 32):
 # (m, n, k, lhs_t, rhs_t) and the family each exercises.
 NARROW_CASES = [
@@ -228,9 +254,12 @@ def _mlp_case(ctx, dims, rows, seed, bias_bound=0.1):
     return g, params, x, dx, mlp
 
 
+# ([128, 512, 256, 128, 8], 6144): every 96 x 128 forward / data-gradient
+# tile and every weight-gradient tile and k-tile full (the exact-fit kernels).
 @pytest.mark.parametrize("dims,rows", [([4, 6, 5, 3], 7), ([123, 512, 256, 128, 29], 4096),
                                        ([123, 512, 256, 128, 1], 1000), ([17, 33, 2], 300),
-                                       ([123, 512, 256, 128, 29], 13001)])
+                                       ([123, 512, 256, 128, 29], 13001),
+                                       ([128, 512, 256, 128, 8], 6144)])
 def test_mlp_forward_vs_oracle(ctx, dims, rows):
     g, params, x, dx, mlp = _mlp_case(ctx, dims, rows, seed=rows)
     got = mlp.output(rows)
@@ -242,7 +271,8 @@ def test_mlp_forward_vs_oracle(ctx, dims, rows):
 
 @pytest.mark.parametrize("dims,rows", [([4, 6, 5, 3], 7), ([123, 512, 256, 128, 29], 4096),
                                        ([123, 512, 256, 128, 1], 2048), ([17, 33, 2], 300),
-                                       ([123, 512, 256, 128, 29], 13001)])
+                                       ([123, 512, 256, 128, 29], 13001),
+                                       ([128, 512, 256, 128, 8], 6144)])
 def test_mlp_backward_vs_oracle(ctx, dims, rows):
     g, params, x, dx, mlp = _mlp_case(ctx, dims, rows, seed=rows + 1)
     gout = (g.standard_normal((rows, dims[-1])) / rows).astype(np.float32)

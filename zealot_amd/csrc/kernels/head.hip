@@ -95,6 +95,7 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   const float inv_sd = expf(-ls);
   const float lo = 1.0f - p.clip, hi = 1.0f + p.clip;
   float gacc = 0.f, sacc = 0.f, kacc = 0.f;
+  float klacc = 0.f;  // sum of (mean - mean_old)^2 of component k over the group's rows
   float dbias = 0.f;  // thread t < 32: bias gradient of component t
   floatx4 wacc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
   // Wave-to-tile mapping: 16-row tile rt = wave % 4; forward components
@@ -186,6 +187,10 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
         if (p.mean_old) {
           const float y = (mu - in[j].mo) * inv_sd;
           kacc += row_sum_ordered(srow, k, on ? 0.5f * (y * y) : 0.f) * p.scale;
+          if (p.kl_part && on) {
+            const float dmu = mu - in[j].mo;
+            klacc += dmu * dmu;
+          }
         }
         srow[k] = on ? gm : 0.f;  // the group's own row: no other reader yet
       }
@@ -272,6 +277,16 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     float v = 0.f;
     for (int j = 0; j < kHeadGroups; ++j) v += sred[j * 34 + 32 + qq];
     p.astat_part[(long long)qq * nblk + blk] = v;
+  }
+  if (p.kl_part) {  // per-component sums for the trainer's full-Gaussian KL
+    lds_barrier();
+    sred[grp * 34 + k] = klacc;
+    lds_barrier();
+    if (t < A) {
+      float v = 0.f;
+      for (int j = 0; j < kHeadGroups; ++j) v += sred[j * 34 + t];
+      p.kl_part[(long long)t * nblk + blk] = v;
+    }
   }
 }
 

@@ -389,22 +389,28 @@ __device__ void adam_body(const AdamArgs& p) {
 
 // --------------------------------------------------------------- epoch logic
 
-__device__ void epoch_begin_body(const EpochBeginArgs& p) {
-  if (p.guard && *p.guard == 0) return;
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  DevState* st = p.st;
-  if (p.pp.mode == 1) {  // biped_train_gpu.rs:1165-1167
-    st->gstep += (unsigned long long)p.pp.n_mb;
+// Opening of an epoch (zk_epoch_begin, or the tail of zk_epoch_end for the
+// next one): the trainer's gstep advance and bias corrections, and cleared
+// epoch sums.
+__device__ __forceinline__ void open_epoch(DevState* st, const PpoParams& pp) {
+  if (pp.mode == 1) {  // biped_train_gpu.rs:1165-1167
+    st->gstep += (unsigned long long)pp.n_mb;
     const unsigned long long cap = 1ull << 30;
     const int tt = (int)(st->gstep < cap ? st->gstep : cap);
-    st->bc1 = 1.0f - powi_f32(p.pp.beta1, tt);
-    st->bc2 = 1.0f - powi_f32(p.pp.beta2, tt);
+    st->bc1 = 1.0f - powi_f32(pp.beta1, tt);
+    st->bc2 = 1.0f - powi_f32(pp.beta2, tt);
   }
   st->ep_kl = 0.f;
   st->ep_surr = 0.f;
   st->ep_vloss = 0.f;
   st->ep_ent = 0.f;
   st->mb_in_epoch = 0;
+}
+
+__device__ void epoch_begin_body(const EpochBeginArgs& p) {
+  if (p.guard && *p.guard == 0) return;
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  open_epoch(p.st, p.pp);
 }
 
 // Full-Gaussian KL(old || new) of src/bin/biped_train_gpu.rs:1478-1491, one
@@ -428,21 +434,64 @@ __device__ void kl_body(const KlArgs& p) {
   if (threadIdx.x == 0) p.part[blockIdx.x] = tot;
 }
 
+// End of an epoch (one block of kFinalizeThreads): epoch statistics, and in
+// trainer mode the full-Gaussian KL of the last minibatch
+// (biped_train_gpu.rs:1478-1491), the adaptive learning rate and the early
+// stop. From zk_head's per-component sums S_k = sum_r (mu_rk - mu_old_rk)^2
+// (kl_form 1) the mean over the R rows of
+//   sum_k log(sig_new/sig_old) + (sig_old^2 + dmu^2) / (2 sig_new^2) - 1/2
+// is sum_k c_k + S_k / (2 R sig_new_k^2) with
+//   c_k = d - 1/2 + exp(-2 d) / 2 = (expm1(-2 d) + 2 d) / 2,  d = ls_new - ls_old,
+// the same quantity with the per-row constant computed once (and without
+// cancellation) per component.
 __device__ void epoch_end_body(const EpochEndArgs& p) {
+  constexpr int kMaxA = 256;
+  __shared__ float sk[kMaxA];
   if (*p.active == 0) return;
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  DevState* st = p.st;
+  const int t = threadIdx.x;
   const PpoParams& pp = p.pp;
+  const bool kl_on = pp.mode == 1 && p.kl_part != nullptr;
+  if (kl_on && p.kl_form == 1) {
+    const int grp = t >> 5, gln = t & 31;
+    for (int k = grp; k < pp.A; k += kFinalizeThreads / 32) {
+      const float* ptr = p.kl_part + (long long)k * p.nkl;
+      float v = 0.f;
+      for (int i0 = gln; i0 < p.nkl; i0 += 8 * 32) {
+        float tv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) tv[u] = i0 + 32 * u < p.nkl ? ptr[i0 + 32 * u] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (i0 + 32 * u < p.nkl) v += tv[u];
+      }
+#pragma unroll
+      for (int m = 16; m > 0; m >>= 1) v = v + __shfl_xor(v, m, 32);
+      if (gln == 0) sk[k] = v;
+    }
+    __syncthreads();
+  }
+  if (t != 0) return;
+  DevState* st = p.st;
   const float inv = 1.0f / (float)pp.n_mb;  // ppo.rs:374-381
   st->stats[0] = st->ep_kl * inv;
   st->stats[1] = st->ep_surr * inv;
   st->stats[2] = st->ep_vloss * inv;
   st->stats[3] = st->ep_ent * inv;
   st->epochs_run += 1;
-  if (pp.mode == 1 && p.kl_part) {
+  if (kl_on) {
     float kl = 0.f;
-    for (int b = 0; b < p.nkl; ++b) kl += p.kl_part[b];
-    kl /= (float)pp.mb;
+    if (p.kl_form == 1) {
+      const float R = (float)pp.mb;
+      for (int k = 0; k < pp.A; ++k) {
+        const float ls_new = p.log_std[k];
+        const float d = ls_new - p.log_std_old[k];
+        const float ck = 0.5f * (expm1f(-2.0f * d) + 2.0f * d);
+        kl += ck + 0.5f * (sk[k] / R) * expf(-2.0f * ls_new);
+      }
+    } else {
+      for (int b = 0; b < p.nkl; ++b) kl += p.kl_part[b];
+      kl /= (float)pp.mb;
+    }
     st->last_kl = kl;
     if (pp.adaptive_lr) {  // biped_train_gpu.rs:1497-1501
       if (kl > pp.desired_kl * 2.0f)
@@ -453,6 +502,7 @@ __device__ void epoch_end_body(const EpochEndArgs& p) {
     if (pp.early_stop && kl > pp.desired_kl * 5.0f) *p.active = 0;  // :1513-1515
   }
   st->stats[4] = st->lr;
+  if (p.begin_next && *p.active) open_epoch(st, pp);
 }
 
 // --------------------------------------------------------- GAE / advantages
@@ -819,7 +869,9 @@ extern "C" __global__ __launch_bounds__(zk::kFinalizeThreads) void zk_finalize(z
 ZK_KERNEL(zk_adam, AdamArgs, adam_body)
 ZK_KERNEL(zk_epoch_begin, EpochBeginArgs, epoch_begin_body)
 ZK_KERNEL(zk_kl, KlArgs, kl_body)
-ZK_KERNEL(zk_epoch_end, EpochEndArgs, epoch_end_body)
+extern "C" __global__ __launch_bounds__(zk::kFinalizeThreads) void zk_epoch_end(zk::EpochEndArgs p) {
+  zk::epoch_end_body(p);
+}
 ZK_KERNEL(zk_gae, GaeArgs, gae_body)
 ZK_KERNEL(zk_adv_norm, AdvNormArgs, adv_norm_body)
 ZK_KERNEL(zk_elu_backward, EluBwdArgs, elu_backward_body)

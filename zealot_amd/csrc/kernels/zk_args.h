@@ -82,14 +82,6 @@ struct ReduceSeg {
   int blk0, nqb, nrb;
 };
 
-constexpr int kMaxReduceSegs = 16;
-struct ReduceAllArgs {
-  ReduceSeg seg[kMaxReduceSegs];
-  int nseg;
-  float* sq_part;  // per-block sum of squares of the block's final values
-  const int* guard;
-};
-
 // Scalars that live on the device for a whole update so that no kernel needs
 // a host round trip (learning rate, Adam step, clip scales, statistics).
 struct DevState {
@@ -119,6 +111,27 @@ struct PpoParams {
   int adaptive_lr, early_stop;
   int clamp_ls;  // clamp log_std to [-1.6, 1.0] in every Adam step
   float beta1, beta2, eps;
+};
+
+struct FinalizeArgs {
+  DevState* st;
+  const float* gls_part;    // [A x nb_a]
+  const float* astat_part;  // [2 x nb_a]
+  const float* vstat_part;  // [nb_v]
+  const float* sq_part;     // [nsq]
+  const float* log_std;     // [A] (pre-step values)
+  float* g_logstd;          // [A] log_std gradient slot in the flat gradient
+  const int* guard;
+  PpoParams pp;
+  int nb_a, nb_v, nsq, nsq_a;
+};
+
+constexpr int kMaxReduceSegs = 16;
+struct ReduceAllArgs {
+  ReduceSeg seg[kMaxReduceSegs];
+  int nseg;
+  float* sq_part;  // per-block sum of squares of the block's final values
+  const int* guard;
 };
 
 struct ActorLossArgs {
@@ -188,6 +201,7 @@ struct HeadArgs {
   float* gls_part;        // [A x blocks] log_std gradient partials
   float* astat_part;      // [2 x blocks] surrogate, kl partials
   float* vstat_part;      // [blocks] value-loss partials
+  float* kl_part;         // [A x blocks] sums of (mean - mean_old)^2 per component, nullable
   const int* guard;
   long long rows;
   int row0, A, ldact, ldmo, tiles_per_block;
@@ -202,19 +216,6 @@ struct SumsqArgs {
   long long off1, len1;  // group 1 range
   int blocks0;           // blocks assigned to group 0; the rest cover group 1
   int chunk;             // elements per block
-};
-
-struct FinalizeArgs {
-  DevState* st;
-  const float* gls_part;    // [A x nb_a]
-  const float* astat_part;  // [2 x nb_a]
-  const float* vstat_part;  // [nb_v]
-  const float* sq_part;     // [nsq]
-  const float* log_std;     // [A] (pre-step values)
-  float* g_logstd;          // [A] log_std gradient slot in the flat gradient
-  const int* guard;
-  PpoParams pp;
-  int nb_a, nb_v, nsq, nsq_a;
 };
 
 struct AdamArgs {
@@ -247,12 +248,19 @@ struct KlArgs {
   int ldm, ldmo, row0, rows, A;
 };
 
+// kl_form 0: kl_part holds the per-block KL totals of zk_kl. kl_form 1: it
+// holds zk_head's [A x nkl] per-component sums of (mean - mean_old)^2 over
+// the last minibatch, combined with log_std / log_std_old here.
 struct EpochEndArgs {
   DevState* st;
-  const float* kl_part;  // [nkl] (trainer mode), nullable
-  int* active;           // early-stop flag (the guard of every later kernel)
+  const float* kl_part;      // trainer mode, nullable
+  const float* log_std;      // [A] current (kl_form 1)
+  const float* log_std_old;  // [A] rollout snapshot (kl_form 1)
+  int* active;               // early-stop flag (the guard of every later kernel)
   PpoParams pp;
   int nkl;
+  int kl_form;
+  int begin_next;            // also open the next epoch (zk_epoch_begin) if still active
 };
 
 struct GaeArgs {

@@ -644,10 +644,12 @@ struct PassCounts {
 // One minibatch: forward of both nets, the PPO losses, backward, and the
 // all-layer reduction with the grad-norm partials (the accumulation of
 // zealot-rl/src/ppo.rs:406-462 before clip / Adam). `px` gathers the
-// layer-0 rows; samples of the batch are perm[row0 + r] (or row0 + r).
+// layer-0 rows; samples of the batch are perm[row0 + r] (or row0 + r). With
+// `head_kl`, zk_head also writes the per-component KL sums of this minibatch
+// there.
 zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int* perm, int row0,
                          int rows, const zl_batch* b, const zl_ppo_config* cfg, float scale,
-                         const int* guard, PassCounts* pc) {
+                         const int* guard, PassCounts* pc, float* head_kl = nullptr) {
   zl_ctx* c = p->c;
   const int La = p->actor.L, Lc = p->critic.L, A = p->A;
   zl_status s = pair_forward(c, v, p->params, px, rows, guard, p->fused_head ? La - 1 : -1);
@@ -697,6 +699,7 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     h.gls_part = p->gls_part;
     h.astat_part = p->astat_part;
     h.vstat_part = p->vstat_part;
+    h.kl_part = head_kl;
     h.guard = guard;
     if ((s = launch(c, K_HEAD, (unsigned)head_blocks, 1, 2, h, 0, zk::kHeadThreads))) return s;
     pc->nb_a = pc->nb_v = head_blocks;
@@ -899,22 +902,31 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
   const int La = p->actor.L;
   const int nb = (int)cdiv(pl.mb, kThreads);
   const float* log_std = p->params + p->ls_off;
+  const bool trainer_kl = pl.mode == ZL_SEMANTICS_GPU_TRAINER && b->mean_old != nullptr;
+  // The per-epoch KL of the last minibatch comes from zk_head's per-component
+  // sums when the output layers are fused, else from zk_kl.
+  const bool head_kl = trainer_kl && p->fused_head;
   for (int e = 0; e < pl.epochs; ++e) {
-    zk::EpochBeginArgs eb{};
-    eb.st = p->dstate;
-    eb.guard = guard;
-    eb.pp = pl.pp;
-    if ((s = launch(c, K_EPOCH_BEGIN, 1, 1, 1, eb))) return s;
+    if (e == 0) {  // later epochs are opened by the previous zk_epoch_end
+      zk::EpochBeginArgs eb{};
+      eb.st = p->dstate;
+      eb.guard = guard;
+      eb.pp = pl.pp;
+      if ((s = launch(c, K_EPOCH_BEGIN, 1, 1, 1, eb))) return s;
+    }
     const int* perm_e = pl.shuffle ? p->perm + (size_t)e * pl.n : nullptr;
+    int nb_kl = nb;
     for (int k = 0; k < pl.n_mb; ++k) {
       const int row0 = k * pl.mb;
       const int* px = perm_e ? perm_e + row0 : nullptr;
       const float* xa = perm_e ? pl.X : pl.X + (size_t)row0 * pl.ldx;
       const float* xc = perm_e ? pl.XC : pl.XC + (size_t)row0 * pl.ldxc;
       const NetView v[2] = {{&p->actor, &p->ab, xa, pl.ldx}, {&p->critic, &p->cb, xc, pl.ldxc}};
+      float* hkl = head_kl && k == pl.n_mb - 1 ? p->kl_part : nullptr;
       PassCounts pc;
-      if ((s = minibatch_pass(p, v, px, perm_e, row0, pl.mb, b, cfg, pl.pp.scale, guard, &pc))) return s;
-      const int nsq = pc.nsq, nsq_a = pc.nsq_a;
+      if ((s = minibatch_pass(p, v, px, perm_e, row0, pl.mb, b, cfg, pl.pp.scale, guard, &pc, hkl)))
+        return s;
+      if (hkl) nb_kl = pc.nb_a;
       zk::FinalizeArgs fz{};
       fz.st = p->dstate;
       fz.gls_part = p->gls_part;
@@ -927,8 +939,8 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
       fz.pp = pl.pp;
       fz.nb_a = pc.nb_a;
       fz.nb_v = pc.nb_v;
-      fz.nsq = nsq;
-      fz.nsq_a = nsq_a;
+      fz.nsq = pc.nsq;
+      fz.nsq_a = pc.nsq_a;
       if ((s = launch(c, K_FINALIZE, 1, 1, 1, fz, 0, zk::kFinalizeThreads))) return s;
       zk::AdamArgs ad{};
       ad.p = p->params;
@@ -946,8 +958,7 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
       ad.clamp_ls = pl.pp.clamp_ls;
       if ((s = launch(c, K_ADAM, (unsigned)cdiv(p->nflat, 4 * kThreads), 1, 1, ad))) return s;
     }
-    const bool trainer_kl = pl.mode == ZL_SEMANTICS_GPU_TRAINER && b->mean_old != nullptr;
-    if (trainer_kl) {  // src/bin/biped_train_gpu.rs:1469-1492 (last minibatch)
+    if (trainer_kl && !head_kl) {  // src/bin/biped_train_gpu.rs:1469-1492 (last minibatch)
       zk::KlArgs kl{};
       kl.mean = p->ab.act[La];
       kl.ldm = p->ab.ld[La];
@@ -966,10 +977,14 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
     zk::EpochEndArgs ee{};
     ee.st = p->dstate;
     ee.kl_part = trainer_kl ? p->kl_part : nullptr;
+    ee.log_std = log_std;
+    ee.log_std_old = p->ls_old;
     ee.active = &p->dstate->active;
     ee.pp = pl.pp;
-    ee.nkl = nb;
-    if ((s = launch(c, K_EPOCH_END, 1, 1, 1, ee))) return s;
+    ee.nkl = nb_kl;
+    ee.kl_form = head_kl ? 1 : 0;
+    ee.begin_next = e + 1 < pl.epochs ? 1 : 0;
+    if ((s = launch(c, K_EPOCH_END, 1, 1, 1, ee, 0, zk::kFinalizeThreads))) return s;
   }
   if (pl.mode == ZL_SEMANTICS_GPU_TRAINER && cfg->clamp_log_std) {
     // src/bin/biped_train_gpu.rs:1529-1541, after the epoch loop (even after an early stop).
@@ -1035,7 +1050,8 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
   dalloc((void**)&p->gls_part, (size_t)p->nb_cap * p->A * 4);
   dalloc((void**)&p->astat_part, (size_t)p->nb_cap * 2 * 4);
   dalloc((void**)&p->vstat_part, (size_t)p->nb_cap * 4);
-  dalloc((void**)&p->kl_part, (size_t)p->nb_cap * 4);
+  // zk_kl's per-block totals, or zk_head's [A x blocks] per-component sums.
+  dalloc((void**)&p->kl_part, (size_t)p->nb_cap * std::max(p->A, 1) * 4);
   // zk_reduce_all takes at least kReduceAllThreads / 64 outputs per block
   // (at most 64 split lanes).
   p->sq_cap = 0;

@@ -34,6 +34,10 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bn_64x128x16_w22", true, false, 64, 128, 16, 256, true},
     {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w24_dg", true, false, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bk_96x128x32_w24_x", true, true, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bn_96x128x32_w24_dg_x", true, false, 96, 128, 32, 512, true},
+    {"zk_gemm_am_bn_128x128x32_w24_x", false, false, 128, 128, 32, 512, true},
+    {"zk_gemm_am_bn_64x128x32_w24_x", false, false, 64, 128, 32, 512, true},
     {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512, true},
     {"zk_gemm_am_bn_128x128x32_w24", false, false, 128, 128, 32, 512, true},
     {"zk_gemm_am_bn_32x128x16_w14", false, false, 32, 128, 16, 256, true},
@@ -63,6 +67,18 @@ static int gemm_id(const char* name) {
   for (int i = 0; i < kGemmCount; ++i)
     if (strcmp(kGemmTable[i].name, name) == 0) return K_GEMM_BASE + i;
   return -1;
+}
+
+// Exact-fit twin (name + "_x": no clamps or masks, for M, N and K that are
+// multiples of the tile) of a tiled variant, and back; -1 if there is none.
+static int exact_form(int kid) {
+  const std::string n = std::string(kernel_name(kid)) + "_x";
+  return gemm_id(n.c_str());
+}
+static int inexact_form(int kid) {
+  const std::string n = kernel_name(kid);
+  if (n.size() < 2 || n.compare(n.size() - 2, 2, "_x") != 0) return kid;
+  return gemm_id(n.substr(0, n.size() - 2).c_str());
 }
 
 static thread_local std::string g_init_error;
@@ -286,6 +302,11 @@ static zl_status plan_gemm(zl_ctx* c, const GemmDesc& d, GemmPlan& P) {
     P.splits = (int)std::max<long long>(1, cdiv(kt, P.per));
     P.gx = (unsigned)cdiv(d.M, g.bm);
     P.gy = (unsigned)cdiv(d.N, g.bn);
+    // Every tile and k-tile full: the exact-fit form of the same variant.
+    if (d.K > 0 && d.M % g.bm == 0 && d.N % g.bn == 0 && d.K % g.bk == 0) {
+      const int x = exact_form(P.kid);
+      if (x >= 0) P.kid = x;
+    }
   }
   return ZL_OK;
 }
@@ -304,6 +325,10 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
     zl_status s = plan_gemm(c, *live[i], P[i]);
     if (s) return s;
   }
+  // A pair whose members differ only in exact fit runs as one launch of
+  // the general form.
+  if (nl == 2 && P[0].kid != P[1].kid && inexact_form(P[0].kid) == inexact_form(P[1].kid))
+    P[0].kid = P[1].kid = inexact_form(P[0].kid);
   if (nl == 2 && P[0].kid != P[1].kid) {
     // Two narrow problems of one family that differ only in the template
     // width (16 vs 32 columns / rows, float4 vs element loads) share the
