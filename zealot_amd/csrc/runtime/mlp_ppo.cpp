@@ -1398,49 +1398,43 @@ static zl_status chunked_forward(zl_ppo* p, bool critic, const float* x, int ld,
   const NetBuffers& nb = critic ? p->cb : p->ab;
   if (!x || !out || n < 0 || ld < nl.dims[0] || ld_out < cols)
     return fail(c, ZL_ERR_INVALID, "forward: bad argument");
+  // The output layer writes straight into the caller's rows.
+  auto desc = [&](const NetBuffers& b, const float* xx, int rows, long long r0, int l) {
+    GemmDesc d = fwd_desc(nl, b, p->params, xx, ld, nullptr, rows, nullptr, l);
+    if (l == nl.L - 1) {
+      d.C = out + (size_t)r0 * ld_out;
+      d.ldc = ld_out;
+    }
+    return d;
+  };
   // The other net's activation buffers can hold a second chunk when every
   // layer of this net fits their widths (the critic's in the actor's, same
   // hidden widths): two chunks then run as one grouped launch per layer.
   const NetLayout& onl = critic ? p->actor : p->critic;
   const NetBuffers& onb = critic ? p->ab : p->cb;
   bool borrow = onl.L == nl.L;
-  for (int l = 1; borrow && l <= nl.L; ++l) borrow = onb.ld[l] >= nl.dims[l];
+  for (int l = 1; borrow && l < nl.L; ++l) borrow = onb.ld[l] >= nl.dims[l];
+  long long r0 = 0;
   if (borrow) {
-    long long r0 = 0;
     for (; r0 + p->mb_cap < n; r0 += 2LL * p->mb_cap) {
       const int rows0 = p->mb_cap;
       const int rows1 = (int)std::min<long long>(p->mb_cap, n - r0 - rows0);
       const float* x0 = x + (size_t)r0 * ld;
       const float* x1 = x + (size_t)(r0 + rows0) * ld;
       for (int l = 0; l < nl.L; ++l) {
-        GemmDesc d[2] = {fwd_desc(nl, nb, p->params, x0, ld, nullptr, rows0, nullptr, l),
-                         fwd_desc(nl, onb, p->params, x1, ld, nullptr, rows1, nullptr, l)};
+        GemmDesc d[2] = {desc(nb, x0, rows0, r0, l), desc(onb, x1, rows1, r0 + rows0, l)};
         zl_status s = run_gemm_batch(c, d, 2);
         if (s) return s;
       }
-      zl_status s = copy_rows(c, out + (size_t)r0 * ld_out, ld_out, nb.act[nl.L], nb.ld[nl.L], cols,
-                              rows0, nullptr, 0, nullptr, false);
-      if (s) return s;
-      s = copy_rows(c, out + (size_t)(r0 + rows0) * ld_out, ld_out, onb.act[nl.L], onb.ld[nl.L], cols,
-                    rows1, nullptr, 0, nullptr, false);
-      if (s) return s;
     }
-    if (r0 < n) {
-      const int rows = (int)(n - r0);
-      zl_status s = net_forward(c, nl, nb, p->params, x + (size_t)r0 * ld, ld, nullptr, rows, nullptr);
-      if (s) return s;
-      return copy_rows(c, out + (size_t)r0 * ld_out, ld_out, nb.act[nl.L], nb.ld[nl.L], cols, rows,
-                       nullptr, 0, nullptr, false);
-    }
-    return ZL_OK;
   }
-  for (long long r0 = 0; r0 < n; r0 += p->mb_cap) {
+  for (; r0 < n; r0 += p->mb_cap) {
     const int rows = (int)std::min<long long>(p->mb_cap, n - r0);
-    zl_status s = net_forward(c, nl, nb, p->params, x + (size_t)r0 * ld, ld, nullptr, rows, nullptr);
-    if (s) return s;
-    s = copy_rows(c, out + (size_t)r0 * ld_out, ld_out, nb.act[nl.L], nb.ld[nl.L], cols, rows,
-                  nullptr, 0, nullptr, false);
-    if (s) return s;
+    for (int l = 0; l < nl.L; ++l) {
+      GemmDesc d = desc(nb, x + (size_t)r0 * ld, rows, r0, l);
+      zl_status s = run_gemm_batch(c, &d, 1);
+      if (s) return s;
+    }
   }
   return ZL_OK;
 }
