@@ -36,7 +36,10 @@ HBM_PEAK = 8.0e12  # bytes/s
 # readings of a 256 MiB copy kernel (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0) and
 # averaged over an update's launch mix; reported as roofline.traffic for the
 # dominant kernel when it is one of these.
-MEASURED_TRAFFIC = {"zk_gemm_ak_bk_96x128x32_w24": 123.2e6}
+MEASURED_TRAFFIC = {
+    "zk_gemm_ak_bn_96x128x32_w24_dg_x": 198.5e6,
+    "zk_gemm_ak_bk_96x128x32_w24_x": 120.3e6,
+}
 
 
 def cpu_baseline(ro, actor, critic, log_std, mean_old, action, logp_old, values, adv):
@@ -192,6 +195,33 @@ def trainer_nets_measurement(ctx, steps):
     }
 
 
+def actor_critic_measurement(ctx, gac, batch, step_values, steps):
+    """The same workload under ActorCritic::update semantics
+    (zealot-rl/src/ppo.rs:338-510): a Fisher-Yates shuffle of the batch per
+    epoch from Lcg(t + 1) on the host, uploaded with the update (5 x 98,304
+    row indices), the observation gather fused into the first layer, clip
+    per net, per-step Adam t, mean-only-KL adaptive learning rate. Wall time
+    per update (critic values + GAE + update) over `steps` updates."""
+    from zealot_amd.rl import PpoConfig, _ffi
+
+    cfg = PpoConfig(epochs=EPOCHS, minibatches=MINIBATCHES, clip=0.2, entropy_coef=0.005,
+                    value_coef=1.0, max_grad_norm=1.0, desired_kl=0.01, lr_min=1e-5, lr_max=1e-2,
+                    shuffle=True, normalize_adv=True, clamp_log_std=True).to_c()
+    stats = _ffi.zl_ppo_stats()
+
+    def step():
+        step_values()
+        ctx.check(ctx.lib.zl_ppo_update(gac.h, C.byref(batch), C.byref(cfg), C.byref(stats)), "update")
+
+    t = _timed(ctx, step, steps)
+    return {
+        "workload": "the headline workload under ActorCritic::update semantics (host Fisher-Yates "
+                    "shuffle per epoch + index upload, gathered minibatches, per-net clip, adaptive lr)",
+        "ms_per_update": t * 1e3,
+        "samples_per_s": EPOCHS * N_ENVS * T_STEPS / t,
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +229,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--breakdown", action="store_true", help="per-kernel time table on stderr")
+    ap.add_argument("--no-aux", action="store_true",
+                    help="headline workload only (no aux lines): the process the rocprofv3 profiles cover")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -348,8 +380,17 @@ def main():
     out["update_graph"] = {"captures": captures, "capture_instantiate_ms": capture_ms,
                            "note": "the update graph is captured once per shape / configuration; "
                                    "new batch buffers are read through a device pointer block"}
-    out["aux"] = aux_measurements(ctx, gac, ro, d_obs, LD, n)
-    out["aux"]["trainer_nets_update"] = trainer_nets_measurement(ctx, max(2, min(args.steps, 5)))
+    if not args.no_aux:
+        out["aux"] = aux_measurements(ctx, gac, ro, d_obs, LD, n)
+        out["aux"]["trainer_nets_update"] = trainer_nets_measurement(ctx, max(2, min(args.steps, 5)))
+
+        def values_and_gae():
+            gac.values(d_obs, n, d_val, ld=LD)
+            gac.values(d_boot, N_ENVS, d_last, ld=LD)
+            ops.gae(ctx, d_rew, d_val, d_done, d_last, T_STEPS, N_ENVS, d_adv, d_ret, 0.99, 0.95)
+
+        out["aux"]["actor_critic_update"] = actor_critic_measurement(ctx, gac, batch, values_and_gae,
+                                                                     max(2, min(args.steps, 5)))
     if not args.no_cpu_baseline:
         mean_old = d_mean.numpy()
         action = d_act.numpy()
