@@ -338,7 +338,7 @@ def _gae_f64(r, v, d, last_v, gamma, lam):
     return adv, adv + np.asarray(v, np.float64)
 
 
-@pytest.mark.parametrize("T,N", [(1, 1), (2, 3), (24, 4096), (37, 100)])
+@pytest.mark.parametrize("T,N", [(1, 1), (2, 3), (24, 4096), (32, 333), (37, 100)])
 def test_gae_bit_exact(ctx, T, N):
     g = np.random.default_rng(T * 7 + N)
     r = g.standard_normal((T, N)).astype(np.float32)
@@ -349,7 +349,8 @@ def test_gae_bit_exact(ctx, T, N):
     adv, ret = ctx.alloc((T, N)), ctx.alloc((T, N))
     ops.gae(ctx, dr, dvv, dd, dl, T, N, adv, ret, 0.99, 0.95)
     ga, gr = adv.numpy(), ret.numpy()
-    for e in range(min(N, 64)):
+    # The first 64 envs and every 61st: envs of several workgroups.
+    for e in sorted(set(range(min(N, 64))) | set(range(0, N, 61))):
         ra, rr = zo.gae(r[:, e], v[:, e], d[:, e], float(lv[e]), 0.99, 0.95)
         assert np.array_equal(ga[:, e], ra) and np.array_equal(gr[:, e], rr), e
         fa, fr = _gae_f64(r[:, e], v[:, e], d[:, e], float(lv[e]), 0.99, 0.95)

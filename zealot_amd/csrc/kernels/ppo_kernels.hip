@@ -508,12 +508,44 @@ __device__ void epoch_end_body(const EpochEndArgs& p) {
 // --------------------------------------------------------- GAE / advantages
 
 // zealot-rl/src/ppo.rs:681-703: one thread per env, serial backward scan.
+// For T <= kGaeMaxT an env's whole trajectory (rewards, values, dones) is
+// loaded into registers before the scan, so the loads are all in flight at
+// once instead of one dependent round trip per step; the recurrence is the
+// reference's, term for term.
 __device__ void gae_body(const GaeArgs& p) {
   if (p.guard && *p.guard == 0) return;
-  const int e = blockIdx.x * kThreads + threadIdx.x;
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= p.N) return;
   float acc = 0.f;
   float next_v = p.last_v[e];
+  if (p.T <= kGaeMaxT) {
+    // Every load unconditional (steps past T re-read step T - 1), so they
+    // issue back to back with one wait.
+    float rr[kGaeMaxT], vv[kGaeMaxT];
+    uint8_t dd[kGaeMaxT];
+#pragma unroll
+    for (int i = 0; i < kGaeMaxT; ++i) {
+      const long long ii = (long long)min(i, p.T - 1) * p.in_ts + (long long)e * p.in_es;
+      rr[i] = p.r[ii];
+      vv[i] = p.v[ii];
+      dd[i] = p.done[ii];
+    }
+    float nn[kGaeMaxT];
+#pragma unroll
+    for (int i = 0; i < kGaeMaxT; ++i) nn[i] = dd[i] ? 0.0f : 1.0f;
+#pragma unroll
+    for (int i = kGaeMaxT - 1; i >= 0; --i) {
+      if (i < p.T) {
+        const long long oi = (long long)i * p.out_ts + (long long)e * p.out_es;
+        const float delta = rr[i] + p.gamma * next_v * nn[i] - vv[i];
+        acc = delta + p.gamma * p.lam * nn[i] * acc;
+        p.adv[oi] = acc;
+        p.ret[oi] = acc + vv[i];
+        next_v = vv[i];
+      }
+    }
+    return;
+  }
   for (int i = p.T - 1; i >= 0; --i) {
     const long long ii = (long long)i * p.in_ts + (long long)e * p.in_es;
     const long long oi = (long long)i * p.out_ts + (long long)e * p.out_es;

@@ -263,6 +263,10 @@ struct EpochEndArgs {
   int begin_next;            // also open the next epoch (zk_epoch_begin) if still active
 };
 
+// zk_gae: one wavefront per block (envs spread over the CUs); trajectories
+// of up to kGaeMaxT steps are scanned from registers.
+constexpr int kGaeThreads = 64;
+constexpr int kGaeMaxT = 32;
 struct GaeArgs {
   const float* r;
   const float* v;

@@ -1184,7 +1184,7 @@ zl_status zl_gae(zl_ctx* c, const float* rewards, const float* values, const uin
   a.N = N;
   a.gamma = gamma;
   a.lam = lam;
-  return launch(c, K_GAE, (unsigned)cdiv(N, kThreads), 1, 1, a);
+  return launch(c, K_GAE, (unsigned)cdiv(N, zk::kGaeThreads), 1, 1, a, 0, zk::kGaeThreads);
 }
 
 }  // extern "C"
