@@ -204,6 +204,9 @@ struct GemmDesc {
   float* C = nullptr;
   int ldc = 0;
   int M = 0, N = 0, K = 0;
+  // > 0: the N / K of the product itself when N / K run over zero padding
+  // (the launch's FLOP count for timing uses these).
+  int N_alg = 0, K_alg = 0;
   int epi = zk::kEpiStore;
   const float* bias = nullptr;
   int bias_stride = 1;

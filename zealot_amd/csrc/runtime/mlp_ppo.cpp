@@ -5,7 +5,8 @@
 //   actor  w[0] b[0] w[1] b[1] ... | critic w[0] b[0] ... | log_std
 // with every tensor start aligned to 64 floats (256 B) and w[l] stored
 // [dims[l+1] x ldw] with ldw = dims[l] rounded up to 4, so every GEMM operand
-// row is 16-byte aligned for float4 loads. Gradients and the two Adam moments
+// row is 16-byte aligned for float4 loads (the update's layer-0 weights: up to
+// a whole GEMM k-tile when that adds little, see input_align). Gradients and the two Adam moments
 // use the same layout, so the optimiser is one flat, vectorised pass (one
 // launch for all 2L + 2L + 1 tensors) and the grad-norm clip is a reduction
 // over two contiguous ranges. Padding stays zero forever (zero grads give a
@@ -35,7 +36,7 @@ struct NetLayout {
   long long begin = 0, end = 0;
   long long packed = 0;  // parameter count in the packed (reference) layout
 
-  void build(const int* d, int nd, long long start) {
+  void build(const int* d, int nd, long long start, int in_align = 4) {
     dims.assign(d, d + nd);
     L = nd - 1;
     w_off.resize(L);
@@ -45,7 +46,7 @@ struct NetLayout {
     long long cur = start;
     packed = 0;
     for (int l = 0; l < L; ++l) {
-      ldw[l] = (int)round_up(dims[l], 4);
+      ldw[l] = (int)round_up(dims[l], l == 0 ? in_align : 4);
       w_off[l] = cur;
       cur += round_up((long long)dims[l + 1] * ldw[l], 64);
       b_off[l] = cur;
@@ -78,6 +79,17 @@ struct NetLayout {
     }
   }
 };
+
+// Row alignment of an update's layer-0 weights and staged observations: a
+// whole 32-wide GEMM k-tile when that adds at most 1/16 to the row (123 -> 128
+// features), else 4. The staged rows are zero past the features and so are
+// the weights' padding columns, so the layer-0 GEMMs can run over the padded
+// width (the forward's K, the weight gradient's N) and take the exact-fit
+// kernels without changing a result: the extra terms are 0 * 0.
+constexpr int kInputTile = 32;
+inline int input_align(int d) {
+  return round_up(d, kInputTile) * 16 <= (long long)d * 17 ? kInputTile : 4;
+}
 
 // Per-row activation and delta buffers of one MLP for up to `rows` rows.
 struct NetBuffers {
@@ -116,10 +128,11 @@ static size_t net_ws_floats(const zl_ctx* c, const NetLayout& nl, int rows) {
 }
 
 // Layer l of GpuMlp::forward (src/bin/biped_train_gpu.rs:364-422): one fused
-// GEMM + bias + ELU, linear last layer (zealot-rl/src/net.rs:88-108).
+// GEMM + bias + ELU, linear last layer (zealot-rl/src/net.rs:88-108). kx: the
+// layer-0 width, as for wgrad_desc.
 static GemmDesc fwd_desc(const NetLayout& nl, const NetBuffers& nb, const float* params,
                          const float* x, int ldx, const int* permx, int rows, const int* guard,
-                         int l) {
+                         int l, int kx = 0) {
   GemmDesc d;
   d.A = l == 0 ? x : nb.act[l];
   d.lda = l == 0 ? ldx : nb.ld[l];
@@ -132,7 +145,8 @@ static GemmDesc fwd_desc(const NetLayout& nl, const NetBuffers& nb, const float*
   d.ldc = nb.ld[l + 1];
   d.M = rows;
   d.N = nl.dims[l + 1];
-  d.K = nl.dims[l];
+  d.K = l == 0 && kx > 0 ? kx : nl.dims[l];
+  d.K_alg = nl.dims[l];
   d.epi = zk::kEpiBiasN;
   d.bias = params + nl.b_off[l];
   d.act = l < nl.L - 1 ? 1 : 0;
@@ -143,10 +157,11 @@ static GemmDesc fwd_desc(const NetLayout& nl, const NetBuffers& nb, const float*
 // Weight gradient of layer l (GpuMlp::backward, src/bin/biped_train_gpu.rs:423-500,
 // math of zealot-rl/src/net.rs:113-140): dW = delta^T . a, split-K over the
 // rows with a fixed-order reduction, and the bias gradient as the row sums
-// of delta^T fused in. `dl` is dL/dz of the layer.
+// of delta^T fused in. `dl` is dL/dz of the layer. kx > 0: layer 0 runs over
+// kx input columns (x and the weights zero past dims[0], kx <= ldw[0]).
 static GemmDesc wgrad_desc(const NetLayout& nl, const NetBuffers& nb, float* grads, const float* x,
                            int ldx, const int* permx, int rows, const float* dl, int ldd,
-                           const int* guard, int l) {
+                           const int* guard, int l, int kx = 0) {
   GemmDesc w;
   w.A = dl;
   w.lda = ldd;
@@ -158,7 +173,8 @@ static GemmDesc wgrad_desc(const NetLayout& nl, const NetBuffers& nb, float* gra
   w.C = grads + nl.w_off[l];
   w.ldc = nl.ldw[l];
   w.M = nl.dims[l + 1];
-  w.N = nl.dims[l];
+  w.N = l == 0 && kx > 0 ? kx : nl.dims[l];
+  w.N_alg = nl.dims[l];
   w.K = rows;
   w.rowsum_out = grads + nl.b_off[l];
   w.guard = guard;
@@ -190,9 +206,9 @@ static GemmDesc dgrad_desc(const NetLayout& nl, const NetBuffers& nb, const floa
 
 static zl_status net_forward(zl_ctx* c, const NetLayout& nl, const NetBuffers& nb,
                              const float* params, const float* x, int ldx, const int* permx,
-                             int rows, const int* guard) {
+                             int rows, const int* guard, int kx = 0) {
   for (int l = 0; l < nl.L; ++l) {
-    const GemmDesc d = fwd_desc(nl, nb, params, x, ldx, permx, rows, guard, l);
+    const GemmDesc d = fwd_desc(nl, nb, params, x, ldx, permx, rows, guard, l, kx);
     zl_status s = run_gemm(c, d);
     if (s) return s;
   }
@@ -227,6 +243,7 @@ struct NetView {
   const NetBuffers* nb;
   const float* x;  // layer-0 input rows
   int ldx;
+  int kx = 0;      // > 0: x is zero past dims[0] up to kx columns (<= ldw[0])
 };
 
 // Forward of both nets, layer by layer, each layer's two GEMMs in one launch
@@ -237,7 +254,7 @@ static zl_status pair_forward(zl_ctx* c, const NetView v[2], const float* params
     for (int l = 0; l < layers; ++l) {
       GemmDesc d[2];
       for (int i = 0; i < 2; ++i)
-        d[i] = fwd_desc(*v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard, l);
+        d[i] = fwd_desc(*v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard, l, v[i].kx);
       zl_status s = run_gemm_batch(c, d, 2);
       if (s) return s;
     }
@@ -245,7 +262,8 @@ static zl_status pair_forward(zl_ctx* c, const NetView v[2], const float* params
   }
   if (v[0].nl->L != v[1].nl->L) {
     for (int i = 0; i < 2; ++i) {
-      zl_status s = net_forward(c, *v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard);
+      zl_status s = net_forward(c, *v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard,
+                                v[i].kx);
       if (s) return s;
     }
     return ZL_OK;
@@ -253,7 +271,7 @@ static zl_status pair_forward(zl_ctx* c, const NetView v[2], const float* params
   for (int l = 0; l < v[0].nl->L; ++l) {
     GemmDesc d[2];
     for (int i = 0; i < 2; ++i)
-      d[i] = fwd_desc(*v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard, l);
+      d[i] = fwd_desc(*v[i].nl, *v[i].nb, params, v[i].x, v[i].ldx, permx, rows, guard, l, v[i].kx);
     zl_status s = run_gemm_batch(c, d, 2);
     if (s) return s;
   }
@@ -276,9 +294,13 @@ struct PartialPlan {
       for (int l = 0; l < nl[i]->L; ++l) {
         off[i][l] = total;
         const long long M = nl[i]->dims[l + 1], N = nl[i]->dims[l];
+        // Layer 0 may run over the padded width ldw[0] (NetView::kx).
         size[i][l] = fused_head && l == nl[i]->L - 1
                          ? (size_t)zk::kHeadMaxBlocks * (M * N + M)
                          : gemm_ws_floats(c, (int)M, (int)N, rows, false, false, zk::kEpiStore);
+        if (l == 0)
+          size[i][l] = std::max(size[i][l], gemm_ws_floats(c, (int)M, nl[i]->ldw[0], rows, false,
+                                                           false, zk::kEpiStore));
         total += round_up((long long)size[i][l], 64);
       }
     }
@@ -306,7 +328,7 @@ static zl_status pair_backward(zl_ctx* c, const NetView v[2], const float* param
       const float* dl = l == nl.L - 1 ? top[i] : nb.delta[l];
       const int ldd = l == nl.L - 1 ? ld_top[i] : nb.ld[l + 1];
       GemmDesc& q = w[nw++];
-      q = wgrad_desc(nl, nb, grads, v[i].x, v[i].ldx, permx, rows, dl, ldd, guard, l);
+      q = wgrad_desc(nl, nb, grads, v[i].x, v[i].ldx, permx, rows, dl, ldd, guard, l, v[i].kx);
       q.ws = pws + pp.off[i][l];
       q.ws_floats = pp.size[i][l];
       q.seg_out = &segs[i * L[0] + l];
@@ -794,12 +816,12 @@ zl_status check_batch(zl_ppo* p, const zl_batch* b, const char* who) {
 // Lay out the staged copy of `rows` batch samples (source sample perm[row0 + r],
 // or row0 + r) in the handle's buffers, growing them as needed: the zk_stage
 // launch reading the caller's pointers from p->bptrs, and the staged batch
-// view (batch-major rows; observation rows padded to a multiple of 4 floats
+// view (batch-major rows; observation rows padded to the layer-0 weight rows
 // and zero-filled, 16-byte aligned for the layer-0 GEMM loads).
 zl_status plan_stage(zl_ppo* p, const zl_batch* b, long long rows, const int* perm, long long row0,
                      zk::StageArgs* st, int* blocks, zl_batch* sb, bool* share_out) {
   const int od = p->actor.dims[0], cd = p->critic.dims[0], A = p->A;
-  const int odp = (int)round_up(od, 4), cdp = (int)round_up(cd, 4);
+  const int odp = p->actor.ldw[0], cdp = p->critic.ldw[0];  // zero-filled past od / cd
   const unsigned fm = b->feature_major;
   const bool share = b->critic_obs == b->obs && b->ld_critic_obs == b->ld_obs && od == cd &&
                      ((fm & ZL_FM_OBS) != 0) == ((fm & ZL_FM_CRITIC_OBS) != 0);
@@ -921,7 +943,8 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
       const int* px = perm_e ? perm_e + row0 : nullptr;
       const float* xa = perm_e ? pl.X : pl.X + (size_t)row0 * pl.ldx;
       const float* xc = perm_e ? pl.XC : pl.XC + (size_t)row0 * pl.ldxc;
-      const NetView v[2] = {{&p->actor, &p->ab, xa, pl.ldx}, {&p->critic, &p->cb, xc, pl.ldxc}};
+      const NetView v[2] = {{&p->actor, &p->ab, xa, pl.ldx, pl.ldx},
+                            {&p->critic, &p->cb, xc, pl.ldxc, pl.ldxc}};
       float* hkl = head_kl && k == pl.n_mb - 1 ? p->kl_part : nullptr;
       PassCounts pc;
       if ((s = minibatch_pass(p, v, px, perm_e, row0, pl.mb, b, cfg, pl.pp.scale, guard, &pc, hkl)))
@@ -1019,8 +1042,8 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
                 zk::kMaxReduceSegs);
   zl_ppo* p = new zl_ppo();
   p->c = c;
-  p->actor.build(adims, na, 0);
-  p->critic.build(cdims, nc, p->actor.end);
+  p->actor.build(adims, na, 0, input_align(adims[0]));
+  p->critic.build(cdims, nc, p->actor.end, input_align(cdims[0]));
   p->A = adims[na - 1];
   p->ls_off = p->critic.end;
   p->nflat = p->ls_off + round_up(p->A, 64);
@@ -1360,8 +1383,9 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
   if ((s = launch(c, K_STAGE, (unsigned)pl.stage_blocks, 1, 1, pl.stage))) return s;
   const int A = p->A;
   if ((s = ensure_partials(p, rows))) return s;
-  const NetView v[2] = {{&p->actor, &p->ab, pl.sb.obs, pl.sb.ld_obs},
-                        {&p->critic, &p->cb, pl.sb.critic_obs, pl.sb.ld_critic_obs}};
+  const NetView v[2] = {{&p->actor, &p->ab, pl.sb.obs, pl.sb.ld_obs, pl.sb.ld_obs},
+                        {&p->critic, &p->cb, pl.sb.critic_obs, pl.sb.ld_critic_obs,
+                         pl.sb.ld_critic_obs}};
   PassCounts pc;
   if ((s = minibatch_pass(p, v, nullptr, nullptr, 0, rows, &pl.sb, cfg, 1.0f / (float)rows,
                           nullptr, &pc)))

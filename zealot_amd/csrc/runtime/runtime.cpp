@@ -408,7 +408,7 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
     gx = std::max(gx, P[i].gx);
     gy = std::max(gy, P[i].gy);
     if (g.kind == G_TILED) B.zper = std::max(B.zper, P[i].splits);
-    flops += 2.0 * q.M * q.N * (double)q.K;
+    flops += 2.0 * q.M * (q.N_alg > 0 ? q.N_alg : q.N) * (double)(q.K_alg > 0 ? q.K_alg : q.K);
   }
   c->pending_flops = flops;
   c->pending_shape = {live[0]->M, live[0]->N, live[0]->K, P[0].splits};
