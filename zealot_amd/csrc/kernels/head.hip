@@ -28,20 +28,37 @@ constexpr int kHeadLds =
 static_assert(kHeadRows == 64 && kHeadMaxHidden == 128 && kHeadMaxActions == 32,
               "wave-to-tile mapping of zk_head");
 
+// A float4 with the components at column c + i >= lim (or all, if !row_ok)
+// replaced by 0.
+__device__ __forceinline__ float4 quad_or_zero(float4 v, bool row_ok, int c, int lim) {
+  v.x = row_ok && c < lim ? v.x : 0.f;
+  v.y = row_ok && c + 1 < lim ? v.y : 0.f;
+  v.z = row_ok && c + 2 < lim ? v.z : 0.f;
+  v.w = row_ok && c + 3 < lim ? v.w : 0.f;
+  return v;
+}
+
 // Rows [r0, r0 + nr) of x into sx (kHeadRows x kHeadPitch), zero past nr
-// rows and past H columns (up to kHeadMaxHidden).
+// rows and past H columns (up to kHeadMaxHidden); nr >= 1. Every thread's
+// loads are unconditional, from clamped in-range addresses (a float4 at a
+// column < H stays inside the row's 4-aligned stride), so they all issue
+// before the first wait; out-of-range values are replaced by 0 afterwards.
 __device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, int nr, float* sx) {
   constexpr int QPR = kHeadMaxHidden / 4;  // float4 quads per row
-  for (int i = threadIdx.x; i < kHeadRows * QPR; i += kHeadThreads) {
-    const int r = i / QPR, c = (i % QPR) * 4;
-    float4 v = {0.f, 0.f, 0.f, 0.f};
-    if (r < nr && c < q.H) {
-      v = *reinterpret_cast<const float4*>(q.x + (r0 + r) * q.ldx + c);
-      if (c + 1 >= q.H) v.y = 0.f;
-      if (c + 2 >= q.H) v.z = 0.f;
-      if (c + 3 >= q.H) v.w = 0.f;
-    }
-    *reinterpret_cast<float4*>(sx + r * kHeadPitch + c) = v;
+  constexpr int NQ = kHeadRows * QPR / kHeadThreads;
+  static_assert(kHeadRows * QPR % kHeadThreads == 0, "whole quads per thread");
+  const int c_last = (q.H - 1) & ~3;
+  const float* base = q.x + r0 * q.ldx;  // uniform; 32-bit offsets within the tile
+  float4 v[NQ];
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int i = threadIdx.x + kHeadThreads * u, r = i / QPR, c = (i % QPR) * 4;
+    v[u] = *reinterpret_cast<const float4*>(base + (min(r, nr - 1) * q.ldx + min(c, c_last)));
+  }
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    const int i = threadIdx.x + kHeadThreads * u, r = i / QPR, c = (i % QPR) * 4;
+    *reinterpret_cast<float4*>(sx + r * kHeadPitch + c) = quad_or_zero(v[u], r < nr, c, q.H);
   }
 }
 
@@ -74,16 +91,22 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   const int lr = lane & 15, lg = lane >> 4;
   const int A = p.A, H = q.H;
 
-  for (int i = t; i < kHeadMaxActions * (kHeadMaxHidden / 4); i += kHeadThreads) {
-    const int m = i / (kHeadMaxHidden / 4), c = (i % (kHeadMaxHidden / 4)) * 4;
-    float4 v = {0.f, 0.f, 0.f, 0.f};
-    if (m < A && c < H) {
-      v.x = q.w[(long long)m * q.ldw + c];
-      v.y = c + 1 < H ? q.w[(long long)m * q.ldw + c + 1] : 0.f;
-      v.z = c + 2 < H ? q.w[(long long)m * q.ldw + c + 2] : 0.f;
-      v.w = c + 3 < H ? q.w[(long long)m * q.ldw + c + 3] : 0.f;
+  {  // the head weights, rows >= A and columns >= H zero (loads as in head_load_tile)
+    constexpr int QPR = kHeadMaxHidden / 4;
+    constexpr int NQ = kHeadMaxActions * QPR / kHeadThreads;
+    static_assert(kHeadMaxActions * QPR % kHeadThreads == 0, "whole quads per thread");
+    const int c_last = (H - 1) & ~3;
+    float4 v[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int i = t + kHeadThreads * u, m = i / QPR, c = (i % QPR) * 4;
+      v[u] = *reinterpret_cast<const float4*>(q.w + (long long)min(m, A - 1) * q.ldw + min(c, c_last));
     }
-    *reinterpret_cast<float4*>(sw + m * kHeadPitch + c) = v;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      const int i = t + kHeadThreads * u, m = i / QPR, c = (i % QPR) * 4;
+      *reinterpret_cast<float4*>(sw + m * kHeadPitch + c) = quad_or_zero(v[u], m < A, c, H);
+    }
   }
 
   // Loss lanes: 16 groups of 32, lane k on action component k.
@@ -115,18 +138,24 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     const int nr = (int)min((long long)kHeadRows, p.rows - r0);
     // Loss inputs of the group's rows, in flight during the tile load and
     // the forward (group g takes rows g, g + 16, ...).
+    // Rows past nr read the last row's inputs (the loss skips those rows),
+    // so every load is unconditional in the row and the sample indices of
+    // a shuffled minibatch are all in flight before the first wait.
+    long long sidx[RG];
+#pragma unroll
+    for (int j = 0; j < RG; ++j) {
+      const long long rr = p.row0 + r0 + min(grp + kHeadGroups * j, nr - 1);
+      sidx[j] = p.perm ? (long long)p.perm[rr] : rr;
+    }
     In in[RG];
 #pragma unroll
     for (int j = 0; j < RG; ++j) {
-      const int row = grp + kHeadGroups * j;
-      In x{0.f, 0.f, 0.f, 0.f};
-      if (row < nr) {
-        const long long s = p.perm ? p.perm[p.row0 + r0 + row] : (long long)(p.row0 + r0 + row);
-        x.act = on ? p.action[s * p.ldact + k] : 0.f;
-        x.lpo = p.logp_old[s];
-        x.adv = p.adv[s];
-        x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
-      }
+      const long long s = sidx[j];
+      In x;
+      x.act = on ? p.action[s * p.ldact + k] : 0.f;
+      x.lpo = p.logp_old[s];
+      x.adv = p.adv[s];
+      x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
       in[j] = x;
     }
     lds_barrier();  // the previous tile's LDS reads are done
@@ -392,7 +421,10 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
 
 }  // namespace zk
 
-extern "C" __global__ __launch_bounds__(zk::kHeadThreads) void zk_head(zk::HeadArgs p) {
+// Held to four waves per SIMD (two blocks of eight wavefronts per CU, which
+// the LDS footprint allows): at most 128 VGPRs.
+extern "C" __global__ __launch_bounds__(zk::kHeadThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void zk_head(zk::HeadArgs p) {
   __shared__ __align__(16) float smem[zk::kHeadLds];
   if (p.guard && *p.guard == 0) return;
   if (blockIdx.z == 0)
