@@ -733,6 +733,3 @@ extern "C" __global__ __launch_bounds__(256) void zk_splitk_reduce(zk::SplitRedu
   zk::splitk_reduce_body(p);
 }
 
-extern "C" __global__ __launch_bounds__(zk::kReduceAllThreads) void zk_reduce_all(zk::ReduceAllArgs a) {
-  zk::reduce_all_body(a);
-}

@@ -6,6 +6,7 @@
 // like the reference's Rust source (zealot-rl/src/net.rs, ppo.rs).
 #pragma once
 #include "common.hip"
+#include "gemm_mfma.hip"  // reduce_all_body (zk_reduce_all is defined here, with its tail block)
 
 namespace zk {
 
@@ -213,23 +214,25 @@ __device__ void sumsq_body(const SumsqArgs& p) {
   if (threadIdx.x == 0) p.part[b] = tot;
 }
 
-// Scalar tail of one minibatch step: ppo.rs:464-489 (ActorCritic::update
-// semantics) or src/bin/biped_train_gpu.rs:1350-1452 (trainer semantics),
-// with every scalar kept on the device.
-__device__ void finalize_body(const FinalizeArgs& p) {
-  // Quantities 0..4: surrogate, kl, value loss, actor and critic squared
-  // norms; 5..5+A-1: the log_std gradient, each a sum over per-block
-  // partials. A group of 32 lanes takes quantities g, g + 32, ...: lane l
-  // adds partials l, l + 32, ... in order (loads issued 8 at a time), then
-  // the group's lanes are combined by a fixed butterfly, so the result is
-  // deterministic.
+// Scalar tail of one minibatch step, the part that needs only the loss
+// partials: ppo.rs:464-489 (ActorCritic::update semantics) or
+// src/bin/biped_train_gpu.rs:1350-1452 (trainer semantics), every scalar kept
+// on the device. Runs as the extra last block of zk_reduce_all (the loss
+// partials are complete when that launch starts); the clip scales follow in
+// zk_adam, which also needs this block's log_std squared norm (sq_part[nsq]).
+__device__ void minibatch_tail_body(const FinalizeArgs& p) {
+  // Quantities 0..2: surrogate, kl, value loss; 3..3+A-1: the log_std
+  // gradient, each a sum over per-block partials. A group of 32 lanes takes
+  // quantities g, g + 32, ...: lane l adds partials l, l + 32, ... in order
+  // (loads issued 8 at a time), then the group's lanes are combined by a
+  // fixed butterfly, so the result is deterministic.
   constexpr int kMaxA = 256;
-  __shared__ float q[5 + kMaxA];
-  if (p.guard && *p.guard == 0) return;
+  constexpr int kQ = 3;
+  __shared__ float q[kQ + kMaxA];
   const int t = threadIdx.x;
   const int wave = t >> 6, lane = t & 63;
   const int A = p.pp.A;
-  const int nq = 5 + A;
+  const int nq = kQ + A;
   const int grp = t >> 5, gln = t & 31;
   constexpr int kGroups = kFinalizeThreads / 32;
   for (int j = grp; j < nq; j += kGroups) {
@@ -241,12 +244,8 @@ __device__ void finalize_body(const FinalizeArgs& p) {
       ptr = p.astat_part + p.nb_a, n = p.nb_a;
     } else if (j == 2) {
       ptr = p.vstat_part, n = p.nb_v;
-    } else if (j == 3) {
-      ptr = p.sq_part, n = p.nsq_a;
-    } else if (j == 4) {
-      ptr = p.sq_part + p.nsq_a, n = p.nsq - p.nsq_a;
     } else {
-      ptr = p.gls_part + (long long)(j - 5) * p.nb_a, n = p.nb_a;
+      ptr = p.gls_part + (long long)(j - kQ) * p.nb_a, n = p.nb_a;
     }
     float v = 0.f;
     for (int i0 = gln; i0 < n; i0 += 8 * 32) {
@@ -261,7 +260,7 @@ __device__ void finalize_body(const FinalizeArgs& p) {
     for (int m = 16; m > 0; m >>= 1) v = v + __shfl_xor(v, m, 32);
     if (gln == 0) {
       q[j] = v;
-      if (j >= 5) p.g_logstd[j - 5] = v;
+      if (j >= kQ) p.g_logstd[j - kQ] = v;
     }
   }
   __syncthreads();
@@ -271,7 +270,7 @@ __device__ void finalize_body(const FinalizeArgs& p) {
   const float c = 0.5f + kLogSqrt2Pi;
   float gl = 0.f, el = 0.f;
   for (int k = lane; k < A; k += 64) {
-    const float g = q[5 + k];
+    const float g = q[kQ + k];
     gl += g * g;
     el += p.log_std[k] + c;
   }
@@ -280,8 +279,8 @@ __device__ void finalize_body(const FinalizeArgs& p) {
   if (lane != 0) return;
   DevState* st = p.st;
   const PpoParams& pp = p.pp;
-  const float surr = q[0], kl = q[1], vloss = q[2], sq_a = q[3], sq_c = q[4];
-
+  const float surr = q[0], kl = q[1], vloss = q[2];
+  p.sq_part[p.nsq] = sq_l;
   if (pp.mode == 0) {
     if (pp.adaptive_lr) {  // ppo.rs:476-482
       if (kl > pp.desired_kl * 2.0f)
@@ -289,34 +288,60 @@ __device__ void finalize_body(const FinalizeArgs& p) {
       else if (kl > 0.0f && kl < pp.desired_kl / 2.0f)
         st->lr = fminf(st->lr * 1.5f, pp.lr_max);
     }
-    // MlpGrad::clip per net (net.rs:197-202); log_std is not clipped.
-    const float na = sqrtf(sq_a), nc = sqrtf(sq_c);
-    st->scale[0] = (na > pp.max_grad_norm && na > 0.0f) ? pp.max_grad_norm / na : 1.0f;
-    st->scale[1] = (nc > pp.max_grad_norm && nc > 0.0f) ? pp.max_grad_norm / nc : 1.0f;
-    st->scale[2] = 1.0f;
-    st->norm[0] = na;
-    st->norm[1] = nc;
     st->norm[2] = sqrtf(sq_l);
     st->t += 1;  // Adam::step / step_log_std advance together (net.rs:235, ppo.rs:497)
     st->bc1 = 1.0f - powi_f32(pp.beta1, st->t);
     st->bc2 = 1.0f - powi_f32(pp.beta2, st->t);
-  } else {
-    // Global clip over actor + critic + log_std (biped_train_gpu.rs:1368-1452).
-    float s = 1.0f;
-    if (pp.max_grad_norm > 0.0f) {
-      const float norm = sqrtf(sq_a + sq_c + sq_l);
-      if (norm > pp.max_grad_norm) s = pp.max_grad_norm / norm;
-      st->norm[0] = norm;
-    }
-    st->scale[0] = s;
-    st->scale[1] = s;
-    st->scale[2] = s;
   }
   st->ep_kl += kl;
   st->ep_surr += surr;
   st->ep_vloss += vloss;
   st->ep_ent += ent;
   st->mb_in_epoch += 1;
+}
+
+// The clip scales of one minibatch step from zk_reduce_all's squared-norm
+// partials (AdamArgs::clip): MlpGrad::clip per net (net.rs:197-202; log_std
+// is not clipped) or the trainer's global clip over actor + critic + log_std
+// (src/bin/biped_train_gpu.rs:1368-1452). Every block of zk_adam sums the
+// partials in the same fixed order (thread-strided, then a fixed tree), so
+// all blocks use the same scales; block 0 records them and the norms in st.
+__device__ __forceinline__ void adam_clip_scales(const AdamArgs& p, float* s0, float* s1, float* s2) {
+  __shared__ float red[kThreads];
+  float a = 0.f, c = 0.f;
+  for (int i = threadIdx.x; i < p.nsq; i += kThreads) {
+    if (i < p.nsq_a)
+      a += p.sq_part[i];
+    else
+      c += p.sq_part[i];
+  }
+  const float sq_a = block_sum<kThreads>(a, red);
+  const float sq_c = block_sum<kThreads>(c, red);
+  const float mg = p.max_grad_norm;
+  const bool rec = blockIdx.x == 0 && threadIdx.x == 0;
+  if (p.clip == 1) {
+    const float na = sqrtf(sq_a), nc = sqrtf(sq_c);
+    *s0 = (na > mg && na > 0.0f) ? mg / na : 1.0f;
+    *s1 = (nc > mg && nc > 0.0f) ? mg / nc : 1.0f;
+    *s2 = 1.0f;
+    if (rec) {
+      p.st->norm[0] = na;
+      p.st->norm[1] = nc;
+    }
+  } else {
+    float sc = 1.0f;
+    if (mg > 0.0f) {
+      const float norm = sqrtf(sq_a + sq_c + p.sq_part[p.nsq]);
+      if (norm > mg) sc = mg / norm;
+      if (rec) p.st->norm[0] = norm;
+    }
+    *s0 = *s1 = *s2 = sc;
+  }
+  if (rec) {
+    p.st->scale[0] = *s0;
+    p.st->scale[1] = *s1;
+    p.st->scale[2] = *s2;
+  }
 }
 
 // Adam element update of zealot-rl/src/net.rs:240-245 over one flat buffer
@@ -329,9 +354,13 @@ __device__ void adam_body(const AdamArgs& p) {
     lr = p.st->lr;
     bc1 = p.st->bc1;
     bc2 = p.st->bc2;
-    s0 = p.st->scale[0];
-    s1 = p.st->scale[1];
-    s2 = p.st->scale[2];
+    if (p.clip) {
+      adam_clip_scales(p, &s0, &s1, &s2);
+    } else {
+      s0 = p.st->scale[0];
+      s1 = p.st->scale[1];
+      s2 = p.st->scale[2];
+    }
   }
   const float b1 = p.beta1, b2 = p.beta2, eps = p.eps;
   const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
@@ -895,10 +924,17 @@ extern "C" __global__ __launch_bounds__(zk::kLossThreads) void zk_actor_loss_g64
 }
 ZK_KERNEL(zk_value_loss, ValueLossArgs, value_loss_body)
 ZK_KERNEL(zk_sumsq, SumsqArgs, sumsq_body)
-extern "C" __global__ __launch_bounds__(zk::kFinalizeThreads) void zk_finalize(zk::FinalizeArgs p) {
-  zk::finalize_body(p);
-}
 ZK_KERNEL(zk_adam, AdamArgs, adam_body)
+
+// All weight and bias gradients of a minibatch step (reduce_all_body) and,
+// when tail_block >= 0, the scalar tail of the step in that extra last block.
+extern "C" __global__ __launch_bounds__(zk::kReduceAllThreads) void zk_reduce_all(zk::ReduceAllArgs a) {
+  if (a.guard && *a.guard == 0) return;
+  if ((int)blockIdx.x == a.tail_block)
+    zk::minibatch_tail_body(a.tail);
+  else
+    zk::reduce_all_body(a);
+}
 ZK_KERNEL(zk_epoch_begin, EpochBeginArgs, epoch_begin_body)
 ZK_KERNEL(zk_kl, KlArgs, kl_body)
 extern "C" __global__ __launch_bounds__(zk::kFinalizeThreads) void zk_epoch_end(zk::EpochEndArgs p) {

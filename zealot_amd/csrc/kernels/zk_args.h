@@ -7,12 +7,14 @@
 
 namespace zk {
 
-// zk_finalize: one block of 16 wavefronts (32 lane groups, one quantity each
-// at a time).
+// The minibatch tail (the extra last block of zk_reduce_all) and
+// zk_epoch_end: one block of 16 wavefronts (32 lane groups, one quantity
+// each at a time).
 constexpr int kFinalizeThreads = 1024;
 // Block sizes of zk_actor_loss (32 lane groups) and zk_reduce_all.
 constexpr int kLossThreads = 1024;
 constexpr int kReduceAllThreads = 1024;
+static_assert(kFinalizeThreads == kReduceAllThreads, "the tail runs as a zk_reduce_all block");
 
 enum EpiMode : int {
   kEpiStore = 0,    // C = acc
@@ -113,17 +115,21 @@ struct PpoParams {
   float beta1, beta2, eps;
 };
 
+// The scalar tail of a minibatch step that needs only the loss partials
+// (statistics, the log_std gradient and its squared norm, the Adam step
+// count and the lr rule): run by one extra block of zk_reduce_all, beside the
+// gradient reduction; the clip scales, which need every block's squared-norm
+// partial, are taken by zk_adam's blocks (AdamArgs::clip).
 struct FinalizeArgs {
   DevState* st;
   const float* gls_part;    // [A x nb_a]
   const float* astat_part;  // [2 x nb_a]
   const float* vstat_part;  // [nb_v]
-  const float* sq_part;     // [nsq]
+  float* sq_part;           // slot nsq receives the log_std gradient's squared norm
   const float* log_std;     // [A] (pre-step values)
   float* g_logstd;          // [A] log_std gradient slot in the flat gradient
-  const int* guard;
   PpoParams pp;
-  int nb_a, nb_v, nsq, nsq_a;
+  int nb_a, nb_v, nsq;
 };
 
 constexpr int kMaxReduceSegs = 16;
@@ -132,6 +138,8 @@ struct ReduceAllArgs {
   int nseg;
   float* sq_part;  // per-block sum of squares of the block's final values
   const int* guard;
+  int tail_block;  // >= 0: this block (the last) runs the minibatch tail `tail`
+  FinalizeArgs tail;
 };
 
 struct ActorLossArgs {
@@ -223,12 +231,20 @@ struct AdamArgs {
   const float* g;
   float* m;
   float* v;
-  const DevState* st;         // lr / bc1 / bc2 / scale from the device, or
+  DevState* st;               // lr / bc1 / bc2 (and with clip 0 the scales) from the device, or
   const int* guard;
   long long n, end_a, end_c;  // groups: [0,end_a) actor, [end_a,end_c) critic, rest log_std
   float lr, bc1, bc2;         // ... these when st == nullptr (scale = 1)
   float beta1, beta2, eps;
   int clamp_ls;               // clamp group 2 to [-1.6, 1.0] (ppo.rs:508)
+  // Clip scales taken here from zk_reduce_all's squared-norm partials (every
+  // block sums them in the same fixed order; block 0 records scales and
+  // norms in st): clip 0 = st->scale as it is; 1 = per net (ActorCritic:
+  // partials [0, nsq_a) actor, [nsq_a, nsq) critic, log_std unclipped);
+  // 2 = one global scale over actor + critic + log_std (sq_part[nsq]).
+  const float* sq_part;
+  int nsq_a, nsq, clip;
+  float max_grad_norm;
 };
 
 struct EpochBeginArgs {

@@ -20,7 +20,6 @@ enum KernelId : int {
   K_ACTOR_LOSS,
   K_VALUE_LOSS,
   K_SUMSQ,
-  K_FINALIZE,
   K_ADAM,
   K_EPOCH_BEGIN,
   K_KL,
@@ -236,8 +235,10 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n);
 // Block layout of zk_reduce_all over `segs` (fills lanes / blk0 / nqb / nrb);
 // returns the block count (= number of sum-of-squares partials).
 int reduce_all_layout(zk::ReduceSeg* segs, int nseg);
+// With `tail`, one extra block runs the minibatch tail (its nsq is set to the
+// reduction's block count, the slot of the log_std squared norm in sq_part).
 zl_status launch_reduce_all(zl_ctx* c, const zk::ReduceSeg* segs, int nseg, float* sq_part,
-                            const int* guard);
+                            const int* guard, const zk::FinalizeArgs* tail = nullptr);
 // Fixed-order sum over the split slices (zk_splitk_reduce); picks the split
 // lanes and grid from the shape. `r.lanes` is set here.
 zl_status launch_splitk_reduce(zl_ctx* c, zk::SplitReduceArgs& r);

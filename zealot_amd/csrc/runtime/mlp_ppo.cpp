@@ -616,8 +616,10 @@ zl_status ensure_partials(zl_ppo* p, int rows) {
 
 // Backward of both nets for one minibatch plus the all-layer reduction with
 // the grad-norm partials; nsq / nsq_a receive the partial counts (all, actor).
+// With `tail`, the reduction launch also runs the minibatch tail.
 zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, int rows,
-                              const int* guard, int* nsq, int* nsq_a, int head_blocks) {
+                              const int* guard, int* nsq, int* nsq_a, int head_blocks,
+                              const zk::FinalizeArgs* tail) {
   zl_ctx* c = p->c;
   const int La = p->actor.L, Lc = p->critic.L;
   const float* top[2] = {p->ab.delta[La - 1], p->cb.delta[Lc - 1]};
@@ -651,11 +653,12 @@ zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, i
   zk::ReduceSeg lay[zk::kMaxReduceSegs];
   std::copy(segs, segs + La + Lc, lay);
   const int blocks = reduce_all_layout(lay, La + Lc);
-  if (blocks > p->sq_cap)
-    return fail(c, ZL_ERR_INVALID, "grad-norm partials: %d blocks > capacity %d", blocks, p->sq_cap);
+  if (blocks + 1 > p->sq_cap)
+    return fail(c, ZL_ERR_INVALID, "grad-norm partials: %d blocks > capacity %d", blocks + 1,
+                p->sq_cap);
   *nsq = blocks;
   *nsq_a = lay[La].blk0;
-  return launch_reduce_all(c, segs, La + Lc, p->sq_part, guard);
+  return launch_reduce_all(c, segs, La + Lc, p->sq_part, guard, tail);
 }
 
 // Loss-partial and grad-norm-partial counts of one minibatch pass.
@@ -668,10 +671,12 @@ struct PassCounts {
 // zealot-rl/src/ppo.rs:406-462 before clip / Adam). `px` gathers the
 // layer-0 rows; samples of the batch are perm[row0 + r] (or row0 + r). With
 // `head_kl`, zk_head also writes the per-component KL sums of this minibatch
-// there.
+// there. With `tail` (its loss-partial counts are filled in here), the
+// reduction launch also runs the minibatch's scalar tail.
 zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int* perm, int row0,
                          int rows, const zl_batch* b, const zl_ppo_config* cfg, float scale,
-                         const int* guard, PassCounts* pc, float* head_kl = nullptr) {
+                         const int* guard, PassCounts* pc, float* head_kl = nullptr,
+                         zk::FinalizeArgs* tail = nullptr) {
   zl_ctx* c = p->c;
   const int La = p->actor.L, Lc = p->critic.L, A = p->A;
   zl_status s = pair_forward(c, v, p->params, px, rows, guard, p->fused_head ? La - 1 : -1);
@@ -773,7 +778,11 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     pc->nb_a = lsh.blocks;
     pc->nb_v = nbv;
   }
-  return backward_and_reduce(p, v, px, rows, guard, &pc->nsq, &pc->nsq_a, head_blocks);
+  if (tail) {
+    tail->nb_a = pc->nb_a;
+    tail->nb_v = pc->nb_v;
+  }
+  return backward_and_reduce(p, v, px, rows, guard, &pc->nsq, &pc->nsq_a, head_blocks, tail);
 }
 
 struct Plan {
@@ -946,10 +955,9 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
       const NetView v[2] = {{&p->actor, &p->ab, xa, pl.ldx, pl.ldx},
                             {&p->critic, &p->cb, xc, pl.ldxc, pl.ldxc}};
       float* hkl = head_kl && k == pl.n_mb - 1 ? p->kl_part : nullptr;
-      PassCounts pc;
-      if ((s = minibatch_pass(p, v, px, perm_e, row0, pl.mb, b, cfg, pl.pp.scale, guard, &pc, hkl)))
-        return s;
-      if (hkl) nb_kl = pc.nb_a;
+      // The step's scalar tail (statistics, log_std gradient, Adam step count,
+      // lr rule) runs as the last block of the gradient reduction; zk_adam
+      // takes the clip scales from the squared-norm partials itself.
       zk::FinalizeArgs fz{};
       fz.st = p->dstate;
       fz.gls_part = p->gls_part;
@@ -958,13 +966,12 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
       fz.sq_part = p->sq_part;
       fz.log_std = log_std;
       fz.g_logstd = p->grads + p->ls_off;
-      fz.guard = guard;
       fz.pp = pl.pp;
-      fz.nb_a = pc.nb_a;
-      fz.nb_v = pc.nb_v;
-      fz.nsq = pc.nsq;
-      fz.nsq_a = pc.nsq_a;
-      if ((s = launch(c, K_FINALIZE, 1, 1, 1, fz, 0, zk::kFinalizeThreads))) return s;
+      PassCounts pc;
+      if ((s = minibatch_pass(p, v, px, perm_e, row0, pl.mb, b, cfg, pl.pp.scale, guard, &pc, hkl,
+                              &fz)))
+        return s;
+      if (hkl) nb_kl = pc.nb_a;
       zk::AdamArgs ad{};
       ad.p = p->params;
       ad.g = p->grads;
@@ -979,6 +986,11 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
       ad.beta2 = pl.pp.beta2;
       ad.eps = pl.pp.eps;
       ad.clamp_ls = pl.pp.clamp_ls;
+      ad.sq_part = p->sq_part;
+      ad.nsq_a = pc.nsq_a;
+      ad.nsq = pc.nsq;
+      ad.clip = pl.pp.mode == 0 ? 1 : 2;
+      ad.max_grad_norm = pl.pp.max_grad_norm;
       if ((s = launch(c, K_ADAM, (unsigned)cdiv(p->nflat, 4 * kThreads), 1, 1, ad))) return s;
     }
     if (trainer_kl && !head_kl) {  // src/bin/biped_train_gpu.rs:1469-1492 (last minibatch)
@@ -1077,7 +1089,7 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
   dalloc((void**)&p->kl_part, (size_t)p->nb_cap * std::max(p->A, 1) * 4);
   // zk_reduce_all takes at least kReduceAllThreads / 64 outputs per block
   // (at most 64 split lanes).
-  p->sq_cap = 0;
+  p->sq_cap = 1;  // + the minibatch tail's slot
   const int min_per_block = zk::kReduceAllThreads / 64;
   for (const NetLayout* nl : {&p->actor, &p->critic})
     for (int l = 0; l < nl->L; ++l)

@@ -15,7 +15,7 @@
 namespace zl {
 
 const char* const kFixedNames[K_GEMM_BASE] = {
-    "zk_splitk_reduce", "zk_actor_loss",  "zk_value_loss", "zk_sumsq",       "zk_finalize",
+    "zk_splitk_reduce", "zk_actor_loss",  "zk_value_loss", "zk_sumsq",
     "zk_adam",          "zk_epoch_begin", "zk_kl",         "zk_epoch_end",   "zk_gae",
     "zk_adv_norm",      "zk_elu_backward", "zk_row_sum",   "zk_copy_rows",   "zk_sample",
     "zk_clamp",         "zk_reduce_all",  "zk_actor_loss_g64", "zk_head",       "zk_norm_set",
@@ -495,7 +495,7 @@ int reduce_all_layout(zk::ReduceSeg* segs, int nseg) {
 }
 
 zl_status launch_reduce_all(zl_ctx* c, const zk::ReduceSeg* segs, int nseg, float* sq_part,
-                            const int* guard) {
+                            const int* guard, const zk::FinalizeArgs* tail) {
   if (nseg < 1 || nseg > zk::kMaxReduceSegs)
     return fail(c, ZL_ERR_INVALID, "reduce_all: %d segments", nseg);
   zk::ReduceAllArgs a{};
@@ -504,7 +504,14 @@ zl_status launch_reduce_all(zl_ctx* c, const zk::ReduceSeg* segs, int nseg, floa
   a.sq_part = sq_part;
   a.guard = guard;
   const int blocks = reduce_all_layout(a.seg, nseg);
-  return launch(c, K_REDUCE_ALL, (unsigned)blocks, 1, 1, a, 0, zk::kReduceAllThreads);
+  a.tail_block = -1;
+  if (tail) {  // one more block, after the reduction's, with its slot sq_part[blocks]
+    a.tail = *tail;
+    a.tail.nsq = blocks;
+    a.tail_block = blocks;
+  }
+  return launch(c, K_REDUCE_ALL, (unsigned)(blocks + (tail ? 1 : 0)), 1, 1, a, 0,
+                zk::kReduceAllThreads);
 }
 
 static std::string code_object_path() {
