@@ -348,24 +348,9 @@ __device__ __forceinline__ void adam_clip_scales(const AdamArgs& p, float* s0, f
 // holding every tensor of the update, float4-vectorised.
 __device__ void adam_body(const AdamArgs& p) {
   if (p.guard && *p.guard == 0) return;
-  float lr = p.lr, bc1 = p.bc1, bc2 = p.bc2;
-  float s0 = 1.f, s1 = 1.f, s2 = 1.f;
-  if (p.st) {
-    lr = p.st->lr;
-    bc1 = p.st->bc1;
-    bc2 = p.st->bc2;
-    if (p.clip) {
-      adam_clip_scales(p, &s0, &s1, &s2);
-    } else {
-      s0 = p.st->scale[0];
-      s1 = p.st->scale[1];
-      s2 = p.st->scale[2];
-    }
-  }
-  const float b1 = p.beta1, b2 = p.beta2, eps = p.eps;
-  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+  // The element loads go first: they do not depend on the clip scales, so
+  // they are in flight while the block takes the scales.
   const long long i0 = ((long long)blockIdx.x * kThreads + threadIdx.x) * 4;
-  if (i0 >= p.n) return;
   const bool quad = i0 + 4 <= p.n &&
                     ((((uintptr_t)p.p | (uintptr_t)p.g | (uintptr_t)p.m | (uintptr_t)p.v) & 15u) == 0);
   float x[4], g[4], m[4], v[4];
@@ -388,6 +373,23 @@ __device__ void adam_body(const AdamArgs& p) {
       v[j] = in ? p.v[i0 + j] : 0.f;
     }
   }
+  float lr = p.lr, bc1 = p.bc1, bc2 = p.bc2;
+  float s0 = 1.f, s1 = 1.f, s2 = 1.f;
+  if (p.st) {
+    lr = p.st->lr;
+    bc1 = p.st->bc1;
+    bc2 = p.st->bc2;
+    if (p.clip) {
+      adam_clip_scales(p, &s0, &s1, &s2);  // every thread of the block takes part
+    } else {
+      s0 = p.st->scale[0];
+      s1 = p.st->scale[1];
+      s2 = p.st->scale[2];
+    }
+  }
+  if (i0 >= p.n) return;
+  const float b1 = p.beta1, b2 = p.beta2, eps = p.eps;
+  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const long long i = i0 + j;
