@@ -125,6 +125,8 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   // 16 * (wave / 4) ..; data-gradient columns 64 * (wave / 4) ..; weight
   // gradient columns 16 * wave ...
   const int rt = wave & 3, half = wave >> 2;
+  const int mf = 16 * half + lr;  // this lane's forward component
+  const float bias_f = mf < A ? q.b[min(mf, A - 1)] : 0.f;
 
   struct In {
     float act, lpo, adv, mo;
@@ -162,23 +164,25 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
     head_load_tile(q, r0, nr, sx);
     lds_barrier();
 
-    // Head forward: rows of tile rt, components 16 * half ...
+    // Head forward: rows of tile rt, components 16 * half ...; the k range
+    // in two interleaved chains (even and odd 16-wide chunks) added at the end.
     {
-      floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+      floatx4 acc2[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int c16 = 0; c16 < kHeadMaxHidden / 16; ++c16) {
         const float4 af = *reinterpret_cast<const float4*>(sx + (16 * rt + lr) * kHeadPitch + 16 * c16 + 4 * lg);
         const float4 bf = *reinterpret_cast<const float4*>(sw + (16 * half + lr) * kHeadPitch + 16 * c16 + 4 * lg);
+        floatx4& acc = acc2[c16 & 1];
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.x, bf.x, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.y, bf.y, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.z, bf.z, acc, 0, 0, 0);
         acc = __builtin_amdgcn_mfma_f32_16x16x4f32(af.w, bf.w, acc, 0, 0, 0);
       }
-      const int m = 16 * half + lr;
+      const int m = mf;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * rt + 4 * lg + r;
-        const float mu = m < A ? acc[r] + q.b[m] : 0.f;
+        const float mu = m < A ? (acc2[0][r] + acc2[1][r]) + bias_f : 0.f;
         sd[row * kHeadDPitch + m] = mu;
         if (m < A && row < nr) q.out[(r0 + row) * q.ldo + m] = mu;
       }
