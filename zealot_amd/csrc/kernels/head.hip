@@ -43,23 +43,31 @@ __device__ __forceinline__ float4 quad_or_zero(float4 v, bool row_ok, int c, int
 // loads are unconditional, from clamped in-range addresses (a float4 at a
 // column < H stays inside the row's 4-aligned stride), so they all issue
 // before the first wait; out-of-range values are replaced by 0 afterwards.
-__device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, int nr, float* sx) {
-  constexpr int QPR = kHeadMaxHidden / 4;  // float4 quads per row
-  constexpr int NQ = kHeadRows * QPR / kHeadThreads;
-  static_assert(kHeadRows * QPR % kHeadThreads == 0, "whole quads per thread");
+constexpr int kHeadQPR = kHeadMaxHidden / 4;                      // float4 quads per row
+constexpr int kHeadTileQuads = kHeadRows * kHeadQPR / kHeadThreads;  // per thread
+static_assert(kHeadRows * kHeadQPR % kHeadThreads == 0, "whole quads per thread");
+__device__ __forceinline__ void head_tile_issue(const HeadNet& q, long long r0, int nr,
+                                                float4 (&v)[kHeadTileQuads]) {
   const int c_last = (q.H - 1) & ~3;
   const float* base = q.x + r0 * q.ldx;  // uniform; 32-bit offsets within the tile
-  float4 v[NQ];
 #pragma unroll
-  for (int u = 0; u < NQ; ++u) {
-    const int i = threadIdx.x + kHeadThreads * u, r = i / QPR, c = (i % QPR) * 4;
+  for (int u = 0; u < kHeadTileQuads; ++u) {
+    const int i = threadIdx.x + kHeadThreads * u, r = i / kHeadQPR, c = (i % kHeadQPR) * 4;
     v[u] = *reinterpret_cast<const float4*>(base + (min(r, nr - 1) * q.ldx + min(c, c_last)));
   }
+}
+__device__ __forceinline__ void head_tile_store(const HeadNet& q, int nr, const float4 (&v)[kHeadTileQuads],
+                                                float* sx) {
 #pragma unroll
-  for (int u = 0; u < NQ; ++u) {
-    const int i = threadIdx.x + kHeadThreads * u, r = i / QPR, c = (i % QPR) * 4;
+  for (int u = 0; u < kHeadTileQuads; ++u) {
+    const int i = threadIdx.x + kHeadThreads * u, r = i / kHeadQPR, c = (i % kHeadQPR) * 4;
     *reinterpret_cast<float4*>(sx + r * kHeadPitch + c) = quad_or_zero(v[u], r < nr, c, q.H);
   }
+}
+__device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, int nr, float* sx) {
+  float4 v[kHeadTileQuads];
+  head_tile_issue(q, r0, nr, v);
+  head_tile_store(q, nr, v, sx);
 }
 
 // Sum over a row's 32 components in component order, every lane of the
@@ -328,28 +336,45 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
   float* sx = smem;
   float* sw = sx + kHeadRows * kHeadPitch;         // w[0..128), zero past H
   float* sdv = sw + kHeadMaxActions * kHeadPitch;  // dL/dvalue per row
-  float* sred = sdv + kHeadRows * kHeadDPitch;
-  const int t = threadIdx.x;
+  float* sred = sdv + kHeadRows * kHeadDPitch;     // [4][128] weight-gradient quarters, [8] wave sums
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int H = q.H;
-  for (int i = t; i < kHeadMaxHidden; i += kHeadThreads) sw[i] = i < H ? q.w[i] : 0.f;
+  // Weights, bias and the first tile's loads go out together (the loads are
+  // unconditional, from clamped in-range addresses, as in head_tile_issue).
+  const float wt = t < kHeadMaxHidden ? q.w[min(t, H - 1)] : 0.f;
   const float bias = q.b[0];
   float vacc = 0.f, dw = 0.f, db = 0.f;
   const long long ntiles = (p.rows + kHeadRows - 1) / kHeadRows;
   constexpr int U = kHeadThreads / kHeadRows;  // lanes per row (8)
-  for (int tt = 0; tt < p.tiles_per_block; ++tt) {
-    const long long tile = blockIdx.x + (long long)tt * gridDim.x;
+  static_assert(kHeadThreads == 4 * kHeadMaxHidden, "four row quarters per weight-gradient column");
+  const int row = t / U, u = t % U;
+  const int cb = blockIdx.x, cbn = p.critic_blocks;
+  if (cb >= cbn) return;  // uniform: a block of the actor's grid with no critic tile
+  // Tiles cb, cb + cbn, ...: each tile's loads are issued while the previous
+  // tile is worked on (cb < ntiles: cbn = ceil(ntiles / critic_tiles)).
+  float4 xv[kHeadTileQuads];
+  head_tile_issue(q, (long long)cb * kHeadRows,
+                  (int)min((long long)kHeadRows, p.rows - (long long)cb * kHeadRows), xv);
+  for (int tt = 0; tt < p.critic_tiles; ++tt) {
+    const long long tile = cb + (long long)tt * cbn;
     if (tile >= ntiles) break;  // uniform
     const long long r0 = tile * kHeadRows;
     const int nr = (int)min((long long)kHeadRows, p.rows - r0);
-    const int row = t / U, u = t % U;
-    float vo = 0.f, R = 0.f;  // loss inputs, in flight during the tile load
-    if (u == 0 && row < nr) {
-      const long long s = p.perm ? p.perm[p.row0 + r0 + row] : (long long)(p.row0 + r0 + row);
-      vo = p.value_old[s];
-      R = p.ret[s];
+    // Loss inputs, in flight during the value (rows past nr read the last
+    // row's; they are not used).
+    float vo = 0.f, R = 0.f;
+    if (u == 0) {
+      const long long rr = p.row0 + r0 + min(row, nr - 1);
+      const long long sidx = p.perm ? (long long)p.perm[rr] : rr;
+      vo = p.value_old[sidx];
+      R = p.ret[sidx];
     }
-    lds_barrier();
-    head_load_tile(q, r0, nr, sx);
+    if (tt == 0 && t < kHeadMaxHidden) sw[t] = t < H ? wt : 0.f;
+    lds_barrier();  // the previous tile's LDS reads are done
+    head_tile_store(q, nr, xv, sx);
+    const long long next = tile + cbn;
+    if (tt + 1 < p.critic_tiles && next < ntiles)
+      head_tile_issue(q, next * kHeadRows, (int)min((long long)kHeadRows, p.rows - next * kHeadRows), xv);
     lds_barrier();
     // value = b + sum_k w_k x_k: U lanes per row, lane u on columns u, u + U,
     // ..., then the U partial sums in lane order.
@@ -357,7 +382,7 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
       float part = 0.f;
 #pragma unroll
       for (int i = 0; i < kHeadMaxHidden / U; ++i) part += sx[row * kHeadPitch + u + U * i] * sw[u + U * i];
-      const int l0 = (t & 63) & ~(U - 1);
+      const int l0 = lane & ~(U - 1);
       float ps[U];
 #pragma unroll
       for (int i = 0; i < U; ++i) ps[i] = __shfl(part, l0 + i, 64);
@@ -390,16 +415,19 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
     lds_barrier();
     // dL/dz = (dv * w) * ELU'(x), four columns per thread (the dz rows are
     // 16-byte aligned: ldz is a multiple of 4).
-    for (int e = t; e < kHeadRows * (kHeadMaxHidden / 4); e += kHeadThreads) {
-      const int rr = e / (kHeadMaxHidden / 4), n = (e % (kHeadMaxHidden / 4)) * 4;
+#pragma unroll
+    for (int uq = 0; uq < kHeadTileQuads; ++uq) {
+      const int e = t + kHeadThreads * uq;
+      const int rr = e / kHeadQPR, n = (e % kHeadQPR) * 4;
+      const float d = sdv[rr];
+      const float4 xr = *reinterpret_cast<const float4*>(sx + rr * kHeadPitch + n);
+      const float4 wr = *reinterpret_cast<const float4*>(sw + n);
+      float4 o;
+      o.x = (d * wr.x) * elu_grad_from_act(xr.x);
+      o.y = (d * wr.y) * elu_grad_from_act(xr.y);
+      o.z = (d * wr.z) * elu_grad_from_act(xr.z);
+      o.w = (d * wr.w) * elu_grad_from_act(xr.w);
       if (rr < nr && n < H) {
-        const float d = sdv[rr];
-        const float* xr = sx + rr * kHeadPitch + n;
-        float4 o;
-        o.x = (d * sw[n]) * elu_grad_from_act(xr[0]);
-        o.y = (d * sw[n + 1]) * elu_grad_from_act(xr[1]);
-        o.z = (d * sw[n + 2]) * elu_grad_from_act(xr[2]);
-        o.w = (d * sw[n + 3]) * elu_grad_from_act(xr[3]);
         float* dst = q.dz + (r0 + rr) * q.ldz + n;
         if (n + 4 <= H) {
           *reinterpret_cast<float4*>(dst) = o;
@@ -410,17 +438,43 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
         }
       }
     }
-    if (t < kHeadMaxHidden) {
-      for (int rr = 0; rr < kHeadRows; ++rr) dw += sdv[rr] * sx[rr * kHeadPitch + t];
-    } else if (t == kHeadThreads - 1) {
-      for (int rr = 0; rr < kHeadRows; ++rr) db += sdv[rr];
+    // Weight gradient of this tile: column c = t % 128 over the row quarter
+    // t / 128 (16 rows, in row order), the quarters then added in order; the
+    // bias gradient by the last thread over all rows in row order.
+    {
+      const int c = t % kHeadMaxHidden, qr = t / kHeadMaxHidden;
+      float pq = 0.f;
+#pragma unroll
+      for (int r = 0; r < kHeadRows / 4; ++r) {
+        const int rr = (kHeadRows / 4) * qr + r;
+        pq += sdv[rr] * sx[rr * kHeadPitch + c];
+      }
+      if (t == kHeadThreads - 1)
+        for (int rr = 0; rr < kHeadRows; ++rr) db += sdv[rr];
+      sred[qr * kHeadMaxHidden + c] = pq;
+      lds_barrier();
+      if (t < kHeadMaxHidden) {
+        const float* qs = sred + t;
+        dw += ((qs[0] + qs[kHeadMaxHidden]) + qs[2 * kHeadMaxHidden]) + qs[3 * kHeadMaxHidden];
+      }
     }
   }
   const int blk = blockIdx.x;
   if (t < H) q.wpart[(long long)blk * H + t] = dw;
   if (t == kHeadThreads - 1) q.bpart[blk] = db;
-  const float tot = block_sum<kHeadThreads>(vacc, sred);
-  if (t == 0) p.vstat_part[blk] = tot;
+  // Value-loss sum: each wave's U-strided row lanes in lane order, then the
+  // waves in order.
+  float ws = 0.f;
+#pragma unroll
+  for (int i = 0; i < 64 / U; ++i) ws += __shfl(vacc, U * i, 64);
+  lds_barrier();  // the weight-gradient quarters are read
+  if (lane == 0) sred[wave] = ws;
+  lds_barrier();
+  if (t == 0) {
+    float tot = 0.f;
+    for (int w = 0; w < kHeadThreads / 64; ++w) tot += sred[w];
+    p.vstat_part[blk] = tot;
+  }
 }
 
 }  // namespace zk

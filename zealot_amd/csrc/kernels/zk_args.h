@@ -208,11 +208,15 @@ struct HeadArgs {
   const int* perm;        // sample = perm ? perm[row0 + r] : row0 + r
   float* gls_part;        // [A x blocks] log_std gradient partials
   float* astat_part;      // [2 x blocks] surrogate, kl partials
-  float* vstat_part;      // [blocks] value-loss partials
+  float* vstat_part;      // [critic_blocks] value-loss partials
   float* kl_part;         // [A x blocks] sums of (mean - mean_old)^2 per component, nullable
   const int* guard;
   long long rows;
+  // Actor: block x (of gridDim.x) takes tiles x, x + gridDim.x, ... (at most
+  // tiles_per_block). Critic: blocks x < critic_blocks take tiles x,
+  // x + critic_blocks, ... (at most critic_tiles), the others exit at once.
   int row0, A, ldact, ldmo, tiles_per_block;
+  int critic_blocks, critic_tiles;
   float clip, entropy_coef, value_coef, scale;
 };
 

@@ -111,6 +111,7 @@ inline int layout_of(bool a_kc, bool b_kc) {
 
 struct zl_ctx {
   int device = 0;
+  int cu_count = 256;  // compute units of the device (zl_init)
   hipStream_t stream = nullptr;
   hipModule_t module = nullptr;
   std::vector<hipFunction_t> fn;  // by kernel id

@@ -616,10 +616,11 @@ zl_status ensure_partials(zl_ppo* p, int rows) {
 
 // Backward of both nets for one minibatch plus the all-layer reduction with
 // the grad-norm partials; nsq / nsq_a receive the partial counts (all, actor).
-// With `tail`, the reduction launch also runs the minibatch tail.
+// With `tail`, the reduction launch also runs the minibatch tail. head_blocks
+// (actor) / critic_blocks: zk_head's partial counts per net (0: no zk_head).
 zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, int rows,
                               const int* guard, int* nsq, int* nsq_a, int head_blocks,
-                              const zk::FinalizeArgs* tail) {
+                              int critic_blocks, const zk::FinalizeArgs* tail) {
   zl_ctx* c = p->c;
   const int La = p->actor.L, Lc = p->critic.L;
   const float* top[2] = {p->ab.delta[La - 1], p->cb.delta[Lc - 1]};
@@ -647,7 +648,7 @@ zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, i
       r.cols = (int)N;
       r.ldo = nl.ldw[l];
       r.rows = (int)M;
-      r.splits = head_blocks;
+      r.splits = i == 0 ? head_blocks : critic_blocks;
     }
   }
   zk::ReduceSeg lay[zk::kMaxReduceSegs];
@@ -681,11 +682,20 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
   const int La = p->actor.L, Lc = p->critic.L, A = p->A;
   zl_status s = pair_forward(c, v, p->params, px, rows, guard, p->fused_head ? La - 1 : -1);
   if (s) return s;
-  int head_blocks = 0;
+  int head_blocks = 0, critic_blocks = 0;
   if (p->fused_head) {
     const long long tiles = cdiv(rows, zk::kHeadRows);
     const long long tpb = cdiv(tiles, zk::kHeadMaxBlocks);
     head_blocks = (int)cdiv(tiles, tpb);
+    // A critic tile is about a third of an actor tile's work: when the actor
+    // blocks leave workgroup slots free (two per CU), the critic takes its
+    // tiles in that many blocks, up to three tiles each (each tile's loads in
+    // flight during the previous one), so both nets finish in one round.
+    const int slots = 2 * c->cu_count;
+    long long ctiles = tpb;
+    if (head_blocks < slots)
+      ctiles = std::max(tpb, std::min(3 * tpb, cdiv(tiles, slots - head_blocks)));
+    critic_blocks = (int)cdiv(tiles, ctiles);
     zk::HeadArgs h{};
     for (int i = 0; i < 2; ++i) {
       const NetLayout& nl = i == 0 ? p->actor : p->critic;
@@ -719,6 +729,8 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     h.rows = rows;
     h.A = A;
     h.tiles_per_block = (int)tpb;
+    h.critic_blocks = critic_blocks;
+    h.critic_tiles = (int)ctiles;
     h.clip = cfg->clip;
     h.entropy_coef = cfg->entropy_coef;
     h.value_coef = cfg->value_coef;
@@ -729,7 +741,8 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     h.kl_part = head_kl;
     h.guard = guard;
     if ((s = launch(c, K_HEAD, (unsigned)head_blocks, 1, 2, h, 0, zk::kHeadThreads))) return s;
-    pc->nb_a = pc->nb_v = head_blocks;
+    pc->nb_a = head_blocks;
+    pc->nb_v = critic_blocks;
   } else {
     const LossShape lsh = actor_loss_shape(rows, A);
     zk::ActorLossArgs al{};
@@ -782,7 +795,8 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     tail->nb_a = pc->nb_a;
     tail->nb_v = pc->nb_v;
   }
-  return backward_and_reduce(p, v, px, rows, guard, &pc->nsq, &pc->nsq_a, head_blocks, tail);
+  return backward_and_reduce(p, v, px, rows, guard, &pc->nsq, &pc->nsq_a, head_blocks, critic_blocks,
+                             tail);
 }
 
 struct Plan {

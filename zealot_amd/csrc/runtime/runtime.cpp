@@ -708,6 +708,7 @@ zl_status zl_init(int device, zl_ctx** out) {
                 prop.gcnArchName);
   zl_ctx* c = new zl_ctx();
   c->device = device;
+  c->cu_count = prop.multiProcessorCount;
   std::string path = code_object_path();
   e = hipModuleLoad(&c->module, path.c_str());
   if (e != hipSuccess) {
