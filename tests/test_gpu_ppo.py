@@ -185,6 +185,42 @@ def test_minibatch_grads_head_variants(ctx, ad, cd):
     gac.close()
 
 
+@pytest.mark.parametrize("n,shuffled", [(3001, False), (24576, False), (33000, True), (40000, False)])
+def test_head_tile_schedules_match_unfused(ctx, n, shuffled):
+    """zk_head's tile schedules against the separate output-layer GEMMs and
+    loss kernels (ZL_FUSED_HEAD=0) on the same minibatch: a ragged last tile
+    (3,001 rows), one actor tile per block with three critic tiles per block
+    (24,576), and two actor tiles per block with three and four critic tiles
+    per block (33,000 shuffled, 40,000)."""
+    ad, cd = [40, 256, 128, 12], [40, 256, 128, 1]
+    g = np.random.default_rng(23)
+    actor = synth.kaiming_uniform_net(g, ad, 0.1)
+    critic = synth.kaiming_uniform_net(g, cd, 0.1)
+    batch, log_std = make_batch(n, ad, cd, actor, critic, seed=9)
+    move_off_branch_boundaries(batch, ad, cd, actor, critic, log_std)
+    db = DeviceBatch(ctx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
+                     batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
+    perm = ctx.to_device(g.permutation(n).astype(np.int32)) if shuffled else None
+    out = []
+    for fused in (True, False):
+        if not fused:
+            os.environ["ZL_FUSED_HEAD"] = "0"
+        try:
+            gac = GpuActorCritic(ctx, ad, cd, n)
+        finally:
+            os.environ.pop("ZL_FUSED_HEAD", None)
+        gac.set_params(actor, critic, log_std, 1e-3)
+        out.append(gac.minibatch_grads(db, PpoConfig(entropy_coef=0.01), 0, n, perm=perm))
+        gac.close()
+    (fa, fc, fl, fs), (ua, uc, ul, us) = out
+    e = (per_tensor_err(ad, fa, ua), per_tensor_err(cd, fc, uc), rel_amax(fl, ul))
+    print(f"[gpu] head schedules n={n} shuffled={shuffled}: fused vs unfused actor {e[0]:.2e} "
+          f"critic {e[1]:.2e} log_std {e[2]:.2e}", flush=True)
+    assert max(e) <= TOL
+    for key in ("surrogate", "value_loss", "kl"):
+        assert abs(fs[key] - us[key]) <= 1e-5 * max(1.0, abs(us[key])), key
+
+
 def test_action_dim_limit(ctx):
     """zl_ppo_create refuses more than 48 actions, its stated maximum (the
     48-action net above is accepted)."""
