@@ -234,7 +234,7 @@ __device__ void minibatch_tail_body(const FinalizeArgs& p) {
   const int A = p.pp.A;
   const int nq = kQ + A;
   const int grp = t >> 5, gln = t & 31;
-  constexpr int kGroups = kFinalizeThreads / 32;
+  constexpr int kGroups = kReduceAllThreads / 32;
   for (int j = grp; j < nq; j += kGroups) {
     const float* ptr;
     int n;

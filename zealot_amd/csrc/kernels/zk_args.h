@@ -7,14 +7,15 @@
 
 namespace zk {
 
-// The minibatch tail (the extra last block of zk_reduce_all) and
 // zk_epoch_end: one block of 16 wavefronts (32 lane groups, one quantity
 // each at a time).
 constexpr int kFinalizeThreads = 1024;
-// Block sizes of zk_actor_loss (32 lane groups) and zk_reduce_all.
+// Block sizes of zk_actor_loss (32 lane groups) and zk_reduce_all (whose
+// extra last block runs the minibatch tail with kReduceAllThreads / 32 lane
+// groups).
 constexpr int kLossThreads = 1024;
-constexpr int kReduceAllThreads = 1024;
-static_assert(kFinalizeThreads == kReduceAllThreads, "the tail runs as a zk_reduce_all block");
+constexpr int kReduceAllThreads = 256;
+static_assert(kReduceAllThreads % 64 == 0, "whole wavefronts");
 
 enum EpiMode : int {
   kEpiStore = 0,    // C = acc
