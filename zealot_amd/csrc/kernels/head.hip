@@ -72,21 +72,28 @@ __device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, i
 
 // Sum over a row's 32 components in component order, every lane of the
 // 32-lane group getting the result: lane k stores its term in the row's LDS
-// slot k (components >= A hold 0, and adding 0 changes no sum), then each
-// lane reads the row back as 8 broadcast float4 loads. LDS instructions of
-// one wavefront execute in order, so no barrier is needed.
+// slot k (components >= A hold 0, and adding 0 changes no sum), the group's
+// first lane reads the row back as 8 float4 loads and adds them in order, and
+// the two groups' sums (lanes 0 and 32 of the wavefront) are broadcast with
+// v_readlane. LDS instructions of one wavefront execute in order, so no
+// barrier is needed; one reading lane per group instead of 32 keeps the LDS
+// traffic of the losses at 1/32.
 __device__ __forceinline__ float row_sum_ordered(float* srow, int k, float term) {
   srow[k] = term;
   float s = 0.f;
+  if (k == 0) {
 #pragma unroll
-  for (int c = 0; c < kHeadMaxActions / 4; ++c) {
-    const float4 v = *reinterpret_cast<const float4*>(srow + 4 * c);
-    s += v.x;
-    s += v.y;
-    s += v.z;
-    s += v.w;
+    for (int c = 0; c < kHeadMaxActions / 4; ++c) {
+      const float4 v = *reinterpret_cast<const float4*>(srow + 4 * c);
+      s += v.x;
+      s += v.y;
+      s += v.z;
+      s += v.w;
+    }
   }
-  return s;
+  const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 0));
+  const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), 32));
+  return (threadIdx.x & 32) ? s1 : s0;
 }
 
 __device__ void head_actor(const HeadArgs& p, float* smem) {
@@ -227,7 +234,13 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
         sacc += surr * p.scale;
         if (p.mean_old) {
           const float y = (mu - in[j].mo) * inv_sd;
-          kacc += row_sum_ordered(srow, k, on ? 0.5f * (y * y) : 0.f) * p.scale;
+          // The mean-only KL (ActorCritic::kl, ppo.rs:327-334) is a statistic:
+          // a fixed butterfly over the group is enough (every lane ends with
+          // the same bits: each step adds two equal-valued partners).
+          float kt = on ? 0.5f * (y * y) : 0.f;
+#pragma unroll
+          for (int m = 16; m > 0; m >>= 1) kt = kt + __shfl_xor(kt, m, 32);
+          kacc += kt * p.scale;
           if (p.kl_part && on) {
             const float dmu = mu - in[j].mo;
             klacc += dmu * dmu;
