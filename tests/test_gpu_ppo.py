@@ -190,8 +190,8 @@ def test_head_tile_schedules_match_unfused(ctx, n, shuffled):
     """zk_head's tile schedules against the separate output-layer GEMMs and
     loss kernels (ZL_FUSED_HEAD=0) on the same minibatch: a ragged last tile
     (3,001 rows), one actor tile per block with three critic tiles per block
-    (24,576), and two actor tiles per block with three and four critic tiles
-    per block (33,000 shuffled, 40,000)."""
+    (24,576), and two tiles per block for both nets (33,000 shuffled,
+    40,000)."""
     ad, cd = [40, 256, 128, 12], [40, 256, 128, 1]
     g = np.random.default_rng(23)
     actor = synth.kaiming_uniform_net(g, ad, 0.1)

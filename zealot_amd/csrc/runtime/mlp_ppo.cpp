@@ -688,13 +688,13 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     const long long tpb = cdiv(tiles, zk::kHeadMaxBlocks);
     head_blocks = (int)cdiv(tiles, tpb);
     // A critic tile is about a third of an actor tile's work: when the actor
-    // blocks leave workgroup slots free (two per CU), the critic takes its
-    // tiles in that many blocks, up to three tiles each (each tile's loads in
-    // flight during the previous one), so both nets finish in one round.
+    // takes one tile per block and leaves workgroup slots free (two per CU),
+    // the critic takes its tiles in that many blocks, up to three tiles each
+    // (each tile's loads in flight during the previous one), so both nets
+    // finish in one round; otherwise it is laid out like the actor.
     const int slots = 2 * c->cu_count;
     long long ctiles = tpb;
-    if (head_blocks < slots)
-      ctiles = std::max(tpb, std::min(3 * tpb, cdiv(tiles, slots - head_blocks)));
+    if (tpb == 1 && head_blocks < slots) ctiles = std::min<long long>(3, cdiv(tiles, slots - head_blocks));
     critic_blocks = (int)cdiv(tiles, ctiles);
     zk::HeadArgs h{};
     for (int i = 0; i < 2; ++i) {
