@@ -342,6 +342,41 @@ def test_update_actor_critic_semantics(ctx, rule):
     gac.close()
 
 
+def test_update_actor_critic_consecutive(ctx):
+    """Three ActorCritic::update calls in a row: the second takes the shuffle
+    orders prepared while the first ran (its Adam step count is known), the
+    third changes the minibatch count, so the prepared orders no longer match
+    and are computed again. Parameters, lr and step counts against three
+    oracle updates."""
+    actor, critic, log_std, batch = _well_posed_problem(43)
+    lr0 = 1e-3
+    ac = zo.ActorCritic(SMALL_A, SMALL_C, 1.0, lr0, 1)
+    ac.set(actor, critic, log_std, lr0)
+    n = batch["obs"].shape[0]
+    gac = GpuActorCritic(ctx, SMALL_A, SMALL_C, n // 4)
+    gac.set_params(actor, critic, log_std, lr0)
+    for k, mbs in enumerate((4, 4, 8)):
+        cfg_o = zo.PpoCfg(0.99, 0.95, WELL_POSED_CLIP, 0.01, 1.0, 2, mbs, 1.0, 0.01, 1e-5, 1e-2, 0)
+        ac.update({key: v.copy() for key, v in batch.items()}, cfg_o, nthreads=NTHREADS,
+                  normalize_obs=False)
+        db = DeviceBatch(ctx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
+                         batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
+        gac.update(db, PpoConfig(epochs=2, minibatches=mbs, clip=WELL_POSED_CLIP, adaptive_lr=False,
+                                 shuffle=True, normalize_adv=True, clamp_log_std=True))
+    ao, co, lso, lro, to = ac.get()
+    ag, cg, lsg, lrg = gac.get_params()
+    t, _ = gac.counters()
+    steps = 2 * (4 + 4 + 8)
+    reps = dict(actor=_param_delta_report(actor, ag, ao, lr0, steps),
+                critic=_param_delta_report(critic, cg, co, lr0, steps),
+                log_std=_param_delta_report(log_std, lsg, lso, lr0, steps))
+    print(f"[gpu] AC consecutive updates: {reps}", flush=True)
+    assert t == to == steps
+    assert lrg == pytest.approx(lro, rel=1e-6)
+    _assert_tight(reps)
+    gac.close()
+
+
 def test_update_actor_critic_full_size(ctx):
     """ActorCritic::update at the headline shapes: 98,304 rows, 5 epochs x 4
     shuffled minibatches of 24,576 rows (the observation gather fused into the

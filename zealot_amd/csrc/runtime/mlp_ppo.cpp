@@ -567,7 +567,19 @@ struct zl_ppo {
   size_t cobs_pad_floats = 0;
   int* perm = nullptr;
   size_t perm_cap = 0;
-  std::vector<int> perm_host;
+  // Shuffle orders of ActorCritic::update in pinned host memory, two
+  // buffers: one uploaded for the update in flight, the other filled with the
+  // next update's orders (its Adam step count is known: one step per
+  // minibatch) while the device runs this one. A buffer is used only if its
+  // key matches the call.
+  struct ShuffleBuf {
+    int* h = nullptr;
+    size_t cap = 0;  // ints
+    long long n = -1;
+    int epochs = 0, minibatches = 0, t = -1;
+  };
+  ShuffleBuf shuf[2];
+  int shuf_cur = 0;
   zk::DevState hstate{};
   // Bumped whenever a device buffer of this handle is reallocated: a captured
   // graph is only replayed while every buffer it references is still alive.
@@ -660,6 +672,41 @@ zl_status backward_and_reduce(zl_ppo* p, const NetView v[2], const int* permx, i
   *nsq = blocks;
   *nsq_a = lay[La].blk0;
   return launch_reduce_all(c, segs, La + Lc, p->sq_part, guard, tail);
+}
+
+// Per-epoch Fisher-Yates orders of ActorCritic::update for Adam step count t
+// (zealot-rl/src/ppo.rs:357-363: Lcg::new(t_logstd + 1), and t_logstd
+// advances once per minibatch, so epoch e starts at t + e * minibatches),
+// into sb (pinned, grown as needed; the allocation is the only failure).
+static hipError_t shuffle_orders(zl_ppo::ShuffleBuf& sb, long long n, int epochs, int minibatches,
+                                 int t) {
+  const size_t need = (size_t)epochs * (size_t)n;
+  sb.n = -1;
+  if (sb.cap < need) {
+    if (sb.h) hipHostFree(sb.h);
+    sb.h = nullptr;
+    sb.cap = 0;
+    hipError_t e = hipHostMalloc((void**)&sb.h, std::max<size_t>(need, 1) * 4, hipHostMallocDefault);
+    if (e != hipSuccess) {
+      sb.h = nullptr;
+      return e;
+    }
+    sb.cap = need;
+  }
+  for (int e = 0; e < epochs; ++e) {
+    int* order = sb.h + (size_t)e * n;
+    for (long long i = 0; i < n; ++i) order[i] = (int)i;
+    Lcg sh((uint64_t)(t + e * minibatches) + 1);
+    for (long long i = n - 1; i >= 1; --i) {
+      size_t j = (size_t)(sh.unit() * (float)(i + 1));
+      std::swap(order[i], order[std::min<long long>((long long)j, i)]);
+    }
+  }
+  sb.n = n;
+  sb.epochs = epochs;
+  sb.minibatches = minibatches;
+  sb.t = t;
+  return hipSuccess;
 }
 
 // Loss-partial and grad-norm-partial counts of one minibatch pass.
@@ -1140,6 +1187,8 @@ void zl_ppo_destroy(zl_ppo* p) {
     if (b) hipFree(b);
   for (float* b : p->stg)
     if (b) hipFree(b);
+  for (zl_ppo::ShuffleBuf& sb : p->shuf)
+    if (sb.h) hipHostFree(sb.h);
   delete p;
 }
 
@@ -1244,17 +1293,13 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
     size_t cap = p->perm_cap * 4;
     if ((s = grow(p, (void**)&p->perm, &cap, (size_t)pl.epochs * pl.n * 4 + 4))) return s;
     p->perm_cap = cap / 4;
-    // Per-epoch Fisher-Yates with Lcg::new(t_logstd + 1) (zealot-rl/src/ppo.rs:357-363);
-    // t_logstd advances once per minibatch, so epoch e starts at t + e*minibatches.
-    p->perm_host.assign((size_t)pl.epochs * pl.n, 0);
-    for (int e = 0; e < pl.epochs; ++e) {
-      int* order = p->perm_host.data() + (size_t)e * pl.n;
-      for (long long i = 0; i < pl.n; ++i) order[i] = (int)i;
-      Lcg sh((uint64_t)(p->hstate.t + e * cfg->minibatches) + 1);
-      for (long long i = pl.n - 1; i >= 1; --i) {
-        size_t j = (size_t)(sh.unit() * (float)(i + 1));
-        std::swap(order[i], order[std::min<long long>((long long)j, i)]);
-      }
+    zl_ppo::ShuffleBuf& sb = p->shuf[p->shuf_cur];
+    if (!(sb.n == pl.n && sb.epochs == pl.epochs && sb.minibatches == cfg->minibatches &&
+          sb.t == p->hstate.t)) {
+      hipError_t e = shuffle_orders(sb, pl.n, pl.epochs, cfg->minibatches, p->hstate.t);
+      if (e != hipSuccess)
+        return fail(c, ZL_ERR_HIP, "zl_ppo_update: hipHostMalloc (shuffle orders): %s",
+                    hipGetErrorString(e));
     }
   }
   zk::PpoParams& pp = pl.pp;
@@ -1343,12 +1388,23 @@ zl_status zl_ppo_update(zl_ppo* p, const zl_batch* b, const zl_ppo_config* cfg,
   ZL_HIP(c, hipMemcpyAsync(p->ls_old, p->params + p->ls_off, (size_t)p->A * 4,
                            hipMemcpyDeviceToDevice, c->stream));
   if (pl.shuffle)
-    ZL_HIP(c, hipMemcpyAsync(p->perm, p->perm_host.data(), p->perm_host.size() * 4,
+    ZL_HIP(c, hipMemcpyAsync(p->perm, p->shuf[p->shuf_cur].h, (size_t)pl.epochs * pl.n * 4,
                              hipMemcpyHostToDevice, c->stream));
   if (eager) {
     if ((s = enqueue_update(p, cfg, pl))) return s;
   } else {
     ZL_HIP(c, hipGraphLaunch(p->gexec, c->stream));
+  }
+  if (pl.shuffle) {
+    // The next update's orders while the device runs this one (every
+    // minibatch of every epoch takes one Adam step under these semantics).
+    // The other buffer's last upload finished with the previous call.
+    p->shuf_cur ^= 1;
+    zl_ppo::ShuffleBuf& nb = p->shuf[p->shuf_cur];
+    // On an allocation failure the buffer's key stays unset and the next
+    // call computes its orders itself.
+    (void)shuffle_orders(nb, pl.n, pl.epochs, cfg->minibatches,
+                         p->hstate.t + pl.epochs * cfg->minibatches);
   }
   ZL_HIP(c, hipMemcpyAsync(&st, p->dstate, sizeof(st), hipMemcpyDeviceToHost, c->stream));
   ZL_HIP(c, hipStreamSynchronize(c->stream));
