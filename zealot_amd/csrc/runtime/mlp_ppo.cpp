@@ -81,14 +81,14 @@ struct NetLayout {
 };
 
 // Row alignment of an update's layer-0 weights and staged observations: a
-// whole 32-wide GEMM k-tile when that adds at most 1/16 to the row (123 -> 128
-// features), else 4. The staged rows are zero past the features and so are
+// whole 32-wide GEMM k-tile when that adds at most 1/8 to the row (123 -> 128
+// or 265 -> 288 features), else 4. The staged rows are zero past the features and so are
 // the weights' padding columns, so the layer-0 GEMMs can run over the padded
 // width (the forward's K, the weight gradient's N) and take the exact-fit
 // kernels without changing a result: the extra terms are 0 * 0.
 constexpr int kInputTile = 32;
 inline int input_align(int d) {
-  return round_up(d, kInputTile) * 16 <= (long long)d * 17 ? kInputTile : 4;
+  return round_up(d, kInputTile) * 8 <= (long long)d * 9 ? kInputTile : 4;
 }
 
 // Per-row activation and delta buffers of one MLP for up to `rows` rows.

@@ -325,6 +325,15 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
     zl_status s = plan_gemm(c, *live[i], P[i]);
     if (s) return s;
   }
+  // Only problems of one shape share a launch: a pair of different shapes
+  // (the actor's and the critic's layer when the nets differ in width) runs
+  // as two launches, which measured faster than one grid sized for the
+  // larger problem (e.g. 24576 x 256 x 256 with 24576 x 512 x 256 data
+  // gradients: 127 us paired, 38 + 71 us apart).
+  if (nl == 2 && (live[0]->M != live[1]->M || live[0]->N != live[1]->N || live[0]->K != live[1]->K)) {
+    zl_status s = run_gemm_batch(c, live[0], 1);
+    return s ? s : run_gemm_batch(c, live[1], 1);
+  }
   // A pair whose members differ only in exact fit runs as one launch of
   // the general form.
   if (nl == 2 && P[0].kid != P[1].kid && inexact_form(P[0].kid) == inexact_form(P[1].kid))
