@@ -19,7 +19,7 @@ import pytest
 import np_ref
 from conftest import rel_amax
 from oracle import zl_oracle as zo
-from zealot_amd import ZealotError, synth
+from zealot_amd import Context, ZealotError, synth
 from zealot_amd.rl import DeviceBatch, GpuActorCritic, PpoConfig
 
 pytestmark = pytest.mark.gpu
@@ -219,6 +219,53 @@ def test_head_tile_schedules_match_unfused(ctx, n, shuffled):
     assert max(e) <= TOL
     for key in ("surrogate", "value_loss", "kl"):
         assert abs(fs[key] - us[key]) <= 1e-5 * max(1.0, abs(us[key])), key
+
+
+@pytest.mark.parametrize("shuffled", [False, True])
+def test_backward_merged_matches_separate(ctx, shuffled):
+    """A layer's weight- and data-gradient GEMMs as one zk_gemm_bwd_* launch
+    against the same GEMMs as two launches (ZL_MERGED_BWD=0): the 512 -> 256
+    layer takes the 128 x 128 weight-gradient form, the 256 -> 128 layer the
+    64 x 128 one, and both runs are bit-identical — the minibatch gradients
+    and a whole update (2 epochs x 2 minibatches of 3,072 rows)."""
+    ad, cd = [64, 512, 256, 128, 12], [64, 512, 256, 128, 1]
+    n = 6144
+    g = np.random.default_rng(31)
+    actor = synth.kaiming_uniform_net(g, ad, 0.1)
+    critic = synth.kaiming_uniform_net(g, cd, 0.1)
+    batch, log_std = make_batch(n, ad, cd, actor, critic, seed=12)
+    order = g.permutation(n).astype(np.int32)
+    out = []
+    for merged in (True, False):
+        # The switch is read when a context is created: the separate run
+        # gets a context of its own.
+        if not merged:
+            os.environ["ZL_MERGED_BWD"] = "0"
+        try:
+            cx = ctx if merged else Context(0)
+        finally:
+            os.environ.pop("ZL_MERGED_BWD", None)
+        # A fresh batch per run: the update normalises its advantages in place.
+        db = DeviceBatch(cx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
+                         batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
+        perm = cx.to_device(order) if shuffled else None
+        gac = GpuActorCritic(cx, ad, cd, n)
+        gac.set_params(actor, critic, log_std, 1e-3)
+        grads = gac.minibatch_grads(db, PpoConfig(entropy_coef=0.01), 0, n, perm=perm)
+        gac.update(db, PpoConfig(epochs=2, minibatches=2))
+        out.append((grads, gac.get_params()))
+        gac.close()
+        del db, perm
+        if not merged:
+            cx.close()
+    (gm, pm), (gs, ps) = out
+    for x, y in zip(gm[:3], gs[:3]):
+        assert np.array_equal(x, y)
+    for key in ("surrogate", "value_loss", "kl"):
+        assert gm[3][key] == gs[3][key], key
+    for x, y in zip(pm[:3], ps[:3]):
+        assert np.array_equal(x, y)
+    print(f"[gpu] merged backward shuffled={shuffled}: gradients and update bit-identical", flush=True)
 
 
 def test_action_dim_limit(ctx):

@@ -245,25 +245,39 @@ struct Tile {
 struct BlockTile {
   int mt, nt, z;
 };
-__device__ __forceinline__ BlockTile block_tile() {
-  const int ntl = (int)gridDim.y, ntiles = (int)gridDim.x * ntl, nz = (int)gridDim.z;
-  const int b = blockIdx.x + gridDim.x * blockIdx.y;
+// Tile of the block with linear dispatch index g (x fastest, then y, then z)
+// in a gx x ntl x nz grid.
+__device__ __forceinline__ BlockTile block_tile_of(int g, int gx, int ntl, int nz) {
+  const int ntiles = gx * ntl;
   if (nz % 8 == 0) {
-    const long long g = b + (long long)ntiles * blockIdx.z;
-    const long long k = g / 8;
-    const int t = (int)(k % ntiles);
-    return {t / ntl, t % ntl, (int)(g % 8) + 8 * (int)(k / ntiles)};
+    const int k = g / 8;
+    const int t = k % ntiles;
+    return {t / ntl, t % ntl, g % 8 + 8 * (k / ntiles)};
   }
+  const int b = g % ntiles;
   if (ntiles % 8 == 0) {
     const int t = (b % 8) * (ntiles / 8) + b / 8;
-    return {t / ntl, t % ntl, (int)blockIdx.z};
+    return {t / ntl, t % ntl, g / ntiles};
   }
-  return {(int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z};
+  return {b % gx, b / gx, g / ntiles};
+}
+__device__ __forceinline__ BlockTile block_tile() {
+  const int g = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  return block_tile_of(g, (int)gridDim.x, (int)gridDim.y, (int)gridDim.z);
+}
+
+// LDS floats of one gemm_body instantiation: both operand tiles, double
+// buffered.
+template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, bool VEC, bool EXACT = false>
+constexpr int gemm_smem_floats() {
+  return 2 * (Tile<BM, AK, BK, 64 * WM * WN, VEC, EXACT>::SIZE +
+              Tile<BN, BKC, BK, 64 * WM * WN, VEC, EXACT>::SIZE);
 }
 
 template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, bool VEC,
           bool YPRE = false, bool EXACT = false>
-__device__ __forceinline__ void gemm_body(const GemmArgs& p, int split, int mt, int nt) {
+__device__ __forceinline__ void gemm_body(float* __restrict__ smem, const GemmArgs& p, int split,
+                                          int mt, int nt) {
   constexpr int NT = 64 * WM * WN;
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
@@ -272,11 +286,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int split, int mt, 
   constexpr int RSG = NT / BM >= 1 ? NT / BM : 1;  // threads per A row in the row sums
   using TA = Tile<BM, AK, BK, NT, VEC, EXACT>;
   using TB = Tile<BN, BKC, BK, NT, VEC, EXACT>;
-  constexpr int SMEM = 2 * (TA::SIZE + TB::SIZE);
-  static_assert(SMEM >= NT, "LDS holds one float per thread for the row sums");
-  // One allocation: [A buf 0][A buf 1][B buf 0][B buf 1], reused after the
-  // k-loop for the row-sum exchange.
-  __shared__ __align__(16) float smem[SMEM];
+  static_assert(gemm_smem_floats<AK, BKC, BM, BN, BK, WM, WN, VEC, EXACT>() >= NT,
+                "LDS holds one float per thread for the row sums");
+  // smem (the caller's LDS, gemm_smem_floats of it, 16-byte aligned):
+  // [A buf 0][A buf 1][B buf 0][B buf 1], reused after the k-loop for the
+  // row-sum exchange.
   auto sA = [&](int b) { return smem + b * TA::SIZE; };
   auto sB = [&](int b) { return smem + 2 * TA::SIZE + b * TB::SIZE; };
 
@@ -679,13 +693,14 @@ __device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
 
 }  // namespace zk
 
-#define ZK_GEMM_X(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC, EXACT)                            \
-  extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(zk::GemmBatch b) {      \
-    const zk::BlockTile bt = zk::block_tile();                                            \
-    const int prob = bt.z / b.zper;                                                       \
-    if (prob >= b.count) return;                                                          \
-    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, VEC, false, EXACT>(b.g[prob], bt.z % b.zper, bt.mt, \
-                                                                 bt.nt);                  \
+#define ZK_GEMM_X(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC, EXACT)                               \
+  extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(zk::GemmBatch b) {         \
+    __shared__ __align__(16) float smem[zk::gemm_smem_floats<AK, BKC, BM, BN, BK, WM, WN, VEC, EXACT>()]; \
+    const zk::BlockTile bt = zk::block_tile();                                               \
+    const int prob = bt.z / b.zper;                                                          \
+    if (prob >= b.count) return;                                                             \
+    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, VEC, false, EXACT>(smem, b.g[prob], bt.z % b.zper, \
+                                                                 bt.mt, bt.nt);              \
   }
 #define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC) \
   ZK_GEMM_X(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC, false)
@@ -704,17 +719,20 @@ ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, true)
 // so that two 8-wave blocks stay resident per CU.
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
 void zk_gemm_ak_bn_96x128x32_w24_dg(zk::GemmBatch b) {
+  __shared__ __align__(16) float smem[zk::gemm_smem_floats<true, false, 96, 128, 32, 2, 4, true>()];
   const zk::BlockTile bt = zk::block_tile();
   const int prob = bt.z / b.zper;
   if (prob >= b.count) return;
-  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true>(b.g[prob], bt.z % b.zper, bt.mt, bt.nt);
+  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true>(smem, b.g[prob], bt.z % b.zper, bt.mt, bt.nt);
 }
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
 void zk_gemm_ak_bn_96x128x32_w24_dg_x(zk::GemmBatch b) {
+  __shared__ __align__(16) float smem[zk::gemm_smem_floats<true, false, 96, 128, 32, 2, 4, true, true>()];
   const zk::BlockTile bt = zk::block_tile();
   const int prob = bt.z / b.zper;
   if (prob >= b.count) return;
-  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(b.g[prob], bt.z % b.zper, bt.mt, bt.nt);
+  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.g[prob], bt.z % b.zper, bt.mt,
+                                                                 bt.nt);
 }
 // Exact-fit forms (suffix _x) of the update's layer-GEMM variants.
 ZK_GEMM_X(zk_gemm_ak_bk_96x128x32_w24_x, true, true, 96, 128, 32, 2, 4, true, true)
@@ -728,6 +746,38 @@ ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22_s, true, true, 64, 128, 16, 2, 2, false)
 ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22_s, true, false, 64, 128, 16, 2, 2, false)
 ZK_GEMM(zk_gemm_am_bn_64x128x16_w22_s, false, false, 64, 128, 16, 2, 2, false)
 ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, false)
+
+// One layer's backward as one launch (GemmPair): the split-K weight-gradient
+// GEMMs of both nets (exact-fit am_bn tiles, blocks [0, w grid)) and their
+// data-gradient GEMMs with the ELU' epilogue (exact-fit 96 x 128 ak_bn tiles,
+// the blocks after). The two parts read the same dL/dz and write disjoint
+// outputs; one grid lets data-gradient tiles start on the CUs that the
+// weight-gradient slices leave, instead of a second launch after the first
+// one's last block. The parts share one LDS allocation, the larger of the two.
+#define ZK_GEMM_BWD(NAME, WBM)                                                                    \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))           \
+  void NAME(zk::GemmPair b) {                                                                     \
+    constexpr int SW = zk::gemm_smem_floats<false, false, WBM, 128, 32, 2, 4, true, true>();      \
+    constexpr int SD = zk::gemm_smem_floats<true, false, 96, 128, 32, 2, 4, true, true>();        \
+    __shared__ __align__(16) float smem[SW > SD ? SW : SD];                                       \
+    const int nw = b.wgx * b.wgy * b.wgz;                                                          \
+    const int g = (int)blockIdx.x;                                                                 \
+    if (g < nw) {                                                                                  \
+      const zk::BlockTile bt = zk::block_tile_of(g, b.wgx, b.wgy, b.wgz);                          \
+      const int prob = bt.z / b.w.zper;                                                            \
+      if (prob >= b.w.count) return;                                                               \
+      zk::gemm_body<false, false, WBM, 128, 32, 2, 4, true, false, true>(smem, b.w.g[prob],         \
+                                                                        bt.z % b.w.zper, bt.mt, bt.nt); \
+    } else {                                                                                       \
+      const zk::BlockTile bt = zk::block_tile_of(g - nw, b.dgx, b.dgy, b.dgz);                     \
+      const int prob = bt.z / b.d.zper;                                                            \
+      if (prob >= b.d.count) return;                                                               \
+      zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.d.g[prob],            \
+                                                                     bt.z % b.d.zper, bt.mt, bt.nt); \
+    }                                                                                              \
+  }
+ZK_GEMM_BWD(zk_gemm_bwd_128x128_dg_x, 128)
+ZK_GEMM_BWD(zk_gemm_bwd_64x128_dg_x, 64)
 
 extern "C" __global__ __launch_bounds__(256) void zk_splitk_reduce(zk::SplitReduceArgs p) {
   zk::splitk_reduce_body(p);

@@ -56,6 +56,15 @@ struct GemmBatch {
   int zper;
 };
 
+// A layer's weight-gradient batch and data-gradient batch as one launch of
+// wgx*wgy*wgz + dgx*dgy*dgz blocks: the weight-gradient blocks first, each
+// part's blocks mapped onto its own grid.
+struct GemmPair {
+  GemmBatch w, d;
+  int wgx, wgy, wgz;
+  int dgx, dgy, dgz;
+};
+
 struct SplitReduceArgs {
   const float* part;     // [splits x rows_mn x cols] dense partials
   float* out;            // element (r, c) at out[r * ldo + c]

@@ -45,6 +45,8 @@ enum KernelId : int {
   K_SUMSQ_MULTI,
   K_CLIP_SCALE,
   K_ADAM_MULTI,
+  K_GEMM_BWD_128,
+  K_GEMM_BWD_64,
   K_GEMM_BASE
 };
 
@@ -149,6 +151,9 @@ struct zl_ctx {
   // off) and the block count their row slices aim at (ZL_NARROW_TARGET).
   bool narrow = true;
   int narrow_target = 256;
+  // A layer's weight- and data-gradient GEMMs as one launch where a merged
+  // kernel covers their variants (ZL_MERGED_BWD=0 runs them as two).
+  bool merged_bwd = true;
   // Device address of the allocation-free scratch array on this context's
   // device (zl_grad_clip_scale_noalloc), set at zl_init.
   float* noalloc_scratch = nullptr;
@@ -233,6 +238,11 @@ zl_status run_gemm(zl_ctx* c, const GemmDesc& d);
 // One launch for n (1 or 2) problems that pick the same variant (else n
 // launches); problems that split K over slices need caller scratch when n > 1.
 zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n);
+// A layer's backward: the weight-gradient batch w and the data-gradient
+// batch d (nd may be 0), as one zk_gemm_bwd_* launch when both are single
+// exact-fit launches of the variants it covers, else as run_gemm_batch(w)
+// then run_gemm_batch(d).
+zl_status run_gemm_bwd(zl_ctx* c, const GemmDesc* w, int nw, const GemmDesc* d, int nd);
 // Block layout of zk_reduce_all over `segs` (fills lanes / blk0 / nqb / nrb);
 // returns the block count (= number of sum-of-squares partials).
 int reduce_all_layout(zk::ReduceSeg* segs, int nseg);

@@ -336,8 +336,7 @@ static zl_status pair_backward(zl_ctx* c, const NetView v[2], const float* param
     }
     zl_status s = ZL_OK;
     if (paired) {
-      s = run_gemm_batch(c, w, nw);
-      if (!s && nd) s = run_gemm_batch(c, d, nd);
+      s = run_gemm_bwd(c, w, nw, d, nd);
     } else {
       for (int j = 0; j < nw && !s; ++j) s = run_gemm_batch(c, &w[j], 1);
       for (int j = 0; j < nd && !s; ++j) s = run_gemm_batch(c, &d[j], 1);

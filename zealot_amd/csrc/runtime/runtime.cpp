@@ -22,6 +22,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_norm_apply",
     "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
     "zk_stage",         "zk_sumsq_multi", "zk_clip_scale",  "zk_adam_multi",
+    "zk_gemm_bwd_128x128_dg_x", "zk_gemm_bwd_64x128_dg_x",
 };
 
 // {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
@@ -311,16 +312,34 @@ static zl_status plan_gemm(zl_ctx* c, const GemmDesc& d, GemmPlan& P) {
   return ZL_OK;
 }
 
-zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
-  // Problems with an empty output do nothing; a pair whose members pick
-  // different variants runs as two launches.
-  const GemmDesc* live[zk::kMaxGemmBatch];
-  int nl = 0;
-  for (int i = 0; i < n; ++i)
-    if (d[i].M > 0 && d[i].N > 0) live[nl++] = &d[i];
-  if (nl == 0) return ZL_OK;
-  if (nl > zk::kMaxGemmBatch) return fail(c, ZL_ERR_INVALID, "GEMM batch of %d problems", nl);
+// One grouped launch, planned: its live problems, variant, grid, arguments
+// and split-K partial buffers.
+struct BatchLaunch {
+  const GemmDesc* live[zk::kMaxGemmBatch] = {};
   GemmPlan P[zk::kMaxGemmBatch];
+  int nl = 0;
+  int kid = -1;
+  unsigned gx = 0, gy = 0, gz = 0, threads = 0;
+  zk::GemmBatch B{};
+  float* part[zk::kMaxGemmBatch] = {};
+  double flops = 0.0;
+};
+
+// Plans the launch of the problems d[0..n) with a non-empty output. `one` is
+// set when they can share a single launch (then L is complete); otherwise
+// the caller runs them one by one.
+static zl_status plan_batch(zl_ctx* c, const GemmDesc* d, int n, BatchLaunch& L, bool& one) {
+  one = false;
+  L.nl = 0;
+  for (int i = 0; i < n; ++i)
+    if (d[i].M > 0 && d[i].N > 0) {
+      if (L.nl == zk::kMaxGemmBatch) return fail(c, ZL_ERR_INVALID, "GEMM batch of %d problems", n);
+      L.live[L.nl++] = &d[i];
+    }
+  const int nl = L.nl;
+  if (nl == 0) return ZL_OK;
+  const GemmDesc* const* live = L.live;
+  GemmPlan* P = L.P;
   for (int i = 0; i < nl; ++i) {
     zl_status s = plan_gemm(c, *live[i], P[i]);
     if (s) return s;
@@ -330,10 +349,8 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
   // as two launches, which measured faster than one grid sized for the
   // larger problem (e.g. 24576 x 256 x 256 with 24576 x 512 x 256 data
   // gradients: 127 us paired, 38 + 71 us apart).
-  if (nl == 2 && (live[0]->M != live[1]->M || live[0]->N != live[1]->N || live[0]->K != live[1]->K)) {
-    zl_status s = run_gemm_batch(c, live[0], 1);
-    return s ? s : run_gemm_batch(c, live[1], 1);
-  }
+  if (nl == 2 && (live[0]->M != live[1]->M || live[0]->N != live[1]->N || live[0]->K != live[1]->K))
+    return ZL_OK;
   // A pair whose members differ only in exact fit runs as one launch of
   // the general form.
   if (nl == 2 && P[0].kid != P[1].kid && inexact_form(P[0].kid) == inexact_form(P[1].kid))
@@ -353,20 +370,16 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
     } else if (g0.kind == G_NARROW_M && g1.kind == G_NARROW_M) {
       shared = gemm_id(live[0]->M > 16 || live[1]->M > 16 ? "zk_narrow_m2" : "zk_narrow_m1");
     }
-    if (shared >= 0) {
-      P[0].kid = P[1].kid = shared;
-    } else {
-      zl_status s = run_gemm_batch(c, live[0], 1);
-      return s ? s : run_gemm_batch(c, live[1], 1);
-    }
+    if (shared < 0) return ZL_OK;
+    P[0].kid = P[1].kid = shared;
   }
   const GemmKernel& g = kGemmTable[P[0].kid - K_GEMM_BASE];
-  zk::GemmBatch B{};
+  zk::GemmBatch& B = L.B;
+  B = zk::GemmBatch{};
   B.count = nl;
   B.zper = 1;
   unsigned gx = 0, gy = 0;
   double flops = 0.0;
-  float* part[zk::kMaxGemmBatch] = {nullptr, nullptr};
   for (int i = 0; i < nl; ++i) {
     const GemmDesc& q = *live[i];
     zk::GemmArgs& a = B.g[i];
@@ -390,6 +403,7 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
     a.nsplit = P[i].splits;
     a.vecA = P[i].vec;
     a.vecB = P[i].vec;
+    L.part[i] = nullptr;
     if (P[i].splits == 1) {
       a.C = q.C;
       a.ldc = q.ldc;
@@ -408,7 +422,7 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
         return fail(c, ZL_ERR_INVALID, "split-K scratch too small (%zu < %zu floats)", q.ws_floats,
                     need);
       }
-      part[i] = ws;
+      L.part[i] = ws;
       a.C = ws;
       a.ldc = q.N;
       a.split_stride = (long long)mn;
@@ -419,32 +433,40 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
     if (g.kind == G_TILED) B.zper = std::max(B.zper, P[i].splits);
     flops += 2.0 * q.M * (q.N_alg > 0 ? q.N_alg : q.N) * (double)(q.K_alg > 0 ? q.K_alg : q.K);
   }
-  c->pending_flops = flops;
-  c->pending_shape = {live[0]->M, live[0]->N, live[0]->K, P[0].splits};
-  zl_status s = launch(c, P[0].kid, gx, gy, (unsigned)(nl * B.zper), B, 0, (unsigned)g.threads);
-  if (s) return s;
-  // Split-K partials: reduced now, or handed to the caller's all-layer
-  // reduction (seg_out), which also takes tensors written directly.
-  for (int i = 0; i < nl; ++i) {
-    const GemmDesc& q = *live[i];
-    const zk::GemmArgs& a = B.g[i];
+  L.kid = P[0].kid;
+  L.gx = gx;
+  L.gy = gy;
+  L.gz = (unsigned)(nl * B.zper);
+  L.threads = (unsigned)g.threads;
+  L.flops = flops;
+  one = true;
+  return ZL_OK;
+}
+
+// After a planned launch: split-K partials reduced now, or handed to the
+// caller's all-layer reduction (seg_out), which also takes tensors written
+// directly.
+static zl_status finish_batch(zl_ctx* c, const BatchLaunch& L) {
+  for (int i = 0; i < L.nl; ++i) {
+    const GemmDesc& q = *L.live[i];
+    const zk::GemmArgs& a = L.B.g[i];
     if (q.seg_out) {
       zk::ReduceSeg& r = *q.seg_out;
       r = zk::ReduceSeg{};
-      r.part = part[i];
-      r.rowpart = part[i] ? a.rowsumA : nullptr;
+      r.part = L.part[i];
+      r.rowpart = L.part[i] ? a.rowsumA : nullptr;
       r.out = q.C;
       r.rowout = q.rowsum_out;
       r.mn = (long long)q.M * q.N;
       r.cols = q.N;
       r.ldo = q.ldc;
       r.rows = q.rowsum_out ? q.M : 0;
-      r.splits = P[i].splits;
+      r.splits = L.P[i].splits;
       continue;
     }
-    if (!part[i]) continue;
+    if (!L.part[i]) continue;
     zk::SplitReduceArgs r{};
-    r.part = part[i];
+    r.part = L.part[i];
     r.out = q.C;
     r.rowpart = a.rowsumA;
     r.rowout = q.rowsum_out;
@@ -453,10 +475,62 @@ zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
     r.cols = q.N;
     r.ldo = q.ldc;
     r.rows = q.rowsum_out ? q.M : 0;
-    r.splits = P[i].splits;
-    if ((s = launch_splitk_reduce(c, r))) return s;
+    r.splits = L.P[i].splits;
+    zl_status s = launch_splitk_reduce(c, r);
+    if (s) return s;
   }
   return ZL_OK;
+}
+
+zl_status run_gemm_batch(zl_ctx* c, const GemmDesc* d, int n) {
+  BatchLaunch L;
+  bool one = false;
+  zl_status s = plan_batch(c, d, n, L, one);
+  if (s || L.nl == 0) return s;
+  if (!one) {
+    s = run_gemm_batch(c, L.live[0], 1);
+    return s ? s : run_gemm_batch(c, L.live[1], 1);
+  }
+  c->pending_flops = L.flops;
+  c->pending_shape = {L.live[0]->M, L.live[0]->N, L.live[0]->K, L.P[0].splits};
+  s = launch(c, L.kid, L.gx, L.gy, L.gz, L.B, 0, L.threads);
+  return s ? s : finish_batch(c, L);
+}
+
+zl_status run_gemm_bwd(zl_ctx* c, const GemmDesc* w, int nw, const GemmDesc* d, int nd) {
+  if (c->merged_bwd && nd > 0) {
+    BatchLaunch W, D;
+    bool ow = false, od = false;
+    zl_status s = plan_batch(c, w, nw, W, ow);
+    if (s) return s;
+    if (ow && W.nl > 0 && (s = plan_batch(c, d, nd, D, od))) return s;
+    int mk = -1;
+    if (ow && od && W.nl > 0 && D.nl > 0 && D.kid == gemm_id("zk_gemm_ak_bn_96x128x32_w24_dg_x")) {
+      if (W.kid == gemm_id("zk_gemm_am_bn_128x128x32_w24_x"))
+        mk = K_GEMM_BWD_128;
+      else if (W.kid == gemm_id("zk_gemm_am_bn_64x128x32_w24_x"))
+        mk = K_GEMM_BWD_64;
+    }
+    if (mk >= 0) {
+      zk::GemmPair a{};
+      a.w = W.B;
+      a.d = D.B;
+      a.wgx = (int)W.gx;
+      a.wgy = (int)W.gy;
+      a.wgz = (int)W.gz;
+      a.dgx = (int)D.gx;
+      a.dgy = (int)D.gy;
+      a.dgz = (int)D.gz;
+      const long long blocks = (long long)W.gx * W.gy * W.gz + (long long)D.gx * D.gy * D.gz;
+      c->pending_flops = W.flops + D.flops;
+      c->pending_shape = {D.live[0]->M, D.live[0]->N, D.live[0]->K, W.P[0].splits};
+      s = launch(c, mk, (unsigned)blocks, 1, 1, a, 0, 512);
+      if (!s) s = finish_batch(c, W);
+      return s ? s : finish_batch(c, D);
+    }
+  }
+  zl_status s = run_gemm_batch(c, w, nw);
+  return s || nd == 0 ? s : run_gemm_batch(c, d, nd);
 }
 
 zl_status run_gemm(zl_ctx* c, const GemmDesc& d) { return run_gemm_batch(c, &d, 1); }
@@ -754,6 +828,7 @@ zl_status zl_init(int device, zl_ctx** out) {
   if (const char* v = getenv("ZL_SPLITK_TARGET")) c->splitk_target = std::max(1, atoi(v));
   if (const char* v = getenv("ZL_NARROW")) c->narrow = atoi(v) != 0;
   if (const char* v = getenv("ZL_NARROW_TARGET")) c->narrow_target = std::max(1, atoi(v));
+  if (const char* v = getenv("ZL_MERGED_BWD")) c->merged_bwd = atoi(v) != 0;
   // Default-priority stream (no priority variants are used anywhere).
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
