@@ -546,7 +546,8 @@ __device__ void epoch_end_body(const EpochEndArgs& p) {
 __device__ void gae_body(const GaeArgs& p) {
   if (p.guard && *p.guard == 0) return;
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= p.N) return;
+  // T = 0 writes nothing (and the clamped loads below need a step to read).
+  if (e >= p.N || p.T <= 0) return;
   float acc = 0.f;
   float next_v = p.last_v[e];
   if (p.T <= kGaeMaxT) {

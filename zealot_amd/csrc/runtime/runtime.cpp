@@ -22,7 +22,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_norm_apply",
     "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
     "zk_stage",         "zk_sumsq_multi", "zk_clip_scale",  "zk_adam_multi",
-    "zk_gemm_bwd_128x128_dg_x", "zk_gemm_bwd_64x128_dg_x",
+    "zk_gemm_bwd_128x128_dg_x", "zk_gemm_bwd_64x128_dg_x", "zk_head_fwd", "zk_head_fwd_x",
 };
 
 // {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
@@ -1261,6 +1261,7 @@ zl_status zl_gae(zl_ctx* c, const float* rewards, const float* values, const uin
   if (!c) return ZL_ERR_INVALID;
   if (!rewards || !values || !dones || !last_values || !adv || !ret || T < 0 || N < 0)
     return fail(c, ZL_ERR_INVALID, "zl_gae: bad argument");
+  if (T == 0 || N == 0) return ZL_OK;  // no steps or no envs: nothing to write
   zk::GaeArgs a{};
   a.r = rewards;
   a.v = values;
