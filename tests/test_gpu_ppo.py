@@ -221,6 +221,46 @@ def test_head_tile_schedules_match_unfused(ctx, n, shuffled):
         assert abs(fs[key] - us[key]) <= 1e-5 * max(1.0, abs(us[key])), key
 
 
+@pytest.mark.parametrize("n,shuffled", [(3001, True), (24576, False), (24576, True)])
+def test_head_forward_fused_matches_separate(ctx, n, shuffled):
+    """zk_head_fwd (the last hidden layer's forward computed tile by tile
+    inside the head launch) against that layer as a GEMM launch of its own
+    before zk_head (ZL_FUSED_HEAD=1): a ragged 3,001-row minibatch takes the
+    masked form, 24,576 rows the exact-fit one. Every activation is summed in
+    the same order, so the actor's gradients and statistics are bit-identical;
+    the critic's output-layer partials are grouped per block, and its tiles
+    go one per block with the forward inside (three per block otherwise at
+    24,576 rows), so its gradients agree to rounding (1e-6)."""
+    ad, cd = [40, 256, 128, 12], [40, 256, 128, 1]
+    g = np.random.default_rng(29)
+    actor = synth.kaiming_uniform_net(g, ad, 0.1)
+    critic = synth.kaiming_uniform_net(g, cd, 0.1)
+    batch, log_std = make_batch(n, ad, cd, actor, critic, seed=4)
+    db = DeviceBatch(ctx, batch["obs"], batch["obs"], batch["action"], batch["mean_old"],
+                     batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
+    perm = ctx.to_device(g.permutation(n).astype(np.int32)) if shuffled else None
+    out = []
+    for fused_fwd in (True, False):
+        if not fused_fwd:
+            os.environ["ZL_FUSED_HEAD"] = "1"
+        try:
+            gac = GpuActorCritic(ctx, ad, cd, n)
+        finally:
+            os.environ.pop("ZL_FUSED_HEAD", None)
+        gac.set_params(actor, critic, log_std, 1e-3)
+        out.append(gac.minibatch_grads(db, PpoConfig(entropy_coef=0.01), 0, n, perm=perm))
+        gac.close()
+    (fa, fc, fl, fs), (sa, sc, sl, ss) = out
+    assert np.array_equal(fa, sa) and np.array_equal(fl, sl)
+    for key in ("surrogate", "kl"):
+        assert fs[key] == ss[key], key
+    ec = per_tensor_err(cd, fc, sc)
+    print(f"[gpu] head forward fused n={n} shuffled={shuffled}: actor bit-identical, critic {ec:.2e}",
+          flush=True)
+    assert ec <= 1e-6
+    assert abs(fs["value_loss"] - ss["value_loss"]) <= 1e-6 * max(1.0, abs(ss["value_loss"]))
+
+
 @pytest.mark.parametrize("shuffled", [False, True])
 def test_backward_merged_matches_separate(ctx, shuffled):
     """A layer's weight- and data-gradient GEMMs as one zk_gemm_bwd_* launch

@@ -274,10 +274,14 @@ constexpr int gemm_smem_floats() {
               Tile<BN, BKC, BK, 64 * WM * WN, VEC, EXACT>::SIZE);
 }
 
+// LDS_OUT: the epilogue writes the whole BM x BN tile (no bounds tests;
+// entries outside C come from zero operands) into the LDS array `cl` with
+// row pitch p.ldc instead of to p.C; `cl` may overlap `smem` (it is written
+// after the k-loop's last barrier).
 template <bool AK, bool BKC, int BM, int BN, int BK, int WM, int WN, bool VEC,
-          bool YPRE = false, bool EXACT = false>
+          bool YPRE = false, bool EXACT = false, bool LDS_OUT = false>
 __device__ __forceinline__ void gemm_body(float* __restrict__ smem, const GemmArgs& p, int split,
-                                          int mt, int nt) {
+                                          int mt, int nt, float* __restrict__ cl = nullptr) {
   constexpr int NT = 64 * WM * WN;
   constexpr int TM = BM / (WM * 16);
   constexpr int TN = BN / (WN * 16);
@@ -464,6 +468,20 @@ __device__ __forceinline__ void gemm_body(float* __restrict__ smem, const GemmAr
   float* C = p.C + (long long)split * p.split_stride;
   const bool full_tile = EXACT || (m0 + BM <= p.M && n0 + BN <= p.N);
   auto emit = [&](auto f) {
+    if constexpr (LDS_OUT) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int ml = (wm * TM + i) * 16 + lg * 4 + r;
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const int nl = (wn * TN + j) * 16 + lr;
+            cl[ml * p.ldc + nl] = f(acc[i][j][r], i, j, r, m0 + ml, n0 + nl);
+          }
+        }
+      return;
+    }
     auto run = [&](auto full) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)

@@ -4,9 +4,10 @@
 // clipped surrogate / the critic's clipped value loss, the head's data
 // gradient times ELU' of the last hidden activations (dL/dz of the last
 // hidden layer), and the head's weight and bias gradients as per-block
-// partials. The activations of a tile are read once into LDS and every
-// intermediate (means, their gradients) stays there. All sums run in a fixed
-// order, so the results are the same on every run.
+// partials. The activations of a tile are read once into LDS (zk_head_fwd*:
+// computed there from the layer below, so that layer's output never goes to
+// HBM) and every intermediate (means, their gradients) stays there. All sums
+// run in a fixed order, so the results are the same on every run.
 #pragma once
 #include "common.hip"
 #include "ppo_kernels.hip"
@@ -70,6 +71,38 @@ __device__ __forceinline__ void head_load_tile(const HeadNet& q, long long r0, i
   head_tile_store(q, nr, v, sx);
 }
 
+// zk_head_fwd*: rows [r0, r0 + kHeadRows) of the last hidden layer's output,
+// ELU(x2 . w2^T + b2), computed into sx by a 64 x 128 GEMM tile whose 32-wide
+// k-tiles are staged in smem (sx overlaps that staging: the tile is written
+// after the k-loop's last barrier). All 64 rows and 128 columns are written;
+// rows past the minibatch and columns past H come from zero operands, so they
+// are finite, and the phases that follow give them zero weight. EXACT: rows,
+// H = 128 and k2 are whole tiles (the host checks), no clamps or masks.
+constexpr int kHeadFwdBK = 32;
+static_assert(gemm_smem_floats<true, true, kHeadRows, kHeadMaxHidden, kHeadFwdBK, 2, 4, true>() <= kHeadLds,
+              "the forward tile's staging fits the head's LDS");
+template <bool EXACT>
+__device__ __forceinline__ void head_forward_tile(const HeadNet& q, long long rows, long long r0,
+                                                  float* smem, float* sx) {
+  GemmArgs a{};
+  a.A = q.x2;
+  a.lda = q.ldx2;
+  a.B = q.w2;
+  a.ldb = q.ldw2;
+  a.bias = q.b2;
+  a.M = (int)rows;
+  a.N = q.H;
+  a.K = q.k2;
+  a.ldc = kHeadPitch;
+  a.epi = kEpiBiasN;
+  a.act = 1;
+  a.vecA = a.vecB = 1;
+  a.kt_per_split = (q.k2 + kHeadFwdBK - 1) / kHeadFwdBK;
+  a.nsplit = 1;
+  gemm_body<true, true, kHeadRows, kHeadMaxHidden, kHeadFwdBK, 2, 4, true, false, EXACT, true>(
+      smem, a, 0, (int)(r0 / kHeadRows), 0, sx);
+}
+
 // Sum over a row's 32 components in component order, every lane of the
 // 32-lane group getting the result: lane k stores its term in the row's LDS
 // slot k (components >= A hold 0, and adding 0 changes no sum), the group's
@@ -96,41 +129,57 @@ __device__ __forceinline__ float row_sum_ordered(float* srow, int k, float term)
   return (threadIdx.x & 32) ? s1 : s0;
 }
 
+// FWD: 0 reads the tile of the last hidden activations; 1 (masked) / 2
+// (exact-fit) computes it (head_forward_tile).
+template <int FWD>
 __device__ void head_actor(const HeadArgs& p, float* smem) {
   const HeadNet& q = p.net[0];
   float* sx = smem;                                      // activations [R x pitch]
   float* sw = sx + kHeadRows * kHeadPitch;               // weights [32 x pitch], rows >= A zero
   float* sd = sw + kHeadMaxActions * kHeadPitch;         // means, then dL/dmean [R x dpitch]
   float* sred = sd + kHeadRows * kHeadDPitch;            // [groups][34]
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int lr = lane & 15, lg = lane >> 4;
+  int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  int lr = lane & 15, lg = lane >> 4;
   const int A = p.A, H = q.H;
 
-  {  // the head weights, rows >= A and columns >= H zero (loads as in head_load_tile)
-    constexpr int QPR = kHeadMaxHidden / 4;
-    constexpr int NQ = kHeadMaxActions * QPR / kHeadThreads;
-    static_assert(kHeadMaxActions * QPR % kHeadThreads == 0, "whole quads per thread");
+  // The head weights, rows >= A and columns >= H zero (loads as in
+  // head_load_tile). With FWD the forward tile's staging overwrites sw, so
+  // they are read after the tile's forward.
+  constexpr int WQPR = kHeadMaxHidden / 4;
+  constexpr int WNQ = kHeadMaxActions * WQPR / kHeadThreads;
+  static_assert(kHeadMaxActions * WQPR % kHeadThreads == 0, "whole quads per thread");
+  float4 wv[WNQ];
+  auto load_weights = [&]() {
     const int c_last = (H - 1) & ~3;
-    float4 v[NQ];
 #pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int i = t + kHeadThreads * u, m = i / QPR, c = (i % QPR) * 4;
-      v[u] = *reinterpret_cast<const float4*>(q.w + (long long)min(m, A - 1) * q.ldw + min(c, c_last));
+    for (int u = 0; u < WNQ; ++u) {
+      const int i = t + kHeadThreads * u, m = i / WQPR, c = (i % WQPR) * 4;
+      wv[u] = *reinterpret_cast<const float4*>(q.w + (long long)min(m, A - 1) * q.ldw + min(c, c_last));
     }
+  };
+  if constexpr (FWD == 0) load_weights();
+  auto store_weights = [&]() {
 #pragma unroll
-    for (int u = 0; u < NQ; ++u) {
-      const int i = t + kHeadThreads * u, m = i / QPR, c = (i % QPR) * 4;
-      *reinterpret_cast<float4*>(sw + m * kHeadPitch + c) = quad_or_zero(v[u], m < A, c, H);
+    for (int u = 0; u < WNQ; ++u) {
+      const int i = t + kHeadThreads * u, m = i / WQPR, c = (i % WQPR) * 4;
+      *reinterpret_cast<float4*>(sw + m * kHeadPitch + c) = quad_or_zero(wv[u], m < A, c, H);
     }
-  }
+  };
+  if constexpr (FWD == 0) store_weights();
 
   // Loss lanes: 16 groups of 32, lane k on action component k.
-  const int grp = t >> 5, k = t & 31;
-  const bool on = k < A;
-  const float ls = on ? p.log_std[k] : 0.f;
-  const float sdv = expf(ls);
-  const float inv_var = expf(-2.0f * ls);
-  const float inv_sd = expf(-ls);
+  int grp = t >> 5, k = t & 31;
+  bool on = k < A;
+  // Per-lane loss constants (with FWD set after each tile's forward, so that
+  // they hold no registers during its GEMM).
+  float ls = 0.f, sdv = 0.f, inv_var = 0.f, inv_sd = 0.f;
+  auto loss_consts = [&]() {
+    ls = on ? p.log_std[k] : 0.f;
+    sdv = expf(ls);
+    inv_var = expf(-2.0f * ls);
+    inv_sd = expf(-ls);
+  };
+  if constexpr (FWD == 0) loss_consts();
   const float lo = 1.0f - p.clip, hi = 1.0f + p.clip;
   float gacc = 0.f, sacc = 0.f, kacc = 0.f;
   float klacc = 0.f;  // sum of (mean - mean_old)^2 of component k over the group's rows
@@ -139,44 +188,84 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   // Wave-to-tile mapping: 16-row tile rt = wave % 4; forward components
   // 16 * (wave / 4) ..; data-gradient columns 64 * (wave / 4) ..; weight
   // gradient columns 16 * wave ...
-  const int rt = wave & 3, half = wave >> 2;
-  const int mf = 16 * half + lr;  // this lane's forward component
-  const float bias_f = mf < A ? q.b[min(mf, A - 1)] : 0.f;
+  int rt = wave & 3, half = wave >> 2;
+  int mf = 16 * half + lr;  // this lane's forward component
+  float bias_f = 0.f;
+  auto load_bias = [&]() { bias_f = mf < A ? q.b[min(mf, A - 1)] : 0.f; };
+  if constexpr (FWD == 0) load_bias();
 
   struct In {
     float act, lpo, adv, mo;
   };
   constexpr int RG = kHeadRows / kHeadGroups;  // rows per loss group
   const long long ntiles = (p.rows + kHeadRows - 1) / kHeadRows;
-  for (int tt = 0; tt < p.tiles_per_block; ++tt) {
+  // With FWD a block takes one tile (the host lays the grid out so), which
+  // leaves the loop's accumulators at zero while the tile's GEMM runs.
+  const int tpb = FWD ? 1 : p.tiles_per_block;
+  for (int tt = 0; tt < tpb; ++tt) {
     const long long tile = blockIdx.x + (long long)tt * gridDim.x;
     if (tile >= ntiles) break;  // uniform
-    const long long r0 = tile * kHeadRows;
-    const int nr = (int)min((long long)kHeadRows, p.rows - r0);
+    long long r0 = tile * kHeadRows;
+    int nr = (int)min((long long)kHeadRows, p.rows - r0);
     // Loss inputs of the group's rows, in flight during the tile load and
-    // the forward (group g takes rows g, g + 16, ...).
+    // the forward (group g takes rows g, g + 16, ...; with FWD, issued after
+    // the tile's GEMM so that they hold no registers during it).
     // Rows past nr read the last row's inputs (the loss skips those rows),
     // so every load is unconditional in the row and the sample indices of
     // a shuffled minibatch are all in flight before the first wait.
-    long long sidx[RG];
-#pragma unroll
-    for (int j = 0; j < RG; ++j) {
-      const long long rr = p.row0 + r0 + min(grp + kHeadGroups * j, nr - 1);
-      sidx[j] = p.perm ? (long long)p.perm[rr] : rr;
-    }
     In in[RG];
+    auto load_inputs = [&]() {
+      long long sidx[RG];
 #pragma unroll
-    for (int j = 0; j < RG; ++j) {
-      const long long s = sidx[j];
-      In x;
-      x.act = on ? p.action[s * p.ldact + k] : 0.f;
-      x.lpo = p.logp_old[s];
-      x.adv = p.adv[s];
-      x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
-      in[j] = x;
-    }
+      for (int j = 0; j < RG; ++j) {
+        const long long rr = p.row0 + r0 + min(grp + kHeadGroups * j, nr - 1);
+        sidx[j] = p.perm ? (long long)p.perm[rr] : rr;
+      }
+#pragma unroll
+      for (int j = 0; j < RG; ++j) {
+        const long long s = sidx[j];
+        In x;
+        x.act = on ? p.action[s * p.ldact + k] : 0.f;
+        x.lpo = p.logp_old[s];
+        x.adv = p.adv[s];
+        x.mo = (p.mean_old && on) ? p.mean_old[s * p.ldmo + k] : 0.f;
+        in[j] = x;
+      }
+    };
+    if constexpr (FWD == 0) load_inputs();
     lds_barrier();  // the previous tile's LDS reads are done
-    head_load_tile(q, r0, nr, sx);
+    if constexpr (FWD == 0) {
+      head_load_tile(q, r0, nr, sx);
+    } else {
+      head_forward_tile<FWD == 2>(q, p.rows, r0, smem, sx);
+      {
+        // The tile's row and the thread's indices made opaque here, so that
+        // the compiler computes the addresses of the phases below after the
+        // GEMM instead of holding them in registers across it (which spills).
+        int ti = (int)tile;
+        asm volatile("" : "+s"(ti));
+        r0 = (long long)ti * kHeadRows;
+        nr = (int)min((long long)kHeadRows, p.rows - r0);
+        int tv = threadIdx.x;
+        asm volatile("" : "+v"(tv));
+        t = tv;
+        lane = t & 63;
+        wave = t >> 6;
+        lr = lane & 15;
+        lg = lane >> 4;
+        grp = t >> 5;
+        k = t & 31;
+        on = k < A;
+        rt = wave & 3;
+        half = wave >> 2;
+        mf = 16 * half + lr;
+      }
+      load_weights();
+      store_weights();
+      load_inputs();
+      loss_consts();
+      load_bias();
+    }
     lds_barrier();
 
     // Head forward: rows of tile rt, components 16 * half ...; the k range
@@ -344,6 +433,7 @@ __device__ void head_actor(const HeadArgs& p, float* smem) {
   }
 }
 
+template <int FWD>
 __device__ void head_critic(const HeadArgs& p, float* smem) {
   const HeadNet& q = p.net[1];
   float* sx = smem;
@@ -366,9 +456,11 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
   // Tiles cb, cb + cbn, ...: each tile's loads are issued while the previous
   // tile is worked on (cb < ntiles: cbn = ceil(ntiles / critic_tiles)).
   float4 xv[kHeadTileQuads];
-  head_tile_issue(q, (long long)cb * kHeadRows,
-                  (int)min((long long)kHeadRows, p.rows - (long long)cb * kHeadRows), xv);
-  for (int tt = 0; tt < p.critic_tiles; ++tt) {
+  if constexpr (FWD == 0)
+    head_tile_issue(q, (long long)cb * kHeadRows,
+                    (int)min((long long)kHeadRows, p.rows - (long long)cb * kHeadRows), xv);
+  const int ctl = p.critic_tiles;
+  for (int tt = 0; tt < ctl; ++tt) {
     const long long tile = cb + (long long)tt * cbn;
     if (tile >= ntiles) break;  // uniform
     const long long r0 = tile * kHeadRows;
@@ -382,12 +474,17 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
       vo = p.value_old[sidx];
       R = p.ret[sidx];
     }
-    if (tt == 0 && t < kHeadMaxHidden) sw[t] = t < H ? wt : 0.f;
+    if (FWD == 0 && tt == 0 && t < kHeadMaxHidden) sw[t] = t < H ? wt : 0.f;
     lds_barrier();  // the previous tile's LDS reads are done
-    head_tile_store(q, nr, xv, sx);
-    const long long next = tile + cbn;
-    if (tt + 1 < p.critic_tiles && next < ntiles)
-      head_tile_issue(q, next * kHeadRows, (int)min((long long)kHeadRows, p.rows - next * kHeadRows), xv);
+    if constexpr (FWD == 0) {
+      head_tile_store(q, nr, xv, sx);
+      const long long next = tile + cbn;
+      if (tt + 1 < p.critic_tiles && next < ntiles)
+        head_tile_issue(q, next * kHeadRows, (int)min((long long)kHeadRows, p.rows - next * kHeadRows), xv);
+    } else {  // the staging of the tile's forward overwrites sw
+      head_forward_tile<FWD == 2>(q, p.rows, r0, smem, sx);
+      if (t < kHeadMaxHidden) sw[t] = t < H ? wt : 0.f;
+    }
     lds_barrier();
     // value = b + sum_k w_k x_k: U lanes per row, lane u on columns u, u + U,
     // ..., then the U partial sums in lane order.
@@ -493,13 +590,19 @@ __device__ void head_critic(const HeadArgs& p, float* smem) {
 }  // namespace zk
 
 // Held to four waves per SIMD (two blocks of eight wavefronts per CU, which
-// the LDS footprint allows): at most 128 VGPRs.
-extern "C" __global__ __launch_bounds__(zk::kHeadThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void zk_head(zk::HeadArgs p) {
-  __shared__ __align__(16) float smem[zk::kHeadLds];
-  if (p.guard && *p.guard == 0) return;
-  if (blockIdx.z == 0)
-    zk::head_actor(p, smem);
-  else
-    zk::head_critic(p, smem);
-}
+// the LDS footprint allows): at most 128 VGPRs. zk_head reads the last hidden
+// activations; zk_head_fwd (masked) and zk_head_fwd_x (exact-fit) compute
+// them from the layer below (HeadNet::x2 / w2 / b2).
+#define ZK_HEAD(NAME, FWD)                                                          \
+  extern "C" __global__ __launch_bounds__(zk::kHeadThreads)                         \
+  __attribute__((amdgpu_waves_per_eu(4))) void NAME(zk::HeadArgs p) {              \
+    __shared__ __align__(16) float smem[zk::kHeadLds];                              \
+    if (p.guard && *p.guard == 0) return;                                           \
+    if (blockIdx.z == 0)                                                            \
+      zk::head_actor<FWD>(p, smem);                                                 \
+    else                                                                            \
+      zk::head_critic<FWD>(p, smem);                                                \
+  }
+ZK_HEAD(zk_head, 0)
+ZK_HEAD(zk_head_fwd, 1)
+ZK_HEAD(zk_head_fwd_x, 2)

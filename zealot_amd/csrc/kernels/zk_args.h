@@ -205,6 +205,13 @@ struct HeadNet {
   float* wpart;    // [blocks x nout x H] weight-gradient partials
   float* bpart;    // [blocks x nout] bias-gradient partials
   int ldx, ldw, ldo, ldz, H;
+  // zk_head_fwd*: the tile of x is computed in the block instead of read,
+  // x = ELU(x2 . w2^T + b2) — the last hidden layer's forward (x2 [rows x
+  // ldx2] its input, w2 [H x ldw2] its weights, k2 its input width).
+  const float* x2;
+  const float* w2;
+  const float* b2;
+  int ldx2, ldw2, k2;
 };
 struct HeadArgs {
   HeadNet net[2];

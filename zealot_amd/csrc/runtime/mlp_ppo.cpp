@@ -530,8 +530,12 @@ struct zl_ppo {
   int mb_cap = 0;
   // The output layers and the losses run as one zk_head launch (last hidden
   // widths <= kHeadMaxHidden, A <= kHeadMaxActions, equal depths;
-  // ZL_FUSED_HEAD=0 turns it off).
+  // ZL_FUSED_HEAD=0 turns it off). head_fwd: with two or more hidden layers
+  // that launch also computes the last hidden layer's forward, tile by tile
+  // (zk_head_fwd*), when a minibatch takes one tile per block
+  // (ZL_FUSED_HEAD=1 keeps that layer a GEMM launch of its own).
   bool fused_head = false;
+  bool head_fwd = false;
   // Reduction partials.
   float* gls_part = nullptr;  // [nb x A]
   float* astat_part = nullptr;
@@ -726,23 +730,42 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
                          zk::FinalizeArgs* tail = nullptr) {
   zl_ctx* c = p->c;
   const int La = p->actor.L, Lc = p->critic.L, A = p->A;
-  zl_status s = pair_forward(c, v, p->params, px, rows, guard, p->fused_head ? La - 1 : -1);
+  const long long tiles = cdiv(rows, zk::kHeadRows);
+  const long long tpb = cdiv(tiles, zk::kHeadMaxBlocks);
+  // The last hidden layer's forward inside zk_head: one tile per block, and
+  // operands that the GEMM tile reads as aligned float4 rows.
+  bool hfwd = p->fused_head && p->head_fwd && tpb == 1;
+  bool hfwd_exact = hfwd && rows % zk::kHeadRows == 0;
+  for (int i = 0; i < 2 && hfwd; ++i) {
+    const NetLayout& nl = i == 0 ? p->actor : p->critic;
+    const NetBuffers& nb = i == 0 ? p->ab : p->cb;
+    const int l = nl.L - 2;
+    const float* w2 = p->params + nl.w_off[l];
+    hfwd = ((uintptr_t)nb.act[l] & 15) == 0 && ((uintptr_t)w2 & 15) == 0 && nb.ld[l] % 4 == 0 &&
+           nl.ldw[l] % 4 == 0;
+    hfwd_exact = hfwd_exact && nl.dims[l + 1] == zk::kHeadMaxHidden && nl.dims[l] % 32 == 0;
+  }
+  zl_status s = pair_forward(c, v, p->params, px, rows, guard,
+                             p->fused_head ? (hfwd ? La - 2 : La - 1) : -1);
   if (s) return s;
   int head_blocks = 0, critic_blocks = 0;
   if (p->fused_head) {
-    const long long tiles = cdiv(rows, zk::kHeadRows);
-    const long long tpb = cdiv(tiles, zk::kHeadMaxBlocks);
     head_blocks = (int)cdiv(tiles, tpb);
     // A critic tile is about a third of an actor tile's work: when the actor
     // takes one tile per block and leaves workgroup slots free (two per CU),
     // the critic takes its tiles in that many blocks, up to three tiles each
     // (each tile's loads in flight during the previous one), so both nets
-    // finish in one round; otherwise it is laid out like the actor.
+    // finish in one round; otherwise it is laid out like the actor. With
+    // the forward inside, a tile of either net is mostly that GEMM: one tile
+    // per block for both (two or three critic tiles per block measured 2-12 %
+    // slower).
     const int slots = 2 * c->cu_count;
     long long ctiles = tpb;
-    if (tpb == 1 && head_blocks < slots) ctiles = std::min<long long>(3, cdiv(tiles, slots - head_blocks));
+    if (!hfwd && tpb == 1 && head_blocks < slots)
+      ctiles = std::min<long long>(3, cdiv(tiles, slots - head_blocks));
     critic_blocks = (int)cdiv(tiles, ctiles);
     zk::HeadArgs h{};
+    double fwd_flops = 0.0;
     for (int i = 0; i < 2; ++i) {
       const NetLayout& nl = i == 0 ? p->actor : p->critic;
       const NetBuffers& nb = i == 0 ? p->ab : p->cb;
@@ -760,6 +783,15 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
       q.H = nl.dims[l];
       q.wpart = p->pws + p->pplan.off[i][l];
       q.bpart = q.wpart + (size_t)zk::kHeadMaxBlocks * nl.dims[l + 1] * nl.dims[l];
+      if (hfwd) {
+        q.x2 = nb.act[l - 1];
+        q.ldx2 = nb.ld[l - 1];
+        q.w2 = p->params + nl.w_off[l - 1];
+        q.ldw2 = nl.ldw[l - 1];
+        q.b2 = p->params + nl.b_off[l - 1];
+        q.k2 = nl.dims[l - 1];
+        fwd_flops += 2.0 * rows * nl.dims[l] * (double)nl.dims[l - 1];
+      }
     }
     h.action = b->action;
     h.ldact = b->ld_action;
@@ -786,7 +818,10 @@ zl_status minibatch_pass(zl_ppo* p, const NetView v[2], const int* px, const int
     h.vstat_part = p->vstat_part;
     h.kl_part = head_kl;
     h.guard = guard;
-    if ((s = launch(c, K_HEAD, (unsigned)head_blocks, 1, 2, h, 0, zk::kHeadThreads))) return s;
+    c->pending_flops = fwd_flops;  // the layer GEMM work inside (timing)
+    if ((s = launch(c, hfwd ? (hfwd_exact ? K_HEAD_FWD_X : K_HEAD_FWD) : K_HEAD, (unsigned)head_blocks,
+                    1, 2, h, 0, zk::kHeadThreads)))
+      return s;
     pc->nb_a = head_blocks;
     pc->nb_v = critic_blocks;
   } else {
@@ -1125,6 +1160,7 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
     const char* env = getenv("ZL_FUSED_HEAD");
     p->fused_head = na == nc && na >= 3 && ha <= zk::kHeadMaxHidden && hc <= zk::kHeadMaxHidden &&
                     p->A <= zk::kHeadMaxActions && !(env && atoi(env) == 0);
+    p->head_fwd = p->fused_head && na >= 4 && !(env && atoi(env) == 1);
   }
   const size_t bytes = (size_t)p->nflat * 4;
   zl_status s = ZL_OK;
