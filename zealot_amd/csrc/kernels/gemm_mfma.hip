@@ -261,9 +261,11 @@ __device__ __forceinline__ BlockTile block_tile_of(int g, int gx, int ntl, int n
   }
   return {b % gx, b / gx, g / ntiles};
 }
-__device__ __forceinline__ BlockTile block_tile() {
-  const int g = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  return block_tile_of(g, (int)gridDim.x, (int)gridDim.y, (int)gridDim.z);
+// Problem and tile of block g of a tiled GemmBatch launch (z = the split-K
+// slice within the problem).
+__device__ __forceinline__ BlockTile batch_tile(const GemmBatch& b, int g, int& prob) {
+  prob = b.count > 1 && g >= b.blk0[1] ? 1 : 0;
+  return block_tile_of(g - b.blk0[prob], b.gx[prob], b.gy[prob], b.gz[prob]);
 }
 
 // LDS floats of one gemm_body instantiation: both operand tiles, double
@@ -714,11 +716,9 @@ __device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
 #define ZK_GEMM_X(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC, EXACT)                               \
   extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(zk::GemmBatch b) {         \
     __shared__ __align__(16) float smem[zk::gemm_smem_floats<AK, BKC, BM, BN, BK, WM, WN, VEC, EXACT>()]; \
-    const zk::BlockTile bt = zk::block_tile();                                               \
-    const int prob = bt.z / b.zper;                                                          \
-    if (prob >= b.count) return;                                                             \
-    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, VEC, false, EXACT>(smem, b.g[prob], bt.z % b.zper, \
-                                                                 bt.mt, bt.nt);              \
+    int prob;                                                                                \
+    const zk::BlockTile bt = zk::batch_tile(b, (int)blockIdx.x, prob);                       \
+    zk::gemm_body<AK, BKC, BM, BN, BK, WM, WN, VEC, false, EXACT>(smem, b.g[prob], bt.z, bt.mt, bt.nt); \
   }
 #define ZK_GEMM(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC) \
   ZK_GEMM_X(NAME, AK, BKC, BM, BN, BK, WM, WN, VEC, false)
@@ -738,19 +738,16 @@ ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, true)
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
 void zk_gemm_ak_bn_96x128x32_w24_dg(zk::GemmBatch b) {
   __shared__ __align__(16) float smem[zk::gemm_smem_floats<true, false, 96, 128, 32, 2, 4, true>()];
-  const zk::BlockTile bt = zk::block_tile();
-  const int prob = bt.z / b.zper;
-  if (prob >= b.count) return;
-  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true>(smem, b.g[prob], bt.z % b.zper, bt.mt, bt.nt);
+  int prob;
+  const zk::BlockTile bt = zk::batch_tile(b, (int)blockIdx.x, prob);
+  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true>(smem, b.g[prob], bt.z, bt.mt, bt.nt);
 }
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
 void zk_gemm_ak_bn_96x128x32_w24_dg_x(zk::GemmBatch b) {
   __shared__ __align__(16) float smem[zk::gemm_smem_floats<true, false, 96, 128, 32, 2, 4, true, true>()];
-  const zk::BlockTile bt = zk::block_tile();
-  const int prob = bt.z / b.zper;
-  if (prob >= b.count) return;
-  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.g[prob], bt.z % b.zper, bt.mt,
-                                                                 bt.nt);
+  int prob;
+  const zk::BlockTile bt = zk::batch_tile(b, (int)blockIdx.x, prob);
+  zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.g[prob], bt.z, bt.mt, bt.nt);
 }
 // Exact-fit forms (suffix _x) of the update's layer-GEMM variants.
 ZK_GEMM_X(zk_gemm_ak_bk_96x128x32_w24_x, true, true, 96, 128, 32, 2, 4, true, true)
@@ -778,20 +775,16 @@ ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, false)
     constexpr int SW = zk::gemm_smem_floats<false, false, WBM, 128, 32, 2, 4, true, true>();      \
     constexpr int SD = zk::gemm_smem_floats<true, false, 96, 128, 32, 2, 4, true, true>();        \
     __shared__ __align__(16) float smem[SW > SD ? SW : SD];                                       \
-    const int nw = b.wgx * b.wgy * b.wgz;                                                          \
     const int g = (int)blockIdx.x;                                                                 \
-    if (g < nw) {                                                                                  \
-      const zk::BlockTile bt = zk::block_tile_of(g, b.wgx, b.wgy, b.wgz);                          \
-      const int prob = bt.z / b.w.zper;                                                            \
-      if (prob >= b.w.count) return;                                                               \
-      zk::gemm_body<false, false, WBM, 128, 32, 2, 4, true, false, true>(smem, b.w.g[prob],         \
-                                                                        bt.z % b.w.zper, bt.mt, bt.nt); \
+    int prob;                                                                                      \
+    if (g < b.nw) {                                                                                \
+      const zk::BlockTile bt = zk::batch_tile(b.w, g, prob);                                      \
+      zk::gemm_body<false, false, WBM, 128, 32, 2, 4, true, false, true>(smem, b.w.g[prob], bt.z,   \
+                                                                        bt.mt, bt.nt);             \
     } else {                                                                                       \
-      const zk::BlockTile bt = zk::block_tile_of(g - nw, b.dgx, b.dgy, b.dgz);                     \
-      const int prob = bt.z / b.d.zper;                                                            \
-      if (prob >= b.d.count) return;                                                               \
-      zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.d.g[prob],            \
-                                                                     bt.z % b.d.zper, bt.mt, bt.nt); \
+      const zk::BlockTile bt = zk::batch_tile(b.d, g - b.nw, prob);                               \
+      zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.d.g[prob], bt.z,      \
+                                                                     bt.mt, bt.nt);                \
     }                                                                                              \
   }
 ZK_GEMM_BWD(zk_gemm_bwd_128x128_dg_x, 128)

@@ -46,23 +46,25 @@ struct GemmArgs {
 };
 
 // Up to two GEMMs of one kernel variant in one launch (the actor's and the
-// critic's layer of the same shape class). grid.z = count * zper: problem
-// blockIdx.z / zper, split-K slice blockIdx.z % zper; blocks outside a
-// problem's tile grid or slice count return at once.
+// critic's layer). Tiled kernels: a 1-D grid in which problem i owns blocks
+// [blk0[i], blk0[i] + gx[i] * gy[i] * gz[i]), laid out as its own tile grid
+// gx x gy with gz split-K slices, so problems of different shapes share a
+// launch without idle blocks. Narrow kernels: grid.z = problem (zper = 1),
+// blocks outside a problem's grid return at once.
 constexpr int kMaxGemmBatch = 2;
 struct GemmBatch {
   GemmArgs g[kMaxGemmBatch];
   int count;
   int zper;
+  int blk0[kMaxGemmBatch];
+  int gx[kMaxGemmBatch], gy[kMaxGemmBatch], gz[kMaxGemmBatch];
 };
 
-// A layer's weight-gradient batch and data-gradient batch as one launch of
-// wgx*wgy*wgz + dgx*dgy*dgz blocks: the weight-gradient blocks first, each
-// part's blocks mapped onto its own grid.
+// A layer's weight-gradient batch and data-gradient batch as one launch: the
+// weight-gradient batch's nw blocks first, then the data-gradient batch's.
 struct GemmPair {
   GemmBatch w, d;
-  int wgx, wgy, wgz;
-  int dgx, dgy, dgz;
+  int nw;
 };
 
 struct SplitReduceArgs {

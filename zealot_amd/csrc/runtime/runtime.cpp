@@ -3,6 +3,7 @@
 #include <dlfcn.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -344,12 +345,14 @@ static zl_status plan_batch(zl_ctx* c, const GemmDesc* d, int n, BatchLaunch& L,
     zl_status s = plan_gemm(c, *live[i], P[i]);
     if (s) return s;
   }
-  // Only problems of one shape share a launch: a pair of different shapes
-  // (the actor's and the critic's layer when the nets differ in width) runs
-  // as two launches, which measured faster than one grid sized for the
-  // larger problem (e.g. 24576 x 256 x 256 with 24576 x 512 x 256 data
-  // gradients: 127 us paired, 38 + 71 us apart).
-  if (nl == 2 && (live[0]->M != live[1]->M || live[0]->N != live[1]->N || live[0]->K != live[1]->K))
+  // Narrow kernels size one grid for both problems, so only problems of one
+  // shape share such a launch. (Tiled kernels give each problem its own
+  // block range, so the actor's and the critic's layer share a launch
+  // whatever their shapes.)
+  const bool narrow_pair = nl == 2 && kGemmTable[P[0].kid - K_GEMM_BASE].kind != G_TILED &&
+                           kGemmTable[P[1].kid - K_GEMM_BASE].kind != G_TILED;
+  if (narrow_pair &&
+      (live[0]->M != live[1]->M || live[0]->N != live[1]->N || live[0]->K != live[1]->K))
     return ZL_OK;
   // A pair whose members differ only in exact fit runs as one launch of
   // the general form.
@@ -430,13 +433,27 @@ static zl_status plan_batch(zl_ctx* c, const GemmDesc* d, int n, BatchLaunch& L,
     }
     gx = std::max(gx, P[i].gx);
     gy = std::max(gy, P[i].gy);
-    if (g.kind == G_TILED) B.zper = std::max(B.zper, P[i].splits);
     flops += 2.0 * q.M * (q.N_alg > 0 ? q.N_alg : q.N) * (double)(q.K_alg > 0 ? q.K_alg : q.K);
   }
   L.kid = P[0].kid;
-  L.gx = gx;
-  L.gy = gy;
-  L.gz = (unsigned)(nl * B.zper);
+  if (g.kind == G_TILED) {  // one block range per problem, a 1-D grid
+    long long blk = 0;
+    for (int i = 0; i < nl; ++i) {
+      B.blk0[i] = (int)blk;
+      B.gx[i] = (int)P[i].gx;
+      B.gy[i] = (int)P[i].gy;
+      B.gz[i] = P[i].splits;
+      blk += (long long)P[i].gx * P[i].gy * P[i].splits;
+    }
+    if (blk > INT_MAX) return fail(c, ZL_ERR_INVALID, "GEMM grid of %lld blocks", blk);
+    L.gx = (unsigned)blk;
+    L.gy = 1;
+    L.gz = 1;
+  } else {
+    L.gx = gx;
+    L.gy = gy;
+    L.gz = (unsigned)nl;
+  }
   L.threads = (unsigned)g.threads;
   L.flops = flops;
   one = true;
@@ -515,13 +532,8 @@ zl_status run_gemm_bwd(zl_ctx* c, const GemmDesc* w, int nw, const GemmDesc* d, 
       zk::GemmPair a{};
       a.w = W.B;
       a.d = D.B;
-      a.wgx = (int)W.gx;
-      a.wgy = (int)W.gy;
-      a.wgz = (int)W.gz;
-      a.dgx = (int)D.gx;
-      a.dgy = (int)D.gy;
-      a.dgz = (int)D.gz;
-      const long long blocks = (long long)W.gx * W.gy * W.gz + (long long)D.gx * D.gy * D.gz;
+      a.nw = (int)W.gx;  // tiled batches: 1-D grids
+      const long long blocks = (long long)W.gx + D.gx;
       c->pending_flops = W.flops + D.flops;
       c->pending_shape = {D.live[0]->M, D.live[0]->N, D.live[0]->K, W.P[0].splits};
       s = launch(c, mk, (unsigned)blocks, 1, 1, a, 0, 512);
