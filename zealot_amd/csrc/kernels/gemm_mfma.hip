@@ -371,8 +371,31 @@ __device__ __forceinline__ void gemm_body(float* __restrict__ smem, const GemmAr
   // so its latency overlaps the last MFMAs instead of the epilogue waiting
   // for it.
   const bool elu_grad = YPRE && p.epi == kEpiEluGrad;
-  float ypre[YPRE ? TM : 1][YPRE ? TN : 1][4];
+  // Staged epilogue (exact-fit data gradients): the tile goes through LDS so
+  // that each thread reads the ELU' operand and stores dL/dz as whole float4
+  // row segments (the layer-1 backward 234 -> 229 us per launch; the forward
+  // and the weight-gradient partials measured no faster, so they keep the
+  // direct stores). The host picks exact-fit forms only for float4-aligned
+  // C and Y rows.
+  constexpr bool STAGED = EXACT && YPRE && !LDS_OUT;
+  constexpr int SQ = BN / 4;        // float4 quads per tile row
+  constexpr int SRP = NT / SQ;      // rows per staged pass
+  constexpr int SPASS = BM / SRP;   // passes
+  constexpr int SPITCH = BN + 4;
+  static_assert(!STAGED || (NT % SQ == 0 && BM % SRP == 0 &&
+                            BM * SPITCH <= gemm_smem_floats<AK, BKC, BM, BN, BK, WM, WN, VEC, EXACT>()),
+                "staged epilogue layout");
+  float4 yq[STAGED && YPRE ? SPASS : 1];
+  float ypre[YPRE && !STAGED ? TM : 1][YPRE && !STAGED ? TN : 1][4];
   auto prefetch_y = [&]() {
+    if constexpr (STAGED) {
+#pragma unroll
+      for (int ps = 0; ps < SPASS; ++ps) {
+        const int ml = tid / SQ + ps * SRP;
+        yq[ps] = *reinterpret_cast<const float4*>(p.Y + (long long)(m0 + ml) * p.ldy + n0 + 4 * (tid % SQ));
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -381,7 +404,7 @@ __device__ __forceinline__ void gemm_body(float* __restrict__ smem, const GemmAr
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + (wm * TM + i) * 16 + lg * 4 + r;
-          if constexpr (YPRE) ypre[i][j][r] = (m < p.M && n < p.N) ? p.Y[(long long)m * p.ldy + n] : 0.f;
+          if constexpr (YPRE && !STAGED) ypre[i][j][r] = (m < p.M && n < p.N) ? p.Y[(long long)m * p.ldy + n] : 0.f;
         }
       }
   };
@@ -468,6 +491,68 @@ __device__ __forceinline__ void gemm_body(float* __restrict__ smem, const GemmAr
   // Epilogue. The kind (and ELU flag) is uniform, so each kind runs its own
   // straight-line element loop; tiles wholly inside C skip the bounds tests.
   float* C = p.C + (long long)split * p.split_stride;
+  if constexpr (STAGED) {
+    // Every LDS read of the k-loop precedes its last barrier, so the
+    // buffers are free: the accumulators go to LDS as they lie, then each
+    // thread takes float4 row segments (column quad tid % SQ, rows tid / SQ
+    // + SRP * pass) through the epilogue to HBM.
+    float* st = smem;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ml = (wm * TM + i) * 16 + lg * 4 + r;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) st[ml * SPITCH + (wn * TN + j) * 16 + lr] = acc[i][j][r];
+      }
+    __syncthreads();
+    const int cq = tid % SQ;
+    const int n = n0 + 4 * cq;
+    float4 bq = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p.epi == kEpiBiasN) bq = make_float4(p.bias[n], p.bias[n + 1], p.bias[n + 2], p.bias[n + 3]);
+#pragma unroll
+    for (int ps = 0; ps < SPASS; ++ps) {
+      const int ml = tid / SQ + ps * SRP;
+      const long long m = m0 + ml;
+      float4 v = *reinterpret_cast<const float4*>(st + ml * SPITCH + 4 * cq);
+      if (p.epi == kEpiBiasN) {
+        v.x += bq.x;
+        v.y += bq.y;
+        v.z += bq.z;
+        v.w += bq.w;
+        if (p.act) {
+          v.x = elu(v.x);
+          v.y = elu(v.y);
+          v.z = elu(v.z);
+          v.w = elu(v.w);
+        }
+      } else if (p.epi == kEpiBiasM) {
+        const float bm = p.bias[m * p.bias_stride];
+        v.x += bm;
+        v.y += bm;
+        v.z += bm;
+        v.w += bm;
+        if (p.act) {
+          v.x = elu(v.x);
+          v.y = elu(v.y);
+          v.z = elu(v.z);
+          v.w = elu(v.w);
+        }
+      } else if (p.epi == kEpiEluGrad) {
+        float4 y;
+        if constexpr (YPRE)
+          y = yq[ps];
+        else
+          y = *reinterpret_cast<const float4*>(p.Y + m * p.ldy + n);
+        v.x *= elu_grad_from_act(y.x);
+        v.y *= elu_grad_from_act(y.y);
+        v.z *= elu_grad_from_act(y.z);
+        v.w *= elu_grad_from_act(y.w);
+      }
+      *reinterpret_cast<float4*>(C + m * p.ldc + n) = v;
+    }
+    return;
+  }
   const bool full_tile = EXACT || (m0 + BM <= p.M && n0 + BN <= p.N);
   auto emit = [&](auto f) {
     if constexpr (LDS_OUT) {

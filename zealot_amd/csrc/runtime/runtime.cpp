@@ -304,8 +304,12 @@ static zl_status plan_gemm(zl_ctx* c, const GemmDesc& d, GemmPlan& P) {
     P.splits = (int)std::max<long long>(1, cdiv(kt, P.per));
     P.gx = (unsigned)cdiv(d.M, g.bm);
     P.gy = (unsigned)cdiv(d.N, g.bn);
-    // Every tile and k-tile full: the exact-fit form of the same variant.
-    if (d.K > 0 && d.M % g.bm == 0 && d.N % g.bn == 0 && d.K % g.bk == 0) {
+    // Every tile and k-tile full: the exact-fit form of the same variant
+    // (which may store C and read the ELU' operand as float4 row segments:
+    // those rows must be 16-byte aligned, unless C is the split-K scratch).
+    const bool c_vec = P.splits > 1 || (aligned16(d.C) && d.ldc % 4 == 0);
+    const bool y_vec = d.epi != zk::kEpiEluGrad || (aligned16(d.Y) && d.ldy % 4 == 0);
+    if (d.K > 0 && d.M % g.bm == 0 && d.N % g.bn == 0 && d.K % g.bk == 0 && c_vec && y_vec) {
       const int x = exact_form(P.kid);
       if (x >= 0) P.kid = x;
     }
