@@ -11,12 +11,14 @@ follow from the GPU means (mean + exp(log_std) * eps, one rounding each) and
 logp is checked against the oracle's ActorCritic::logp of the GPU's own
 action and mean."""
 
+import os
+
 import numpy as np
 import pytest
 
 from conftest import rel_amax
 from oracle import zl_oracle as zo
-from zealot_amd import synth
+from zealot_amd import Context, synth
 from zealot_amd.rl import GpuActorCritic, GpuNormalizer
 
 pytestmark = pytest.mark.gpu
@@ -108,3 +110,57 @@ def test_act_rejects_critic_norm_without_value(ctx):
     with pytest.raises(ZealotError):
         gac.act(x, 4, ctx.alloc((4, 3)), ctx.alloc((4, 3)), ctx.alloc(4), critic_norm=cn, critic_obs=x)
     gac.close()
+
+
+@pytest.mark.parametrize("n", [4096, 1000, 17, 1])
+def test_fused_policy_step_matches_layer_launches(ctx, n):
+    """zk_policy (normalise, every layer of both nets and the sampling in one
+    launch, 16 rows per block) against the layer-GEMM launches
+    (ZL_POLICY_FUSED=0, read when a context is created: that run gets a
+    context of its own). Both add every reduction in the same order, so
+    actions, log-probabilities, means and values are bit-identical; so are the
+    plain forwards of zl_ppo_values and zl_ppo_actor_mean at these sizes."""
+    ad, cd = synth.ACTOR_DIMS, [64, 512, 256, 128, 1]
+    g = np.random.default_rng(40 + n)
+    actor = synth.kaiming_uniform_net(g, ad, 0.1)
+    critic = synth.kaiming_uniform_net(g, cd, 0.1)
+    log_std = (g.uniform(-1.0, 0.0, ad[-1])).astype(np.float32)
+    st_o = zo.norm_update(zo.norm_new(ad[0]), raw_obs(5, 300, ad[0]))
+    st_c = zo.norm_update(zo.norm_new(cd[0]), raw_obs(6, 300, cd[0]))
+    obs, cobs = raw_obs(7 + n, n, ad[0]), raw_obs(8 + n, n, cd[0])
+    eps = g.standard_normal((n, ad[-1])).astype(np.float32)
+    A = ad[-1]
+    out = []
+    for fused in (True, False):
+        if not fused:
+            os.environ["ZL_POLICY_FUSED"] = "0"
+        try:
+            cx = ctx if fused else Context(0)
+        finally:
+            os.environ.pop("ZL_POLICY_FUSED", None)
+        gac = GpuActorCritic(cx, ad, cd, 2048)
+        gac.set_params(actor, critic, log_std, 1e-3)
+        on = GpuNormalizer.from_state(cx, st_o[:ad[0]], st_o[ad[0]:2 * ad[0]], float(st_o[-1]))
+        cn = GpuNormalizer.from_state(cx, st_c[:cd[0]], st_c[cd[0]:2 * cd[0]], float(st_c[-1]))
+        d_obs, d_cobs, d_eps = cx.to_device(obs), cx.to_device(cobs), cx.to_device(eps)
+        d_act, d_lp, d_mean, d_val = cx.alloc((n, A)), cx.alloc(n), cx.alloc((n, A)), cx.alloc(n)
+        gac.act(d_obs, n, d_eps, d_act, d_lp, mean=d_mean, value=d_val, critic_obs=d_cobs,
+                obs_norm=on, critic_norm=cn)
+        r = [d_act.numpy(), d_lp.numpy(), d_mean.numpy(), d_val.numpy()]
+        # actor only, inputs already normalised
+        gac.act(d_obs, n, d_eps, d_act, d_lp)
+        r += [d_act.numpy(), d_lp.numpy()]
+        pv, pm = cx.alloc(n), cx.alloc((n, A))
+        gac.values(d_cobs, n, pv)
+        gac.actor_mean(d_obs, n, pm)
+        r += [pv.numpy(), pm.numpy()]
+        out.append(r)
+        gac.close()
+        del on, cn, d_obs, d_cobs, d_eps, d_act, d_lp, d_mean, d_val, pv, pm
+        if not fused:
+            cx.close()
+    names = ["action", "logp", "mean", "value", "action (actor only)", "logp (actor only)", "values",
+             "actor mean"]
+    for name, x, y in zip(names, out[0], out[1]):
+        assert np.array_equal(x, y), name
+    print(f"[gpu] fused policy step n={n}: bit-identical to the layer launches", flush=True)

@@ -7,3 +7,4 @@
 #include "obs_norm.hip"
 #include "ppo_kernels.hip"
 #include "head.hip"
+#include "policy.hip"

@@ -367,6 +367,39 @@ struct SampleArgs {
   const int* guard;
 };
 
+// One rollout step in one launch (zk_policy): per block kPolicyRows rows, grid
+// (row blocks, nets). Net 0 is the actor, net 1 (when present) the critic.
+// Each block normalises its rows of x with the net's Normalizer state (when
+// norm is set), runs every layer with the activations in LDS and writes the
+// last layer to out (when set); with `sample`, the actor's blocks then draw
+// action = mean + exp(log_std) * eps and its log-probability. Hidden widths
+// are multiples of 16 up to kPolicyMaxWidth, the input padded to a multiple
+// of 16 within the layer-0 weight rows, and the output width at most 32
+// (the host checks).
+constexpr int kPolicyRows = 16;
+constexpr int kPolicyThreads = 512;
+constexpr int kPolicyMaxWidth = 512;
+constexpr int kPolicyMaxLayers = 8;
+struct PolicyNet {
+  const float* x;     // [rows x ldx] inputs (raw, or already normalised)
+  const float* norm;  // Normalizer state [2 * dims[0] + 1], nullable
+  float* out;         // [rows x ldo] the last layer's output, nullable
+  long long w_off[kPolicyMaxLayers], b_off[kPolicyMaxLayers];
+  int ldw[kPolicyMaxLayers];
+  int dims[kPolicyMaxLayers + 1];
+  int L, ldx, ldo;
+};
+struct PolicyArgs {
+  PolicyNet net[2];
+  const float* params;
+  const float* log_std;  // [A]
+  const float* eps;      // [rows x lde]
+  float* action;         // [rows x lda]
+  float* logp;           // [rows]
+  long long rows;
+  int A, lde, lda, sample;
+};
+
 // Observation normaliser (Normalizer / PendingNorm, zealot-rl/src/ppo.rs:104-206).
 // A state is float[2 * dim + 1]: mean[dim], m2[dim], count; a pending state
 // with count 0 is empty (its mean and m2 are zero).

@@ -49,6 +49,7 @@ enum KernelId : int {
   K_GEMM_BWD_64,
   K_HEAD_FWD,
   K_HEAD_FWD_X,
+  K_POLICY,
   K_GEMM_BASE
 };
 
@@ -156,6 +157,9 @@ struct zl_ctx {
   // A layer's weight- and data-gradient GEMMs as one launch where a merged
   // kernel covers their variants (ZL_MERGED_BWD=0 runs them as two).
   bool merged_bwd = true;
+  // Forwards of up to kPolicyFusedRows rows (a rollout step) as one zk_policy
+  // launch where the nets fit it (ZL_POLICY_FUSED=0 keeps the layer GEMMs).
+  bool fused_policy = true;
   // Device address of the allocation-free scratch array on this context's
   // device (zl_grad_clip_scale_noalloc), set at zl_init.
   float* noalloc_scratch = nullptr;

@@ -1532,6 +1532,43 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
   return ZL_OK;
 }
 
+// zk_policy: below this many rows a forward runs as one launch (each block
+// reads every weight once from L2, so the weight traffic grows with the row
+// blocks; the layer GEMMs take larger batches).
+constexpr long long kPolicyFusedRows = 8192;
+
+// Whether a net fits zk_policy: at most kPolicyMaxLayers layers, hidden widths
+// multiples of 16 up to kPolicyMaxWidth, input width up to kPolicyMaxWidth
+// with its 16-padded width inside the layer-0 weight rows, at most 32 outputs,
+// 16-byte aligned weight rows.
+static bool policy_fits(const zl_ppo* p, const NetLayout& nl) {
+  if (nl.L < 1 || nl.L > zk::kPolicyMaxLayers || nl.dims[0] > zk::kPolicyMaxWidth ||
+      nl.dims[nl.L] > 32 || nl.ldw[0] < round_up(nl.dims[0], 16))
+    return false;
+  for (int l = 1; l < nl.L; ++l)
+    if (nl.dims[l] % 16 != 0 || nl.dims[l] > zk::kPolicyMaxWidth) return false;
+  for (int l = 0; l < nl.L; ++l)
+    if (nl.w_off[l] % 4 != 0 || nl.ldw[l] % 4 != 0) return false;
+  return ((uintptr_t)p->params & 15) == 0;
+}
+
+static void policy_net(zk::PolicyNet& q, const NetLayout& nl, const float* x, int ldx,
+                       const float* norm, float* out, int ldo) {
+  q = zk::PolicyNet{};
+  q.x = x;
+  q.ldx = ldx;
+  q.norm = norm;
+  q.out = out;
+  q.ldo = ldo;
+  q.L = nl.L;
+  for (int l = 0; l <= nl.L; ++l) q.dims[l] = nl.dims[l];
+  for (int l = 0; l < nl.L; ++l) {
+    q.w_off[l] = nl.w_off[l];
+    q.b_off[l] = nl.b_off[l];
+    q.ldw[l] = nl.ldw[l];
+  }
+}
+
 static zl_status chunked_forward(zl_ppo* p, bool critic, const float* x, int ld, long long n,
                                  float* out, int ld_out, int cols) {
   zl_ctx* c = p->c;
@@ -1539,6 +1576,13 @@ static zl_status chunked_forward(zl_ppo* p, bool critic, const float* x, int ld,
   const NetBuffers& nb = critic ? p->cb : p->ab;
   if (!x || !out || n < 0 || ld < nl.dims[0] || ld_out < cols)
     return fail(c, ZL_ERR_INVALID, "forward: bad argument");
+  if (n > 0 && n <= kPolicyFusedRows && c->fused_policy && policy_fits(p, nl)) {
+    zk::PolicyArgs a{};
+    policy_net(a.net[0], nl, x, ld, nullptr, out, ld_out);
+    a.params = p->params;
+    a.rows = n;
+    return launch(c, K_POLICY, (unsigned)cdiv(n, zk::kPolicyRows), 1, 1, a, 0, zk::kPolicyThreads);
+  }
   // The output layer writes straight into the caller's rows.
   auto desc = [&](const NetBuffers& b, const float* xx, int rows, long long r0, int l) {
     GemmDesc d = fwd_desc(nl, b, p->params, xx, ld, nullptr, rows, nullptr, l);
@@ -1591,6 +1635,25 @@ zl_status zl_ppo_act(zl_ppo* p, const float* obs_norm, const float* obs, int ld_
       (value && (!cobs || ld_cobs < cd)) || (!value && critic_norm))
     return fail(c, ZL_ERR_INVALID, "zl_ppo_act: bad argument");
   if (n == 0) return ZL_OK;
+  if (n <= kPolicyFusedRows && c->fused_policy && A <= 32 && policy_fits(p, p->actor) &&
+      (!value || policy_fits(p, p->critic))) {
+    // One launch: normalise, both nets' layers, sampling (zk_policy).
+    zk::PolicyArgs a{};
+    policy_net(a.net[0], p->actor, obs, ld_obs, obs_norm, mean, ld_mean);
+    if (value) policy_net(a.net[1], p->critic, cobs, ld_cobs, critic_norm, value, 1);
+    a.params = p->params;
+    a.log_std = p->params + p->ls_off;
+    a.eps = eps;
+    a.lde = A;
+    a.action = action;
+    a.lda = A;
+    a.logp = logp;
+    a.rows = n;
+    a.A = A;
+    a.sample = 1;
+    return launch(c, K_POLICY, (unsigned)cdiv(n, zk::kPolicyRows), value ? 2 : 1, 1, a, 0,
+                  zk::kPolicyThreads);
+  }
   // Normalised inputs go to the padded staging buffers (16-byte aligned rows
   // for the layer-0 GEMM); raw inputs that are already normalised are read
   // in place.

@@ -24,6 +24,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
     "zk_stage",         "zk_sumsq_multi", "zk_clip_scale",  "zk_adam_multi",
     "zk_gemm_bwd_128x128_dg_x", "zk_gemm_bwd_64x128_dg_x", "zk_head_fwd", "zk_head_fwd_x",
+    "zk_policy",
 };
 
 // {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
@@ -845,6 +846,7 @@ zl_status zl_init(int device, zl_ctx** out) {
   if (const char* v = getenv("ZL_NARROW")) c->narrow = atoi(v) != 0;
   if (const char* v = getenv("ZL_NARROW_TARGET")) c->narrow_target = std::max(1, atoi(v));
   if (const char* v = getenv("ZL_MERGED_BWD")) c->merged_bwd = atoi(v) != 0;
+  if (const char* v = getenv("ZL_POLICY_FUSED")) c->fused_policy = atoi(v) != 0;
   // Default-priority stream (no priority variants are used anywhere).
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
