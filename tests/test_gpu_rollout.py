@@ -112,16 +112,25 @@ def test_act_rejects_critic_norm_without_value(ctx):
     gac.close()
 
 
-@pytest.mark.parametrize("n", [4096, 1000, 17, 1])
-def test_fused_policy_step_matches_layer_launches(ctx, n):
+TRAINER_A, TRAINER_C = [265, 256, 256, 128, 12], [64, 512, 256, 128, 1]
+
+
+@pytest.mark.parametrize("n,ad,cd", [(4096, synth.ACTOR_DIMS, [64, 512, 256, 128, 1]),
+                                     (1000, synth.ACTOR_DIMS, [64, 512, 256, 128, 1]),
+                                     (17, synth.ACTOR_DIMS, [64, 512, 256, 128, 1]),
+                                     (1, synth.ACTOR_DIMS, [64, 512, 256, 128, 1]),
+                                     (4096, TRAINER_A, TRAINER_C),
+                                     (777, [64, 128, 64, 9], [48, 96, 48, 1])])
+def test_fused_policy_step_matches_layer_launches(ctx, n, ad, cd):
     """zk_policy (normalise, every layer of both nets and the sampling in one
     launch, 16 rows per block) against the layer-GEMM launches
     (ZL_POLICY_FUSED=0, read when a context is created: that run gets a
-    context of its own). Both add every reduction in the same order, so
-    actions, log-probabilities, means and values are bit-identical; so are the
-    plain forwards of zl_ppo_values and zl_ppo_actor_mean at these sizes."""
-    ad, cd = synth.ACTOR_DIMS, [64, 512, 256, 128, 1]
-    g = np.random.default_rng(40 + n)
+    context of its own), on the headline nets, the reference trainer's nets
+    (a 265-wide input, 16-padded inside its 288-wide weight rows) and narrow
+    ones. Both add every reduction in the same order, so actions,
+    log-probabilities, means and values are bit-identical; so are the plain
+    forwards of zl_ppo_values and zl_ppo_actor_mean at these sizes."""
+    g = np.random.default_rng(40 + n + ad[0])
     actor = synth.kaiming_uniform_net(g, ad, 0.1)
     critic = synth.kaiming_uniform_net(g, cd, 0.1)
     log_std = (g.uniform(-1.0, 0.0, ad[-1])).astype(np.float32)
@@ -163,4 +172,4 @@ def test_fused_policy_step_matches_layer_launches(ctx, n):
              "actor mean"]
     for name, x, y in zip(names, out[0], out[1]):
         assert np.array_equal(x, y), name
-    print(f"[gpu] fused policy step n={n}: bit-identical to the layer launches", flush=True)
+    print(f"[gpu] fused policy step n={n} actor {ad}: bit-identical to the layer launches", flush=True)
