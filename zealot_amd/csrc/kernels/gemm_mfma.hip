@@ -811,6 +811,7 @@ __device__ __forceinline__ void reduce_all_body(const ReduceAllArgs& a) {
 // Naming: a{k,m} = A K- or M-contiguous, b{k,n} = B K- or N-contiguous,
 // then BMxBNxBK, the wave grid WMxWN and (_s) scalar global loads for
 // operands that are not 16-byte aligned row by row.
+ZK_GEMM(zk_gemm_ak_bk_128x128x32_w24, true, true, 128, 128, 32, 2, 4, true)
 ZK_GEMM(zk_gemm_ak_bk_96x128x32_w24, true, true, 96, 128, 32, 2, 4, true)
 ZK_GEMM(zk_gemm_ak_bk_64x64x32_w22, true, true, 64, 64, 32, 2, 2, true)
 ZK_GEMM(zk_gemm_ak_bk_32x64x32_w12, true, true, 32, 64, 32, 1, 2, true)
@@ -835,6 +836,7 @@ void zk_gemm_ak_bn_96x128x32_w24_dg_x(zk::GemmBatch b) {
   zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.g[prob], bt.z, bt.mt, bt.nt);
 }
 // Exact-fit forms (suffix _x) of the update's layer-GEMM variants.
+ZK_GEMM_X(zk_gemm_ak_bk_128x128x32_w24_x, true, true, 128, 128, 32, 2, 4, true, true)
 ZK_GEMM_X(zk_gemm_ak_bk_96x128x32_w24_x, true, true, 96, 128, 32, 2, 4, true, true)
 ZK_GEMM_X(zk_gemm_am_bn_128x128x32_w24_x, false, false, 128, 128, 32, 2, 4, true, true)
 ZK_GEMM_X(zk_gemm_am_bn_64x128x32_w24_x, false, false, 64, 128, 32, 2, 4, true, true)

@@ -38,6 +38,8 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w24_dg", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bk_96x128x32_w24_x", true, true, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bk_128x128x32_w24", true, true, 128, 128, 32, 512, true},
+    {"zk_gemm_ak_bk_128x128x32_w24_x", true, true, 128, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w24_dg_x", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_am_bn_128x128x32_w24_x", false, false, 128, 128, 32, 512, true},
     {"zk_gemm_am_bn_64x128x32_w24_x", false, false, 64, 128, 32, 512, true},
@@ -139,9 +141,10 @@ zl_status ensure_ws(zl_ctx* c, size_t floats) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Variant choice. M = 24,576 rows (and every multiple of 96) tiles into an
-// exact multiple of the 256 CUs with 96-row tiles, so the row-major layer
-// GEMMs use them; the narrow output layers use narrow-N tiles. The weight
+// Variant choice. The row-major forwards take the largest of 128 x 128,
+// 96 x 128, 64 x 64 and 32 x 64 tiles that still gives every CU a
+// workgroup; the data gradients 96 x 128 tiles (24,576 = 256 x 96 rows tile
+// evenly over the 256 CUs); the narrow output layers narrow-N tiles. The weight
 // gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
 // 512- and 256-wide layers, 64 x 128 for the 128-wide one (both with 32-row
 // k-tiles, so that the k-loop's barrier sits between two chunks) and
@@ -176,12 +179,14 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
         // Largest tile that still gives every CU a workgroup (small-batch
         // forwards such as a 4096-env rollout step), else the smallest.
         // (64 x 64 x 32 ahead of 64 x 128 x 16: its 32-row k-tiles measured
-        // faster on the 4,096-row rollout step's 123 -> 512 layer.)
-        static const char* const kFill[3] = {"zk_gemm_ak_bk_96x128x32_w24", "zk_gemm_ak_bk_64x64x32_w22",
-                                             "zk_gemm_ak_bk_32x64x32_w12"};
-        static const int kTile[3][2] = {{96, 128}, {64, 64}, {32, 64}};
-        int pick = 2;
-        for (int i = 0; i < 3; ++i)
+        // faster on the 4,096-row rollout step's 123 -> 512 layer; 128 x 128
+        // ahead of 96 x 128: the update's 24,576-row forwards 72.9 -> 69.3 us
+        // (123 -> 512) and 114.3 -> 108.2 us (512 -> 256) per pair.)
+        static const char* const kFill[4] = {"zk_gemm_ak_bk_128x128x32_w24", "zk_gemm_ak_bk_96x128x32_w24",
+                                             "zk_gemm_ak_bk_64x64x32_w22", "zk_gemm_ak_bk_32x64x32_w12"};
+        static const int kTile[4][2] = {{128, 128}, {96, 128}, {64, 64}, {32, 64}};
+        int pick = 3;
+        for (int i = 0; i < 4; ++i)
           if (cdiv(M, kTile[i][0]) * cdiv(N, kTile[i][1]) >= 256) {
             pick = i;
             break;
