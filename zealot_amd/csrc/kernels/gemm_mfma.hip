@@ -851,16 +851,16 @@ ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, false)
 
 // One layer's backward as one launch (GemmPair): the split-K weight-gradient
 // GEMMs of both nets (exact-fit am_bn tiles, blocks [0, w grid)) and their
-// data-gradient GEMMs with the ELU' epilogue (exact-fit 96 x 128 ak_bn tiles,
+// data-gradient GEMMs with the ELU' epilogue (exact-fit DBM x 128 ak_bn tiles,
 // the blocks after). The two parts read the same dL/dz and write disjoint
 // outputs; one grid lets data-gradient tiles start on the CUs that the
 // weight-gradient slices leave, instead of a second launch after the first
 // one's last block. The parts share one LDS allocation, the larger of the two.
-#define ZK_GEMM_BWD(NAME, WBM)                                                                    \
+#define ZK_GEMM_BWD(NAME, WBM, DBM)                                                               \
   extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))           \
   void NAME(zk::GemmPair b) {                                                                     \
     constexpr int SW = zk::gemm_smem_floats<false, false, WBM, 128, 32, 2, 4, true, true>();      \
-    constexpr int SD = zk::gemm_smem_floats<true, false, 96, 128, 32, 2, 4, true, true>();        \
+    constexpr int SD = zk::gemm_smem_floats<true, false, DBM, 128, 32, 2, 4, true, true>();       \
     __shared__ __align__(16) float smem[SW > SD ? SW : SD];                                       \
     const int g = (int)blockIdx.x;                                                                 \
     int prob;                                                                                      \
@@ -870,12 +870,28 @@ ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, false)
                                                                         bt.mt, bt.nt);             \
     } else {                                                                                       \
       const zk::BlockTile bt = zk::batch_tile(b.d, g - b.nw, prob);                               \
-      zk::gemm_body<true, false, 96, 128, 32, 2, 4, true, true, true>(smem, b.d.g[prob], bt.z,      \
+      zk::gemm_body<true, false, DBM, 128, 32, 2, 4, true, true, true>(smem, b.d.g[prob], bt.z,     \
                                                                      bt.mt, bt.nt);                \
     }                                                                                              \
   }
-ZK_GEMM_BWD(zk_gemm_bwd_128x128_dg_x, 128)
-ZK_GEMM_BWD(zk_gemm_bwd_64x128_dg_x, 64)
+ZK_GEMM_BWD(zk_gemm_bwd_128x128_dg_x, 128, 96)
+ZK_GEMM_BWD(zk_gemm_bwd_64x128_dg_x, 64, 96)
+ZK_GEMM_BWD(zk_gemm_bwd_128x128_dg128_x, 128, 128)
+ZK_GEMM_BWD(zk_gemm_bwd_64x128_dg128_x, 64, 128)
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+void zk_gemm_ak_bn_128x128x32_w24_dg(zk::GemmBatch b) {
+  __shared__ __align__(16) float smem[zk::gemm_smem_floats<true, false, 128, 128, 32, 2, 4, true>()];
+  int prob;
+  const zk::BlockTile bt = zk::batch_tile(b, (int)blockIdx.x, prob);
+  zk::gemm_body<true, false, 128, 128, 32, 2, 4, true, true>(smem, b.g[prob], bt.z, bt.mt, bt.nt);
+}
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+void zk_gemm_ak_bn_128x128x32_w24_dg_x(zk::GemmBatch b) {
+  __shared__ __align__(16) float smem[zk::gemm_smem_floats<true, false, 128, 128, 32, 2, 4, true, true>()];
+  int prob;
+  const zk::BlockTile bt = zk::batch_tile(b, (int)blockIdx.x, prob);
+  zk::gemm_body<true, false, 128, 128, 32, 2, 4, true, true, true>(smem, b.g[prob], bt.z, bt.mt, bt.nt);
+}
 
 extern "C" __global__ __launch_bounds__(256) void zk_splitk_reduce(zk::SplitReduceArgs p) {
   zk::splitk_reduce_body(p);

@@ -47,6 +47,8 @@ enum KernelId : int {
   K_ADAM_MULTI,
   K_GEMM_BWD_128,
   K_GEMM_BWD_64,
+  K_GEMM_BWD_128_D128,
+  K_GEMM_BWD_64_D128,
   K_HEAD_FWD,
   K_HEAD_FWD_X,
   K_POLICY,

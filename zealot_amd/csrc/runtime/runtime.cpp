@@ -23,7 +23,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_norm_apply",
     "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
     "zk_stage",         "zk_sumsq_multi", "zk_clip_scale",  "zk_adam_multi",
-    "zk_gemm_bwd_128x128_dg_x", "zk_gemm_bwd_64x128_dg_x", "zk_head_fwd", "zk_head_fwd_x",
+    "zk_gemm_bwd_128x128_dg_x", "zk_gemm_bwd_64x128_dg_x", "zk_gemm_bwd_128x128_dg128_x", "zk_gemm_bwd_64x128_dg128_x", "zk_head_fwd", "zk_head_fwd_x",
     "zk_policy",
 };
 
@@ -41,6 +41,8 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bk_128x128x32_w24", true, true, 128, 128, 32, 512, true},
     {"zk_gemm_ak_bk_128x128x32_w24_x", true, true, 128, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w24_dg_x", true, false, 96, 128, 32, 512, true},
+    {"zk_gemm_ak_bn_128x128x32_w24_dg", true, false, 128, 128, 32, 512, true},
+    {"zk_gemm_ak_bn_128x128x32_w24_dg_x", true, false, 128, 128, 32, 512, true},
     {"zk_gemm_am_bn_128x128x32_w24_x", false, false, 128, 128, 32, 512, true},
     {"zk_gemm_am_bn_64x128x32_w24_x", false, false, 64, 128, 32, 512, true},
     {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512, true},
@@ -143,8 +145,8 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Variant choice. The row-major forwards take the largest of 128 x 128,
 // 96 x 128, 64 x 64 and 32 x 64 tiles that still gives every CU a
-// workgroup; the data gradients 96 x 128 tiles (24,576 = 256 x 96 rows tile
-// evenly over the 256 CUs); the narrow output layers narrow-N tiles. The weight
+// workgroup; the data gradients 128 x 128 tiles where the rows divide into
+// them, else 96 x 128; the narrow output layers narrow-N tiles. The weight
 // gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
 // 512- and 256-wide layers, 64 x 128 for the 128-wide one (both with 32-row
 // k-tiles, so that the k-loop's barrier sits between two chunks) and
@@ -196,8 +198,11 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
       break;
     case L_AK_BN:
       // Data gradients (ELU' epilogue) take the variant that prefetches the
-      // activation operand.
-      name = M >= 4096 ? (epi == zk::kEpiEluGrad ? "zk_gemm_ak_bn_96x128x32_w24_dg"
+      // activation operand: 128-row tiles where the rows divide into them
+      // (24,576-row layer-1 / layer-2 backward 226.3 -> 224.6 / 71.9 ->
+      // 70.7 us), else 96-row tiles.
+      name = M >= 4096 ? (epi == zk::kEpiEluGrad ? (M % 128 == 0 ? "zk_gemm_ak_bn_128x128x32_w24_dg"
+                                                                  : "zk_gemm_ak_bn_96x128x32_w24_dg")
                                                  : "zk_gemm_ak_bn_96x128x32_w24")
                        : "zk_gemm_ak_bn_64x128x16_w22";
       break;
@@ -537,6 +542,12 @@ zl_status run_gemm_bwd(zl_ctx* c, const GemmDesc* w, int nw, const GemmDesc* d, 
         mk = K_GEMM_BWD_128;
       else if (W.kid == gemm_id("zk_gemm_am_bn_64x128x32_w24_x"))
         mk = K_GEMM_BWD_64;
+    }
+    if (ow && od && W.nl > 0 && D.nl > 0 && D.kid == gemm_id("zk_gemm_ak_bn_128x128x32_w24_dg_x")) {
+      if (W.kid == gemm_id("zk_gemm_am_bn_128x128x32_w24_x"))
+        mk = K_GEMM_BWD_128_D128;
+      else if (W.kid == gemm_id("zk_gemm_am_bn_64x128x32_w24_x"))
+        mk = K_GEMM_BWD_64_D128;
     }
     if (mk >= 0) {
       zk::GemmPair a{};
