@@ -124,6 +124,86 @@ def aux_measurements(ctx, gac, ro, d_obs, ld, n):
     }
 
 
+def _kernel_ms(ctx, fn, reps, between=None):
+    """Summed HIP-event kernel time per call of fn (every launch on the context
+    stream bracketed by events); between(), if given, runs before each call
+    outside the timed launches (a cache flush by hipMemcpyAsync)."""
+    fn()
+    ctx.synchronize()
+    tot = C.c_double()
+    ctx.check(ctx.lib.zl_timing_begin(ctx.h, b"*"), "timing_begin")
+    for _ in range(reps):
+        if between is not None:
+            between()
+        fn()
+    ctx.check(ctx.lib.zl_timing_end(ctx.h, C.byref(tot), None, None), "timing_end")
+    return tot.value / 1e3 / reps
+
+
+def operator_measurements(ctx):
+    """The two operator-level workloads: the single dense layer (X [4096 x
+    123] . W [123 x 512] + b, ELU; the reference's feature-major
+    gemm_bias_act, src/biped/cutile_gemm.rs:578-625) and the clipped Adam
+    step over actor + critic + log_std (459,323 parameters in the trainer's
+    17 tensors: device grad-norm clip at 1.0, then one tensor-list Adam
+    launch; src/bin/biped_train_gpu.rs:1368-1461). Kernel time by HIP
+    events; Adam warm (working set in the Infinity Cache) and cold (a
+    512 MiB device copy between calls evicts it)."""
+    from zealot_amd import ops, synth
+
+    c1 = synth.config1()
+    x, w_kn, b = c1["x"], c1["w_kn"], c1["b"]
+    m, n, k = 512, x.shape[0], x.shape[1]
+    dwt, dxt, db = ctx.to_device(w_kn.T.copy()), ctx.to_device(x.T.copy()), ctx.to_device(b)
+    out_t = ctx.alloc((m, n))
+    layer = lambda: ops.gemm_bias_act(ctx, out_t, dwt, dxt, m, n, k, db, 1, True)
+    t_layer = _kernel_ms(ctx, layer, 200)
+    t_layer_wall = _timed(ctx, layer, 200)
+    flop1 = 2.0 * m * n * k
+
+    sizes = []
+    for dims in (synth.ACTOR_DIMS, synth.CRITIC_DIMS):
+        for l in range(len(dims) - 1):
+            sizes += [dims[l + 1] * dims[l], dims[l + 1]]
+    sizes.append(synth.ACTOR_DIMS[-1])
+    npar = sum(sizes)
+    c3 = synth.config3(sum(sizes[:8]), sum(sizes[8:16]))
+    p0 = np.concatenate([c3["actor"], c3["critic"], c3["log_std"]]).astype(np.float32)
+    dp, dg = ctx.to_device(p0), ctx.to_device(c3["grads"][0])
+    dm, dv = ctx.to_device(np.zeros(npar, np.float32)), ctx.to_device(np.zeros(npar, np.float32))
+    scale, norm = ctx.alloc(1), ctx.alloc(1)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+    gt = [(dg.offset(int(o)), int(s)) for o, s in zip(offs[:-1], sizes)]
+    at = [(dp.offset(int(o)), dg.offset(int(o)), dm.offset(int(o)), dv.offset(int(o)), int(s))
+          for o, s in zip(offs[:-1], sizes)]
+    bc1, bc2 = float(np.float32(1.0) - np.float32(0.9 ** 11)), float(np.float32(1.0) - np.float32(0.999 ** 11))
+
+    def adam():
+        ops.grad_clip_scale(ctx, gt, 1.0, scale, norm)
+        ops.adam_multi(ctx, at, 1e-3, bc1, bc2, clip_scale=scale)
+
+    flush_bytes = 512 << 20
+    fa, fb = ctx.alloc(flush_bytes, np.uint8), ctx.alloc(flush_bytes, np.uint8)
+    flush = lambda: ctx.check(ctx.lib.zl_copy_d2d(ctx.h, fb.p, fa.p, flush_bytes), "zl_copy_d2d")
+    t_warm = _kernel_ms(ctx, adam, 100)
+    t_cold = _kernel_ms(ctx, adam, 30, between=flush)
+    t_adam_wall = _timed(ctx, adam, 100)
+    bytes3 = 32.0 * npar  # sum of squares 4 B + Adam 28 B per parameter
+    return {
+        "dense_layer": {
+            "workload": f"ELU(X [{n}x{k}] . W [{k}x{m}] + b), feature-major out [{m}x{n}]",
+            "kernel_us": t_layer * 1e6, "wall_us": t_layer_wall * 1e6,
+            "tflops": flop1 / t_layer / 1e12, "fp32_mfma_frac": flop1 / t_layer / 157.3e12,
+        },
+        "adam_clip": {
+            "workload": f"global grad-norm clip 1.0 + Adam over {npar} params (17 tensors)",
+            "warm_kernel_us": t_warm * 1e6, "cold_kernel_us": t_cold * 1e6, "wall_us": t_adam_wall * 1e6,
+            "warm_GBps": bytes3 / t_warm / 1e9, "cold_GBps": bytes3 / t_cold / 1e9,
+            "cold_hbm_frac": bytes3 / t_cold / 8e12,
+        },
+    }
+
+
 def gemm_flop_per_row(ad, cd):
     """Layer-GEMM FLOP per minibatch row of one update step: forward and
     weight gradient of every layer, data gradient of every layer above the
@@ -385,6 +465,7 @@ def main():
                                    "new batch buffers are read through a device pointer block"}
     if not args.no_aux:
         out["aux"] = aux_measurements(ctx, gac, ro, d_obs, LD, n)
+        out["aux"].update(operator_measurements(ctx))
         out["aux"]["trainer_nets_update"] = trainer_nets_measurement(ctx, max(2, min(args.steps, 5)))
 
         def values_and_gae():

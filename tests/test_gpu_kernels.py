@@ -242,6 +242,29 @@ def test_config1_single_layer(ctx):
     assert rel_amax(got, ref) <= FWD_BWD_TOL
 
 
+
+def test_config1_aligned_and_odd_stride_agree(ctx):
+    """The single layer through both feature-major tile paths: K = 123 (row
+    stride 123: scalar-load 64 x 64 tiles) and the same product with K
+    padded to 128 by zero columns / rows (float4 loads, 64 x 64 tiles). The
+    padded terms add exact zeros in the same 16-wide chunk order, so the two
+    outputs are bit-identical; both match the oracle."""
+    c1 = synth.config1()
+    x, w_kn, b = c1["x"], c1["w_kn"], c1["b"]
+    wp = np.zeros((512, 128), np.float32)
+    wp[:, :123] = w_kn.T
+    xp = np.zeros((128, 4096), np.float32)
+    xp[:123] = x.T
+    db = ctx.to_device(b)
+    o123, o128 = ctx.alloc((512, 4096)), ctx.alloc((512, 4096))
+    ops.gemm_bias_act(ctx, o123, ctx.to_device(w_kn.T.copy()), ctx.to_device(x.T.copy()), 512, 4096, 123, db, 1, True)
+    ops.gemm_bias_act(ctx, o128, ctx.to_device(wp), ctx.to_device(xp), 512, 4096, 128, db, 1, True)
+    a, p = o123.numpy(), o128.numpy()
+    params = np.concatenate([w_kn.T.ravel(), b, np.zeros(513, np.float32)]).astype(np.float32)
+    ref = zo.mlp_forward([123, 512, 1], params, x)[0]
+    assert np.array_equal(a, p)
+    assert rel_amax(p.T, ref) <= FWD_BWD_TOL
+
 def _mlp_case(ctx, dims, rows, seed, bias_bound=0.1):
     g = np.random.default_rng(seed)
     params = synth.kaiming_uniform_net(g, dims, bias_bound=bias_bound)

@@ -817,8 +817,8 @@ ZK_GEMM(zk_gemm_ak_bk_64x64x32_w22, true, true, 64, 64, 32, 2, 2, true)
 ZK_GEMM(zk_gemm_ak_bk_32x64x32_w12, true, true, 32, 64, 32, 1, 2, true)
 ZK_GEMM(zk_gemm_ak_bk_128x32x16_w41, true, true, 128, 32, 16, 4, 1, true)
 ZK_GEMM(zk_gemm_ak_bk_256x16x16_w41, true, true, 256, 16, 16, 4, 1, true)
-ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22, true, false, 64, 128, 16, 2, 2, true)
 ZK_GEMM(zk_gemm_ak_bn_96x128x32_w24, true, false, 96, 128, 32, 2, 4, true)
+ZK_GEMM(zk_gemm_ak_bn_64x64x32_w22, true, false, 64, 64, 32, 2, 2, true)
 // Data-gradient variant (ELU' operand prefetched), held to 4 waves per SIMD
 // so that two 8-wave blocks stay resident per CU.
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
@@ -846,6 +846,7 @@ ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, true)
 ZK_GEMM(zk_gemm_am_bk_64x128x16_w22, false, true, 64, 128, 16, 2, 2, true)
 ZK_GEMM(zk_gemm_ak_bk_64x128x16_w22_s, true, true, 64, 128, 16, 2, 2, false)
 ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22_s, true, false, 64, 128, 16, 2, 2, false)
+ZK_GEMM(zk_gemm_ak_bn_64x64x32_w22_s, true, false, 64, 64, 32, 2, 2, false)
 ZK_GEMM(zk_gemm_am_bn_64x128x16_w22_s, false, false, 64, 128, 16, 2, 2, false)
 ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, false)
 

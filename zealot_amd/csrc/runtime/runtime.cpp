@@ -34,7 +34,6 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bk_32x64x32_w12", true, true, 32, 64, 32, 128, true},
     {"zk_gemm_ak_bk_128x32x16_w41", true, true, 128, 32, 16, 256, true},
     {"zk_gemm_ak_bk_256x16x16_w41", true, true, 256, 16, 16, 256, true},
-    {"zk_gemm_ak_bn_64x128x16_w22", true, false, 64, 128, 16, 256, true},
     {"zk_gemm_ak_bn_96x128x32_w24", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bn_96x128x32_w24_dg", true, false, 96, 128, 32, 512, true},
     {"zk_gemm_ak_bk_96x128x32_w24_x", true, true, 96, 128, 32, 512, true},
@@ -53,6 +52,8 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_ak_bn_64x128x16_w22_s", true, false, 64, 128, 16, 256, false},
     {"zk_gemm_am_bn_64x128x16_w22_s", false, false, 64, 128, 16, 256, false},
     {"zk_gemm_am_bk_64x128x16_w22_s", false, true, 64, 128, 16, 256, false},
+    {"zk_gemm_ak_bn_64x64x32_w22", true, false, 64, 64, 32, 256, true},
+    {"zk_gemm_ak_bn_64x64x32_w22_s", true, false, 64, 64, 32, 256, false},
     {"zk_narrow_n1_v", true, true, kNarrowRows, 16, 16, 256, true, G_NARROW_N},
     {"zk_narrow_n2_v", true, true, kNarrowRows, 32, 16, 256, true, G_NARROW_N},
     {"zk_narrow_n1_s", true, true, kNarrowRows, 16, 16, 256, false, G_NARROW_N},
@@ -146,7 +147,9 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // Variant choice. The row-major forwards take the largest of 128 x 128,
 // 96 x 128, 64 x 64 and 32 x 64 tiles that still gives every CU a
 // workgroup; the data gradients 128 x 128 tiles where the rows divide into
-// them, else 96 x 128; the narrow output layers narrow-N tiles. The weight
+// them, else 96 x 128; other A-K-contiguous / B-N-contiguous products (the
+// feature-major layers, short-batch data gradients) 96 x 128 on long row
+// counts, else 64 x 64; the narrow output layers narrow-N tiles. The weight
 // gradients (M x N small, K = rows, split-K) use 128 x 128 tiles for the
 // 512- and 256-wide layers, 64 x 128 for the 128-wide one (both with 32-row
 // k-tiles, so that the k-loop's barrier sits between two chunks) and
@@ -164,6 +167,11 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
     if (lay == L_AM_BN && M <= 32) return gemm_id(M <= 16 ? "zk_narrow_m1" : "zk_narrow_m2");
   }
   if (!vec) {
+    if (forced && !kGemmTable[c->force_gemm[lay] - K_GEMM_BASE].vec) return c->force_gemm[lay];
+    // Feature-major layers with an odd reduction width (the single
+    // 4096-column 123 -> 512 layer: 25.7 -> 20.7 us) take 64 x 64 tiles while
+    // 64 x 128 ones would leave CUs with fewer than two workgroups.
+    if (lay == L_AK_BN && (long long)cdiv(M, 64) * cdiv(N, 128) < 512) return gemm_id("zk_gemm_ak_bn_64x64x32_w22_s");
     static const char* const kScalar[4] = {
         "zk_gemm_ak_bk_64x128x16_w22_s", "zk_gemm_ak_bn_64x128x16_w22_s",
         "zk_gemm_am_bn_64x128x16_w22_s", "zk_gemm_am_bk_64x128x16_w22_s"};
@@ -200,11 +208,16 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
       // Data gradients (ELU' epilogue) take the variant that prefetches the
       // activation operand: 128-row tiles where the rows divide into them
       // (24,576-row layer-1 / layer-2 backward 226.3 -> 224.6 / 71.9 ->
-      // 70.7 us), else 96-row tiles.
-      name = M >= 4096 ? (epi == zk::kEpiEluGrad ? (M % 128 == 0 ? "zk_gemm_ak_bn_128x128x32_w24_dg"
-                                                                  : "zk_gemm_ak_bn_96x128x32_w24_dg")
-                                                 : "zk_gemm_ak_bn_96x128x32_w24")
-                       : "zk_gemm_ak_bn_64x128x16_w22";
+      // 70.7 us), else 96-row tiles. The rest take 96 x 128 tiles on long
+      // row counts that give two workgroups per CU, else 64 x 64 (the
+      // feature-major 512 x 4096 x 128 layer 17.7 -> 14.8 us, 256 x 4096 x
+      // 512 35.6 -> 22.2 us, 8192 x 128 x 256 24.7 -> 15.1 us).
+      if (M >= 4096 && epi == zk::kEpiEluGrad)
+        name = M % 128 == 0 ? "zk_gemm_ak_bn_128x128x32_w24_dg" : "zk_gemm_ak_bn_96x128x32_w24_dg";
+      else if (M >= 4096 && (long long)cdiv(M, 96) * cdiv(N, 128) >= 512)
+        name = "zk_gemm_ak_bn_96x128x32_w24";
+      else
+        name = "zk_gemm_ak_bn_64x64x32_w22";
       break;
     case L_AM_BN:
       if (M >= 256)
