@@ -841,6 +841,10 @@ ZK_GEMM_X(zk_gemm_ak_bk_96x128x32_w24_x, true, true, 96, 128, 32, 2, 4, true, tr
 ZK_GEMM_X(zk_gemm_am_bn_128x128x32_w24_x, false, false, 128, 128, 32, 2, 4, true, true)
 ZK_GEMM_X(zk_gemm_am_bn_64x128x32_w24_x, false, false, 64, 128, 32, 2, 4, true, true)
 ZK_GEMM(zk_gemm_am_bn_64x128x32_w24, false, false, 64, 128, 32, 2, 4, true)
+ZK_GEMM(zk_gemm_am_bn_128x96x32_w42, false, false, 128, 96, 32, 4, 2, true)
+ZK_GEMM_X(zk_gemm_am_bn_128x96x32_w42_x, false, false, 128, 96, 32, 4, 2, true, true)
+ZK_GEMM(zk_gemm_am_bn_128x64x32_w42, false, false, 128, 64, 32, 4, 2, true)
+ZK_GEMM_X(zk_gemm_am_bn_128x64x32_w42_x, false, false, 128, 64, 32, 4, 2, true, true)
 ZK_GEMM(zk_gemm_am_bn_128x128x32_w24, false, false, 128, 128, 32, 2, 4, true)
 ZK_GEMM(zk_gemm_am_bn_32x128x16_w14, false, false, 32, 128, 16, 1, 4, true)
 ZK_GEMM(zk_gemm_am_bk_64x128x16_w22, false, true, 64, 128, 16, 2, 2, true)

@@ -47,6 +47,10 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_am_bn_64x128x32_w24", false, false, 64, 128, 32, 512, true},
     {"zk_gemm_am_bn_128x128x32_w24", false, false, 128, 128, 32, 512, true},
     {"zk_gemm_am_bn_32x128x16_w14", false, false, 32, 128, 16, 256, true},
+    {"zk_gemm_am_bn_128x96x32_w42", false, false, 128, 96, 32, 512, true},
+    {"zk_gemm_am_bn_128x96x32_w42_x", false, false, 128, 96, 32, 512, true},
+    {"zk_gemm_am_bn_128x64x32_w42", false, false, 128, 64, 32, 512, true},
+    {"zk_gemm_am_bn_128x64x32_w42_x", false, false, 128, 64, 32, 512, true},
     {"zk_gemm_am_bk_64x128x16_w22", false, true, 64, 128, 16, 256, true},
     {"zk_gemm_ak_bk_64x128x16_w22_s", true, true, 64, 128, 16, 256, false},
     {"zk_gemm_ak_bn_64x128x16_w22_s", true, false, 64, 128, 16, 256, false},
@@ -220,7 +224,14 @@ int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool v
         name = "zk_gemm_ak_bn_64x64x32_w22";
       break;
     case L_AM_BN:
-      if (M >= 256)
+      // Widths that 128-column tiles would leave partly empty but 96 or 64
+      // divide (the trainer nets' input layers: 265 -> 288 padded columns,
+      // 64 columns) take tiles that fit them exactly.
+      if (M >= 256 && N % 128 != 0 && N % 96 == 0)
+        name = "zk_gemm_am_bn_128x96x32_w42";
+      else if (M >= 256 && N % 128 != 0 && N % 64 == 0)
+        name = "zk_gemm_am_bn_128x64x32_w42";
+      else if (M >= 256)
         name = "zk_gemm_am_bn_128x128x32_w24";
       else if (M >= 96)
         name = "zk_gemm_am_bn_64x128x32_w24";
@@ -263,8 +274,13 @@ int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int 
     // (256 = one workgroup per CU: more slices buy no speed in the GEMM at
     // 24,576 rows and cost reduction traffic), keeping at least 8 k-tiles
     // per slice.
-    const int target = c ? c->splitk_target : 256;
+    int target = c ? c->splitk_target : 256;
     if (tiles >= target || kt < 16) return 1;
+    // Tiles narrower than 128 columns (the odd-width input layers, launched
+    // alone) whose slices would run past 16 k-tiles aim at two workgroups
+    // per CU (the trainer actor's 256 x 288 input layer: 59.0 -> 46.8 us;
+    // the critic's 512 x 64, 12 k-tiles per slice, stays: 24.5 us).
+    if (g.bn < 128 && cdiv(kt, cdiv(target, tiles)) > 16) target *= 2;
     s = std::min<long long>(cdiv(target, tiles), std::max<long long>(1, kt / 8));
   }
   s = std::max<long long>(1, std::min(s, kt));
