@@ -85,6 +85,16 @@ LARGE_CASES = [
     # (64x64 here, 32x64 when even that leaves CUs idle).
     (4001, 300, 76, False, True),
     (3001, 100, 132, False, True),
+    # Weight-gradient-shaped products (A M-contiguous, long K: split-K) whose
+    # widths 128-column tiles would leave partly empty: 128 x 96 and
+    # 128 x 64 tiles, exact-fit (256 x 288, 512 x 64) and masked (ragged M
+    # and K), and the feature-major 64 x 64 tiles with a ragged M.
+    (256, 288, 24576, True, False),
+    (512, 64, 24576, True, False),
+    (300, 96, 5000, True, False),
+    (260, 64, 7001, True, False),
+    (1000, 2000, 123, False, False),
+    (1000, 2000, 128, False, False),
 ]
 
 
@@ -95,7 +105,7 @@ def test_gemm_large_ragged(ctx, case):
     L = g.standard_normal((m, k)).astype(np.float32)
     R = g.standard_normal((k, n)).astype(np.float32)
     ref = L.astype(np.float64) @ R.astype(np.float64)
-    dl = ctx.to_device(L)
+    dl = ctx.to_device(L.T.copy() if lt else L)
     dr = ctx.to_device(R.T.copy() if rt else R)
     out = ctx.alloc((m, n))
     ops.gemm(ctx, out, dl, lt, dr, rt, m, n, k)
