@@ -10,7 +10,11 @@ semantics (src/bin/biped_train_gpu.rs:1164-1553), fixed learning rate and no
 KL early stop so every step does the same work.
 
 Prints ONE JSON line. `value` = PPO-update samples/s = 5 * 98,304 / t_step
-(sample-gradient evaluations per second).
+(sample-gradient evaluations per second). Unless --no-aux, `aux` adds the
+workloads around the update: the 4096-env rollout step, the observation
+normaliser, the single dense layer (4096 x 123 -> 512, ELU) and the clipped
+Adam step over the 459,323 parameters, the reference trainer's own nets and
+the update under ActorCritic::update semantics.
 """
 
 from __future__ import annotations
