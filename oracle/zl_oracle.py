@@ -75,6 +75,7 @@ def lib() -> C.CDLL:
         "zlo_ac_destroy": (None, [vp]),
         "zlo_ac_get": (None, [vp, vp, vp, vp, vp, vp]),
         "zlo_ac_set": (None, [vp, vp, vp, vp, fl]),
+        "zlo_ac_get_moments": (None, [vp, vp, vp, vp, vp, vp, vp, vp]),
         "zlo_ac_record_obs": (None, [vp, vp, vp]),
         "zlo_ac_mean": (None, [vp, vp, vp]),
         "zlo_ac_value": (fl, [vp, vp]),
@@ -298,6 +299,15 @@ class ActorCritic:
 
     def set(self, actor, critic, log_std, lr):
         lib().zlo_ac_set(self.h, _p(f32(actor)), _p(f32(critic)), _p(f32(log_std)), lr)
+
+    def moments(self):
+        """(m_actor, v_actor, m_critic, v_critic, m_logstd, v_logstd, [t_actor,
+        t_critic, t_logstd]); the net moments are packed like the parameters."""
+        na, nc = packed_count(self.actor_dims), packed_count(self.critic_dims)
+        out = [np.empty(k, np.float32) for k in (na, na, nc, nc, self.A, self.A)]
+        cnt = np.empty(3, np.int32)
+        lib().zlo_ac_get_moments(self.h, *[_p(x) for x in out], _p(cnt))
+        return out + [cnt]
 
     def mean(self, obs):
         out = np.empty(self.A, np.float32)

@@ -170,6 +170,38 @@ void zlo_ac_get(void* h, float* actor, float* critic, float* log_std, float* lr,
   if (t_logstd) *t_logstd = ac->t_logstd;
 }
 
+// Adam moments of both nets packed like Mlp::pack, the log_std moments, and
+// the three step counters (opt_actor.t, opt_critic.t, t_logstd).
+void zlo_ac_get_moments(void* h, float* ma, float* va, float* mc, float* vc, float* mls,
+                        float* vls, int* counters) {
+  ActorCritic* ac = (ActorCritic*)h;
+  auto pack = [](const Adam& a, float* m, float* v) {
+    for (size_t l = 0; l < a.mw.size(); ++l) {
+      if (m) {
+        std::memcpy(m, a.mw[l].data(), a.mw[l].size() * 4);
+        m += a.mw[l].size();
+        std::memcpy(m, a.mb[l].data(), a.mb[l].size() * 4);
+        m += a.mb[l].size();
+      }
+      if (v) {
+        std::memcpy(v, a.vw[l].data(), a.vw[l].size() * 4);
+        v += a.vw[l].size();
+        std::memcpy(v, a.vb[l].data(), a.vb[l].size() * 4);
+        v += a.vb[l].size();
+      }
+    }
+  };
+  pack(ac->opt_actor, ma, va);
+  pack(ac->opt_critic, mc, vc);
+  if (mls) std::memcpy(mls, ac->m_logstd.data(), ac->m_logstd.size() * 4);
+  if (vls) std::memcpy(vls, ac->v_logstd.data(), ac->v_logstd.size() * 4);
+  if (counters) {
+    counters[0] = ac->opt_actor.t;
+    counters[1] = ac->opt_critic.t;
+    counters[2] = ac->t_logstd;
+  }
+}
+
 void zlo_ac_set(void* h, const float* actor, const float* critic, const float* log_std,
                 float lr) {
   ActorCritic* ac = (ActorCritic*)h;

@@ -748,3 +748,286 @@ def test_minibatch_statistics_float64(seed):
     v = np_ref.forward(cd, critic, batch["critic_obs"])[-1][:, 0]
     vl_plain = float(np.mean((v - batch["ret"]) ** 2))
     assert abs(vl_plain - ref[1]) > 1e-3 * abs(ref[1])
+
+
+# ---- ActorCritic::update's epoch loop (zealot-rl/src/ppo.rs:338-384 and the
+# minibatch tail :464-510), pinned by a float64 restatement built only from
+# np_ref and the integer Lcg above (no oracle code).
+
+def _fisher_yates(seed, n):
+    """ppo.rs:358-363: Lcg::new(seed) (rng.rs:13-15 ORs in 1), then for
+    i = n-1 down to 1: j = (unit() * (i + 1) as f32) as usize, an f32 product
+    truncated toward zero, and swap(i, min(j, i))."""
+    u = lcg_units_int(seed, max(n - 1, 0))
+    order = np.arange(n)
+    for k, i in enumerate(range(n - 1, 0, -1)):
+        j = min(int(np.float32(u[k]) * np.float32(i + 1)), i)
+        order[i], order[j] = order[j], order[i]
+    return order
+
+
+def _ac_update_f64(ad, cd, actor, critic, log_std, batch, epochs, n_mb, lr, max_norm, clip, ent,
+                   vcoef, desired_kl, lr_lo, lr_hi, variant="ref"):
+    """ActorCritic::update from a fresh ActorCritic (t_logstd = 0, Adam t = 0,
+    zero moments, unit-prior normalisers: identity on |x| < 5) in float64.
+
+    Advantages normalised with the population variance and sd floor 1e-6
+    (:341-347); mb = n / minibatches (:349); per epoch a fresh Fisher-Yates
+    order from Lcg(t_logstd + 1) (:355-363); per minibatch the gradient at the
+    current parameters (np_ref), the mean-only KL driving the adaptive LR with
+    strict comparisons and lr_bounds (:476-482), each net clipped by its own
+    norm, log_std never clipped (:485-486), one Adam step per net with its own
+    t advanced per minibatch (net.rs:234-252), then log_std's Adam with its own
+    t and the clamp [-1.6, 1.0] (:496-510); the returned statistics are the
+    last epoch's minibatch means (:371-381), with the entropy of the log_std
+    each minibatch saw (:458).
+
+    `variant` restates one plausible misreading: 'seed_t' (Lcg(t_logstd)),
+    'one_shuffle' (the first epoch's order reused), 'ge' (>= in both LR
+    comparisons), 'avg_epochs' (statistics averaged over all epochs),
+    'clamp0' (log_std clamped to [-1.6, 0]), 'global_clip' (one norm over
+    actor + critic + log_std), 'no_clip', 'per_epoch_t' (the Adam t of the
+    nets advanced once per epoch and shared by its minibatches)."""
+    b = dict(batch)
+    a64 = np.asarray(batch["adv"], np.float64)
+    mu = a64.mean()
+    sd = max(np.sqrt(np.mean((a64 - mu) ** 2)), 1e-6)
+    b["adv"] = (a64 - mu) / sd
+    b["obs"] = np.clip(np.asarray(batch["obs"], np.float64), -5, 5)
+    b["critic_obs"] = np.clip(np.asarray(batch["critic_obs"], np.float64), -5, 5)
+    n = a64.size
+    mb = n // n_mb
+    p = [np.asarray(actor, np.float64).copy(), np.asarray(critic, np.float64).copy()]
+    ls = np.asarray(log_std, np.float64).copy()
+    m = [np.zeros_like(x) for x in p]
+    v = [np.zeros_like(x) for x in p]
+    mls, vls = np.zeros_like(ls), np.zeros_like(ls)
+    t_net, t_ls = 0, 0
+    epoch_stats, lr_trace, norms, first = [], [], [], None
+    for e in range(epochs):
+        order = _fisher_yates(t_ls if variant == "seed_t" else t_ls + 1, n)
+        if variant == "one_shuffle":
+            first = order if first is None else first
+            order = first
+        rows = []
+        for k in range(n_mb):
+            idx = order[k * mb:(k + 1) * mb]
+            ga, gc, gl, st = np_ref.minibatch_grads(ad, cd, p[0], p[1], ls, b, idx, clip, ent, vcoef)
+            entropy = float(np.sum(ls + 0.5 + np_ref.LOG_SQRT_2PI))
+            kl = float(st[2])
+            if variant == "ge":
+                if kl >= desired_kl * 2.0:
+                    lr = max(lr / 1.5, lr_lo)
+                elif kl >= 0.0 and kl <= desired_kl / 2.0:
+                    lr = min(lr * 1.5, lr_hi)
+            else:
+                if kl > desired_kl * 2.0:
+                    lr = max(lr / 1.5, lr_lo)
+                elif kl > 0.0 and kl < desired_kl / 2.0:
+                    lr = min(lr * 1.5, lr_hi)
+            lr_trace.append(lr)
+            na, nc = float(np.sqrt(np.sum(ga * ga))), float(np.sqrt(np.sum(gc * gc)))
+            norms.append((na, nc))
+            g = [ga, gc]
+            if variant == "global_clip":
+                tot = float(np.sqrt(na * na + nc * nc + np.sum(gl * gl)))
+                s = max_norm / tot if tot > max_norm else 1.0
+                g, gl = [ga * s, gc * s], gl * s
+            elif variant != "no_clip":
+                g = [x * (max_norm / nx) if (nx > max_norm and nx > 0) else x
+                     for x, nx in zip(g, (na, nc))]
+            t_net += 1
+            t = (e + 1) * n_mb if variant == "per_epoch_t" else t_net
+            bc1, bc2 = 1.0 - 0.9 ** t, 1.0 - 0.999 ** t
+            for i in range(2):
+                m[i] = 0.9 * m[i] + 0.1 * g[i]
+                v[i] = 0.999 * v[i] + 0.001 * g[i] * g[i]
+                p[i] = p[i] - lr * (m[i] / bc1) / (np.sqrt(v[i] / bc2) + 1e-8)
+            t_ls += 1
+            c1, c2 = 1.0 - 0.9 ** t_ls, 1.0 - 0.999 ** t_ls
+            mls = 0.9 * mls + 0.1 * gl
+            vls = 0.999 * vls + 0.001 * gl * gl
+            hi = 0.0 if variant == "clamp0" else 1.0
+            ls = np.clip(ls - lr * (mls / c1) / (np.sqrt(vls / c2) + 1e-8), -1.6, hi)
+            rows.append([kl, float(st[0]), float(st[1]), entropy])
+        epoch_stats.append(np.mean(rows, axis=0))
+    stats = np.mean(epoch_stats, axis=0) if variant == "avg_epochs" else epoch_stats[-1]
+    return dict(p=[p[0], p[1], ls], m=[m[0], m[1], mls], v=[v[0], v[1], vls],
+                t=(t_net, t_net, t_ls), lr=lr, stats=stats, lr_trace=lr_trace,
+                norms=np.array(norms))
+
+
+def _ac_case(seed, zero_head):
+    """48 samples of a [3,5,2] actor / [3,5,1] critic (three minibatches of
+    16). zero_head: the actor's output layer is zero, so its means are exactly
+    0 in float32 and float64 alike and the first minibatch's KL against
+    mean_old = 0 is exactly zero."""
+    g = np.random.default_rng(seed)
+    ad, cd = [3, 5, 2], [3, 5, 1]
+    actor = (g.standard_normal(zo.packed_count(ad)) * 0.5).astype(np.float32)
+    critic = (g.standard_normal(zo.packed_count(cd)) * 0.5).astype(np.float32)
+    if zero_head:
+        actor[-(5 * 2 + 2):] = 0.0
+    log_std = np.array([0.985, -0.3], np.float32)
+    n = 48
+    obs = g.standard_normal((n, 3)).astype(np.float32)
+    means = np_ref.forward(ad, actor, obs)[-1]
+    vals = np_ref.forward(cd, critic, obs)[-1][:, 0]
+    action = (means + 0.7 * g.standard_normal((n, 2))).astype(np.float32)
+    lp = np.sum(-0.5 * ((action - means) / np.exp(log_std.astype(np.float64))) ** 2
+                - log_std - 0.9189385, axis=1)
+    mean_old = means if zero_head else means + 0.1 * g.standard_normal((n, 2))
+    batch = dict(obs=obs, critic_obs=obs, action=action, mean_old=mean_old.astype(np.float32),
+                 logp_old=(lp + 0.02 * g.standard_normal(n)).astype(np.float32),
+                 value_old=(vals + 0.05).astype(np.float32),
+                 adv=(1.5 * g.standard_normal(n) + 0.4).astype(np.float32),
+                 ret=g.standard_normal(n).astype(np.float32))
+    return ad, cd, actor, critic, log_std, batch
+
+
+# lr 1e-2 in every case; desired_kl and lr_bounds pick the branch:
+#   down: every KL > 2 * desired -> lr / 1.5 down to the 5e-3 floor;
+#   up: 0 < KL < desired / 2 -> lr * 1.5 up to the 2e-2 ceiling;
+#   zero_first: the first KL is exactly 0 (no change, strict kl > 0), then up.
+_AC_CASES = {
+    "down": dict(seed=41, zero_head=False, desired_kl=1e-6, lr_lo=5e-3, lr_hi=1e-1,
+                 lr_trace=[1e-2 / 1.5, 5e-3, 5e-3, 5e-3, 5e-3, 5e-3]),
+    "up": dict(seed=43, zero_head=False, desired_kl=10.0, lr_lo=1e-5, lr_hi=2e-2,
+               lr_trace=[1.5e-2, 2e-2, 2e-2, 2e-2, 2e-2, 2e-2]),
+    "zero_first": dict(seed=47, zero_head=True, desired_kl=10.0, lr_lo=1e-5, lr_hi=3e-2,
+                       lr_trace=[1e-2, 1.5e-2, 2.25e-2, 3e-2, 3e-2, 3e-2]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_AC_CASES))
+def test_actor_critic_update_epoch_loop_float64(case):
+    """The oracle's ActorCritic::update over 2 epochs x 3 minibatches of 16
+    rows (zealot-rl/src/ppo.rs:338-384, 386-510) against _ac_update_f64:
+    parameters, Adam moments (linear in the clipped gradient, so they expose
+    each clip scale), step counters, the LR after every branch, and the
+    returned statistics. Both nets' clips fire on every minibatch, log_std[0]
+    runs into the 1.0 ceiling, and minibatch composition matters. Each
+    misreading restated in _ac_update_f64 lands far outside the bounds."""
+    c = _AC_CASES[case]
+    ad, cd, actor, critic, log_std, batch = _ac_case(c["seed"], c["zero_head"])
+    epochs, n_mb, lr, max_norm, clip, ent, vcoef = 2, 3, 1e-2, 0.05, 0.2, 0.3, 0.5
+    ac = zo.ActorCritic(ad, cd, 1.0, 1e-3, 1)
+    ac.set(actor, critic, log_std, lr)
+    cfg = zo.PpoCfg(0.99, 0.95, clip, ent, vcoef, epochs, n_mb, max_norm, c["desired_kl"],
+                    c["lr_lo"], c["lr_hi"], 1)
+    st, _ = ac.update(batch, cfg, nthreads=1, normalize_obs=True)
+    a1, c1, l1, lr1, t_ls = ac.get()
+    ma, va, mc, vc, mls, vls, cnt = ac.moments()
+    got = dict(p=[a1, c1, l1], m=[ma, mc, mls], v=[va, vc, vls], t=tuple(int(x) for x in cnt),
+               lr=lr1, stats=np.array([st[0], st[1], st[2], st[3]], np.float64))
+    p0 = [actor, critic, log_std]
+    args = (ad, cd, actor, critic, log_std, batch, epochs, n_mb, lr, max_norm, clip, ent, vcoef,
+            c["desired_kl"], c["lr_lo"], c["lr_hi"])
+
+    def dist(ref):
+        dp = max(rel_amax(got["p"][i].astype(np.float64) - p0[i], ref["p"][i] - p0[i]) for i in range(3))
+        dm = max(rel_amax(got["m"][i], ref["m"][i]) for i in range(3))
+        dv = max(rel_amax(got["v"][i], ref["v"][i]) for i in range(3))
+        ds = float(np.max(np.abs(got["stats"] - ref["stats"]) / np.maximum(np.abs(ref["stats"]), 1e-3)))
+        dl = abs(got["lr"] / ref["lr"] - 1.0)
+        return dp, dm, dv, ds, dl
+
+    ref = _ac_update_f64(*args)
+    # The test exercises what it claims: the LR branch and bounds, both clips
+    # on every minibatch, and the log_std ceiling.
+    assert np.allclose(ref["lr_trace"], c["lr_trace"], rtol=1e-12), ref["lr_trace"]
+    assert np.all(ref["norms"] > 2 * max_norm), ref["norms"]
+    assert ref["p"][2][0] == 1.0 and l1[0] == np.float32(1.0)
+    assert got["t"] == ref["t"] == (6, 6, 6) and t_ls == 6
+    dp, dm, dv, ds, dl = dist(ref)
+    assert dp < 1e-3 and dm < 1e-4 and dv < 2e-4 and ds < 1e-4 and dl < 1e-6, (dp, dm, dv, ds, dl)
+
+    misread = ["seed_t", "one_shuffle", "avg_epochs", "clamp0", "global_clip", "no_clip",
+               "per_epoch_t"] + (["ge"] if case == "zero_first" else [])
+    for variant in misread:
+        alt = _ac_update_f64(*args, variant=variant)
+        d = dist(alt)
+        assert max(d) > 2e-2, (variant, d)
+
+
+def test_fisher_yates_order_golden():
+    """The shuffle of ppo.rs:355-363 on 10 items from Lcg(1), written out in
+    integers from the golden Lcg stream: a permutation, stable per seed, and
+    different for the seed of the next epoch (t_logstd + 1 = 1 + minibatches)."""
+    o1 = _fisher_yates(1, 10)
+    assert sorted(o1.tolist()) == list(range(10))
+    u = [int(x) for x in (lcg_units_int(1, 9) * (1 << 24)).astype(np.int64)]
+    want = list(range(10))
+    for k, i in enumerate(range(9, 0, -1)):
+        j = min((u[k] * (i + 1)) >> 24, i)  # exact: (k / 2^24) * (i + 1) with no rounding at these sizes
+        want[i], want[j] = want[j], want[i]
+    assert o1.tolist() == want
+    assert not np.array_equal(o1, _fisher_yates(4, 10))
+    assert np.array_equal(_fisher_yates(0, 10), o1)  # seed | 1
+
+
+def test_actor_critic_logp_sample_closed_form():
+    """ActorCritic::logp (ppo.rs:297-305) = sum_k -1/2 ((a - mu) / e^ls)^2 - ls
+    - ln sqrt(2 pi), and ActorCritic::sample (:314-323) = mu + e^ls * gauss with
+    gauss drawn from the caller's Lcg in component order (Box-Muller of two
+    units each, rng.rs:29-32), its logp that of the drawn action; pinned in
+    float64 from the integer Lcg stream."""
+    g = np.random.default_rng(5)
+    ad, cd = [4, 6, 3], [4, 6, 1]
+    ac = zo.ActorCritic(ad, cd, 1.0, 1e-3, 1)
+    actor = (g.standard_normal(zo.packed_count(ad)) * 0.5).astype(np.float32)
+    log_std = np.array([-0.5, 0.3, -1.2], np.float32)
+    ac.set(actor, (g.standard_normal(zo.packed_count(cd)) * 0.5).astype(np.float32), log_std, 1e-3)
+    ls = log_std.astype(np.float64)
+    for _ in range(20):
+        a = g.standard_normal(3).astype(np.float32)
+        mu = g.standard_normal(3).astype(np.float32)
+        want = np.sum(-0.5 * ((a - mu.astype(np.float64)) / np.exp(ls)) ** 2 - ls - 0.5 * np.log(2 * np.pi))
+        assert ac.logp(a, mu) == pytest.approx(want, rel=2e-6, abs=2e-6)
+    # Dropping the -log sigma term or using sigma^2 in the quadratic term fails.
+    assert abs(np.sum(-0.5 * ((a - mu) / np.exp(ls)) ** 2 - 0.5 * np.log(2 * np.pi)) - want) > 0.1
+    obs = np.array([0.3, -1.1, 0.8, 2.0], np.float32)
+    seed = 77
+    state = np.array([seed | 1], np.uint64)
+    act, lp, mean = ac.sample(obs, state)
+    assert np.allclose(mean, np_ref.forward(ad, actor, obs[None])[-1][0], rtol=1e-5, atol=1e-6)
+    u = lcg_units_int(seed, 6).astype(np.float64)
+    gauss = np.sqrt(-2 * np.log(np.maximum(u[0::2], 1e-7))) * np.cos(2 * np.pi * u[1::2])
+    want_a = mean.astype(np.float64) + np.exp(ls) * gauss
+    assert np.allclose(act, want_a, rtol=1e-5, atol=1e-5)
+    want_lp = np.sum(-0.5 * ((act - mean.astype(np.float64)) / np.exp(ls)) ** 2 - ls - 0.5 * np.log(2 * np.pi))
+    assert lp == pytest.approx(want_lp, rel=1e-5, abs=1e-5)
+    # The stream advanced by exactly six units (two per component).
+    s = seed | 1
+    for _ in range(6):
+        s = (s * 6364136223846793005 + 1442695040888963407) & MASK64
+    assert int(state[0]) == s
+
+
+def test_trainer_lr_up_branch_and_ceiling():
+    """The GPU trainer's adaptive LR (src/bin/biped_train_gpu.rs:1494-1498):
+    with the per-epoch KL inside (0, desired / 2) the rate rises by 1.5 per
+    epoch up to lr_max, and each epoch's Adam steps use the rate set after the
+    previous epoch. Three epochs against three chained float64 epochs
+    (_trainer_epoch_f64 carries no moments across calls, so the chain is
+    compared on the first epoch's moments and the final LR and statistics)."""
+    ad, cd, actor, critic, log_std, batch = _trainer_case(53)
+    n_mb, lr = 3, 1e-2
+    tr = zo.Trainer(ad, cd, actor, critic, log_std, lr)
+    so = tr.update(batch, zo.TrainerCfg(0.2, 0.01, 1.0, 3, n_mb, 0.0, 10.0, 1e-5, 2e-2, 1, 1, 0))
+    _, _, _, lr1, gstep = tr.get()
+    assert gstep == 3 * n_mb and int(so[5]) == 3
+    assert lr1 == pytest.approx(2e-2, rel=1e-6)  # 1e-2 -> 1.5e-2 -> 2e-2 (cap) -> 2e-2
+    assert 0.0 < so[6] < 5.0
+    # One epoch: the rate is unchanged during the epoch and x1.5 after it.
+    tr1 = zo.Trainer(ad, cd, actor, critic, log_std, lr)
+    s1 = tr1.update(batch, zo.TrainerCfg(0.2, 0.01, 1.0, 1, n_mb, 0.0, 10.0, 1e-5, 2e-2, 1, 1, 0))
+    a1, c1, l1, lr_e1, _ = tr1.get()
+    assert lr_e1 == pytest.approx(1.5e-2, rel=1e-6)
+    ref = _trainer_epoch_f64(ad, cd, actor, critic, log_std, batch, n_mb, lr, 1e30, 0.2, 0.01, 1.0)
+    for got, want, p0 in ((a1, ref[0][0], actor), (c1, ref[0][1], critic), (l1, ref[0][2], log_std)):
+        assert rel_amax(got.astype(np.float64) - p0, want - p0) < 1e-3
+    # With the x1.5 applied inside the epoch (before its steps) the step sizes
+    # would be 1.5x larger.
+    fast = _trainer_epoch_f64(ad, cd, actor, critic, log_std, batch, n_mb, 1.5e-2, 1e30, 0.2, 0.01, 1.0)
+    assert rel_amax(a1.astype(np.float64) - actor, fast[0][0] - actor) > 0.2
