@@ -256,8 +256,18 @@ zl_status zl_norm_normalize(zl_ctx* ctx, const float* state, int dim, const floa
 
 /* A dense ELU MLP (hidden ELU, linear output) with device-resident weights,
  * Adam moments and activation buffers for up to `batch` rows: the GpuMlp of
- * src/bin/biped_train_gpu.rs:316-564, batch-major ([rows x dim]). */
+ * src/bin/biped_train_gpu.rs:316-564. zl_mlp_create takes the caller's
+ * input, output and output gradient batch-major ([rows x dim], a row stride). */
 zl_status zl_mlp_create(zl_ctx* ctx, const int* dims, int ndims, int batch, zl_mlp** out);
+/* flags = ZL_MLP_FEATURE_MAJOR: the input x, the output and the output
+ * gradient are feature-major [dim x rows] with a feature stride ld >= rows
+ * (element (row r, feature f) at f * ld + r), as GpuMlp keeps a[0], a[L] and
+ * delta[L-1] ([d[i] x m], src/bin/biped_train_gpu.rs:351-355, used as W.a at
+ * :382-394 and over delta at :436-492). Results are bit-identical to the
+ * batch-major handle given the same values at 16-byte aligned strides. */
+#define ZL_MLP_FEATURE_MAJOR 1
+zl_status zl_mlp_create_ex(zl_ctx* ctx, const int* dims, int ndims, int batch, int flags,
+                           zl_mlp** out);
 void zl_mlp_destroy(zl_mlp* mlp);
 /* Number of parameters in the packed layout w[0], b[0], w[1], b[1], ... with
  * w[l] row-major [dims[l+1] x dims[l]] (zealot-rl/src/net.rs:30-34). */
@@ -265,13 +275,21 @@ long long zl_mlp_num_params(const zl_mlp* mlp);
 /* Host packed params <-> device (GpuMlp::write_w / read_into, :541-563). */
 zl_status zl_mlp_write_weights(zl_mlp* mlp, const float* packed_host);
 zl_status zl_mlp_read_weights(zl_mlp* mlp, float* packed_host);
-/* Forward over `rows` input rows (device x, row stride ldx): all layer
- * activations stay resident for zl_mlp_backward (GpuMlp::forward, :364-422). */
+/* Forward over `rows` input rows (device x; batch-major: row stride
+ * ldx >= dims[0]; feature-major: feature stride ldx >= rows): all layer
+ * activations stay resident for zl_mlp_backward (GpuMlp::forward, :364-422).
+ * A batch-major x is borrowed (read again by zl_mlp_backward, as GpuMlp
+ * reads a[0]) and must stay valid until then; a feature-major x is staged
+ * into the handle's own buffer and may be released after the call. */
 zl_status zl_mlp_forward(zl_mlp* mlp, const float* x, int ldx, int rows);
-/* Device pointer to the output activations [rows x dims[L]] and its stride. */
+/* Device pointer to the output activations of the last forward and their
+ * stride: [rows x dims[L]] (row stride) or, feature-major, [dims[L] x rows]
+ * (feature stride; GpuMlp's a[L]). Owned by the handle. */
 const float* zl_mlp_output(const zl_mlp* mlp, int* ld_out);
-/* Backward of dL/dout (device, row stride ld_g) through the last forward:
- * weight/bias gradients summed over the rows (GpuMlp::backward, :423-500). */
+/* Backward of dL/dout (device; batch-major [rows x dims[L]] with row stride
+ * ld_g, or feature-major [dims[L] x rows] with feature stride ld_g >= rows)
+ * through the last forward: weight/bias gradients summed over the rows
+ * (GpuMlp::backward, :423-500). */
 zl_status zl_mlp_backward(zl_mlp* mlp, const float* g_out, int ld_g);
 /* Download the gradients of the last backward, packed like the params. */
 zl_status zl_mlp_read_grads(zl_mlp* mlp, float* packed_host);

@@ -324,6 +324,63 @@ def test_mlp_backward_vs_oracle(ctx, dims, rows):
     assert worst <= FWD_BWD_TOL
 
 
+@pytest.mark.parametrize("dims,rows,pad", [([123, 512, 256, 128, 29], 4096, 0),
+                                           ([265, 256, 256, 128, 12], 6000, 40),
+                                           ([17, 33, 2], 301, 3)])
+def test_mlp_feature_major_matches_batch_major(ctx, dims, rows, pad):
+    """zl_mlp_create_ex(ZL_MLP_FEATURE_MAJOR): the input, the output and the
+    output gradient as [dim x rows] with feature stride rows + pad, as GpuMlp
+    keeps a[0], a[L] and delta[L-1] (src/bin/biped_train_gpu.rs:351-355,
+    382-394, 436-492), in a handle sized for more rows than are used. The
+    stride padding holds NaN (never read). Output and gradients are
+    bit-identical to the batch-major handle on the same values at 16-byte
+    aligned row strides, and within 1e-4 of the oracle."""
+    g = np.random.default_rng(rows + 7)
+    params = synth.kaiming_uniform_net(g, dims, bias_bound=0.1)
+    x = np.clip(g.standard_normal((rows, dims[0])), -5, 5).astype(np.float32)
+    gout = (g.standard_normal((rows, dims[-1])) / rows).astype(np.float32)
+    ldx, ldg = -(-dims[0] // 4) * 4, -(-dims[-1] // 4) * 4
+    xb = np.zeros((rows, ldx), np.float32)
+    xb[:, :dims[0]] = x
+    gb = np.zeros((rows, ldg), np.float32)
+    gb[:, :dims[-1]] = gout
+    mb = GpuMlp(ctx, dims, rows)
+    mb.write_weights(params)
+    dxb = ctx.to_device(xb)  # borrowed by the batch-major handle until its backward
+    mb.forward(dxb, rows, ldx)
+    out_b = mb.output(rows)
+    mb.backward(ctx.to_device(gb), ldg)
+    grads_b = mb.read_grads()
+    ld = rows + pad
+    xf = np.full((dims[0], ld), np.nan, np.float32)
+    xf[:, :rows] = x.T
+    gf = np.full((dims[-1], ld), np.nan, np.float32)
+    gf[:, :rows] = gout.T
+    mf = GpuMlp(ctx, dims, rows + 7, feature_major=True)
+    mf.write_weights(params)
+    dxf = ctx.to_device(xf)
+    mf.forward(dxf, rows, ld)
+    del dxf  # the feature-major handle staged its own copy
+    out_f = mf.output(rows)
+    mf.backward(ctx.to_device(gf), ld)
+    grads_f = mf.read_grads()
+    ref = zo.mlp_forward(dims, params, x)[-1]
+    rg, _ = zo.mlp_backward(dims, params, x, gout)
+    o, worst = 0, 0.0
+    for l in range(len(dims) - 1):
+        for sz in (dims[l + 1] * dims[l], dims[l + 1]):
+            worst = max(worst, rel_amax(grads_f[o:o + sz], rg[o:o + sz]))
+            o += sz
+    e_fwd = rel_amax(out_f, ref)
+    print(f"[gpu] mlp feature-major {dims} x {rows} (ld {ld}): fwd err {e_fwd:.2e}, bwd worst {worst:.2e}, "
+          f"identical fwd {np.array_equal(out_f, out_b)} bwd {np.array_equal(grads_f, grads_b)}", flush=True)
+    assert np.array_equal(out_f, out_b)
+    assert np.array_equal(grads_f, grads_b)
+    assert e_fwd <= FWD_BWD_TOL and worst <= FWD_BWD_TOL
+    mb.close()
+    mf.close()
+
+
 def test_config3_adam_bit_exact(ctx):
     """Adam over actor + critic + log_std (config 3): 10 warm steps then one
     more, on identical gradients, vs net.rs:240-245 on the CPU. <= 2 ulp."""

@@ -181,6 +181,7 @@ SIGNATURES = {
     "zl_ppo_load_bytes": (C.c_int, [vp, vp, vp, C.c_int, vp, C.c_size_t]),
     "zl_checkpoint_dims": (C.c_int, [vp, C.c_size_t, ip, ip, ip, ip, C.c_int]),
     "zl_mlp_create": (C.c_int, [vp, ip, C.c_int, C.c_int, C.POINTER(vp)]),
+    "zl_mlp_create_ex": (C.c_int, [vp, ip, C.c_int, C.c_int, C.c_int, C.POINTER(vp)]),
     "zl_mlp_destroy": (None, [vp]),
     "zl_mlp_num_params": (C.c_longlong, [vp]),
     "zl_mlp_write_weights": (C.c_int, [vp, vp]),

@@ -681,6 +681,26 @@ __device__ void copy_rows_body(const CopyRowsArgs& p) {
   p.dst[r * p.ldd + c] = v;
 }
 
+// Out-of-place transpose (TransposeArgs): reads along a source row and
+// writes along a destination row, both coalesced, through a padded LDS tile.
+__device__ void transpose_body(const TransposeArgs& p) {
+  constexpr int T = kTransposeTile, P = kThreads / T;  // P rows per pass
+  __shared__ float tile[T][T + 1];
+  const long long i0 = (long long)blockIdx.y * T, j0 = (long long)blockIdx.x * T;
+  const int tx = threadIdx.x % T, ty = threadIdx.x / T;
+#pragma unroll
+  for (int u = 0; u < T / P; ++u) {
+    const long long i = i0 + ty + u * P, j = j0 + tx;
+    if (i < p.rows && j < p.cols) tile[ty + u * P][tx] = p.src[i * p.lds + j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < T / P; ++u) {
+    const long long j = j0 + ty + u * P, i = i0 + tx;
+    if (i < p.rows && j < p.cols) p.dst[j * p.ldd + i] = tile[tx][ty + u * P];
+  }
+}
+
 // ActorCritic::sample + logp (zealot-rl/src/ppo.rs:314-323, :297-305) with
 // the Gaussian noise supplied by the caller, A <= G: a lane group of G lanes
 // per row, lane k on action component k (coalesced row reads and writes);
@@ -948,6 +968,7 @@ ZK_KERNEL(zk_adv_norm, AdvNormArgs, adv_norm_body)
 ZK_KERNEL(zk_elu_backward, EluBwdArgs, elu_backward_body)
 ZK_KERNEL(zk_row_sum, RowSumArgs, row_sum_body)
 ZK_KERNEL(zk_copy_rows, CopyRowsArgs, copy_rows_body)
+ZK_KERNEL(zk_transpose, TransposeArgs, transpose_body)
 ZK_KERNEL(zk_sample, SampleArgs, sample_body)
 extern "C" __global__ __launch_bounds__(256) void zk_sample_g32(zk::SampleArgs p) { zk::sample_lanes_body<32>(p); }
 extern "C" __global__ __launch_bounds__(256) void zk_sample_g64(zk::SampleArgs p) { zk::sample_lanes_body<64>(p); }

@@ -357,6 +357,15 @@ struct CopyRowsArgs {
   const int* guard;
 };
 
+// zk_transpose: dst[j * ldd + i] = src[i * lds + j] for i < rows, j < cols,
+// 64 x 64 tiles through LDS (grid x over column tiles, y over row tiles).
+constexpr int kTransposeTile = 64;
+struct TransposeArgs {
+  const float* src;
+  float* dst;
+  long long rows, cols, lds, ldd;
+};
+
 struct SampleArgs {
   const float* mean;  // [rows x ldm]
   const float* log_std;

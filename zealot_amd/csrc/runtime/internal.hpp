@@ -52,6 +52,7 @@ enum KernelId : int {
   K_HEAD_FWD,
   K_HEAD_FWD_X,
   K_POLICY,
+  K_TRANSPOSE,
   K_GEMM_BASE
 };
 

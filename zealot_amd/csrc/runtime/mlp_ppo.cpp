@@ -389,17 +389,46 @@ struct zl_mlp {
   size_t ws_floats = 0;
   const float* x = nullptr;
   int ldx = 0, rows = 0;
+  // ZL_MLP_FEATURE_MAJOR: the caller's input, output and output gradient are
+  // [dim x rows] (GpuMlp's a[0], a[L] and delta[L-1]). The input and the
+  // output gradient are transposed into batch-major staging (xs, gtop), the
+  // output out of it (out_fm, stride ld_fm), so the GEMMs, their variants and
+  // split-K slicing -- and hence every result bit -- are those of the
+  // batch-major handle.
+  bool fm = false;
+  float *xs = nullptr, *gtop = nullptr, *out_fm = nullptr;
+  int ldxs = 0, ld_fm = 0;
 };
+
+namespace zl {
+// dst[j * ldd + i] = src[i * lds + j], i < rows, j < cols (zk_transpose).
+static zl_status transpose(zl_ctx* c, float* dst, long long ldd, const float* src, long long lds,
+                           long long rows, long long cols) {
+  zk::TransposeArgs a{};
+  a.src = src;
+  a.dst = dst;
+  a.rows = rows;
+  a.cols = cols;
+  a.lds = lds;
+  a.ldd = ldd;
+  const long long T = zk::kTransposeTile;
+  return launch(c, K_TRANSPOSE, (unsigned)cdiv(cols, T), (unsigned)cdiv(rows, T), 1, a);
+}
+}  // namespace zl
 
 extern "C" {
 
-zl_status zl_mlp_create(zl_ctx* c, const int* dims, int nd, int batch, zl_mlp** out) {
+zl_status zl_mlp_create_ex(zl_ctx* c, const int* dims, int nd, int batch, int flags,
+                           zl_mlp** out) {
   if (!c || !dims || !out || nd < 2 || batch < 1) return ZL_ERR_INVALID;
   *out = nullptr;
+  if (flags & ~ZL_MLP_FEATURE_MAJOR)
+    return fail(c, ZL_ERR_INVALID, "zl_mlp_create_ex: unknown flags 0x%x", flags);
   for (int i = 0; i < nd; ++i)
     if (dims[i] < 1) return fail(c, ZL_ERR_INVALID, "zl_mlp_create: dims[%d] = %d", i, dims[i]);
   zl_mlp* p = new zl_mlp();
   p->c = c;
+  p->fm = (flags & ZL_MLP_FEATURE_MAJOR) != 0;
   p->nl.build(dims, nd, 0);
   p->nflat = p->nl.end;
   const size_t bytes = (size_t)p->nflat * 4;
@@ -407,6 +436,19 @@ zl_status zl_mlp_create(zl_ctx* c, const int* dims, int nd, int batch, zl_mlp** 
   for (float** b : {&p->params, &p->grads, &p->m, &p->v}) {
     if (e == hipSuccess) e = hipMalloc((void**)b, bytes);
     if (e == hipSuccess) e = hipMemsetAsync(*b, 0, bytes, c->stream);
+  }
+  if (p->fm) {
+    // Staging rows are zero past the features (never written there).
+    const int L = p->nl.L;
+    p->ldxs = (int)round_up(dims[0], 4);
+    p->ld_fm = (int)round_up(batch, 4);
+    const size_t sz[3] = {(size_t)batch * p->ldxs, (size_t)batch * round_up(dims[L], 4),
+                          (size_t)dims[L] * p->ld_fm};
+    float** dst[3] = {&p->xs, &p->gtop, &p->out_fm};
+    for (int i = 0; i < 3; ++i) {
+      if (e == hipSuccess) e = hipMalloc((void**)dst[i], sz[i] * 4);
+      if (e == hipSuccess) e = hipMemsetAsync(*dst[i], 0, sz[i] * 4, c->stream);
+    }
   }
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   zl_status s = e == hipSuccess ? ZL_OK : fail(c, ZL_ERR_HIP, "zl_mlp_create: %s", hipGetErrorString(e));
@@ -424,11 +466,15 @@ zl_status zl_mlp_create(zl_ctx* c, const int* dims, int nd, int batch, zl_mlp** 
   return ZL_OK;
 }
 
+zl_status zl_mlp_create(zl_ctx* c, const int* dims, int nd, int batch, zl_mlp** out) {
+  return zl_mlp_create_ex(c, dims, nd, batch, 0, out);
+}
+
 void zl_mlp_destroy(zl_mlp* p) {
   if (!p) return;
   if (p->c && p->c->stream) hipStreamSynchronize(p->c->stream);
   p->nb.release();
-  for (float* b : {p->params, p->grads, p->m, p->v, p->ws})
+  for (float* b : {p->params, p->grads, p->m, p->v, p->ws, p->xs, p->gtop, p->out_fm})
     if (b) hipFree(b);
   delete p;
 }
@@ -486,27 +532,50 @@ zl_status zl_mlp_write_moments(zl_mlp* p, const float* mh, const float* vh) {
 
 zl_status zl_mlp_forward(zl_mlp* p, const float* x, int ldx, int rows) {
   if (!p) return ZL_ERR_INVALID;
-  if (!x || rows < 1 || rows > p->nb.rows || ldx < p->nl.dims[0])
+  const int L = p->nl.L;
+  // Batch-major x: ldx >= dims[0] (row stride); feature-major: ldx >= rows.
+  if (!x || rows < 1 || rows > p->nb.rows || ldx < (p->fm ? rows : p->nl.dims[0]))
     return fail(p->c, ZL_ERR_INVALID, "zl_mlp_forward: rows %d (batch %d), ldx %d", rows,
                 p->nb.rows, ldx);
-  p->x = x;
-  p->ldx = ldx;
   p->rows = rows;
-  return net_forward(p->c, p->nl, p->nb, p->params, x, ldx, nullptr, rows, nullptr);
+  if (!p->fm) {
+    p->x = x;
+    p->ldx = ldx;
+    return net_forward(p->c, p->nl, p->nb, p->params, x, ldx, nullptr, rows, nullptr);
+  }
+  p->x = p->xs;
+  p->ldx = p->ldxs;
+  zl_status s = transpose(p->c, p->xs, p->ldxs, x, ldx, p->nl.dims[0], rows);
+  if (!s) s = net_forward(p->c, p->nl, p->nb, p->params, p->xs, p->ldxs, nullptr, rows, nullptr);
+  if (!s) s = transpose(p->c, p->out_fm, p->ld_fm, p->nb.act[L], p->nb.ld[L], rows, p->nl.dims[L]);
+  return s;
 }
 
 const float* zl_mlp_output(const zl_mlp* p, int* ld_out) {
   if (!p) return nullptr;
+  if (p->fm) {
+    if (ld_out) *ld_out = p->ld_fm;
+    return p->out_fm;
+  }
   if (ld_out) *ld_out = p->nb.ld[p->nl.L];
   return p->nb.act[p->nl.L];
 }
 
 zl_status zl_mlp_backward(zl_mlp* p, const float* g_out, int ld_g) {
   if (!p) return ZL_ERR_INVALID;
-  if (!g_out || !p->x || ld_g < p->nl.dims[p->nl.L])
+  const int L = p->nl.L;
+  if (!g_out || !p->x || ld_g < (p->fm ? p->rows : p->nl.dims[L]))
     return fail(p->c, ZL_ERR_INVALID, "zl_mlp_backward: no forward or bad gradient");
+  const float* top = g_out;
+  int ld_top = ld_g;
+  if (p->fm) {
+    top = p->gtop;
+    ld_top = p->nb.ld[L];
+    zl_status s = transpose(p->c, p->gtop, ld_top, g_out, ld_g, p->nl.dims[L], p->rows);
+    if (s) return s;
+  }
   return net_backward(p->c, p->nl, p->nb, p->params, p->grads, p->x, p->ldx, nullptr, p->rows,
-                      g_out, ld_g, nullptr, p->ws, p->ws_floats);
+                      top, ld_top, nullptr, p->ws, p->ws_floats);
 }
 
 zl_status zl_mlp_adam(zl_mlp* p, float lr, float bc1, float bc2) {

@@ -103,16 +103,25 @@ class PpoStats:
     grad_norm: tuple
 
 
-class GpuMlp:
-    """Device-resident MLP (the GpuMlp of src/bin/biped_train_gpu.rs:316-564)."""
+MLP_FEATURE_MAJOR = 1  # ZL_MLP_FEATURE_MAJOR
 
-    def __init__(self, ctx: Context, dims, batch: int):
+
+class GpuMlp:
+    """Device-resident MLP (the GpuMlp of src/bin/biped_train_gpu.rs:316-564).
+    feature_major: inputs, outputs and output gradients are [dim x rows]
+    with a feature stride (GpuMlp's a[0], a[L], delta[L-1]); otherwise
+    [rows x dim] with a row stride."""
+
+    def __init__(self, ctx: Context, dims, batch: int, feature_major: bool = False):
         self.ctx = ctx
         self.dims = [int(d) for d in dims]
         self.batch = int(batch)
+        self.fm = bool(feature_major)
         d = (C.c_int * len(self.dims))(*self.dims)
         h = C.c_void_p()
-        ctx.check(ctx.lib.zl_mlp_create(ctx.h, d, len(self.dims), self.batch, C.byref(h)), "zl_mlp_create")
+        flags = MLP_FEATURE_MAJOR if self.fm else 0
+        ctx.check(ctx.lib.zl_mlp_create_ex(ctx.h, d, len(self.dims), self.batch, flags, C.byref(h)),
+                  "zl_mlp_create_ex")
         self.h = h
         self.n_params = int(ctx.lib.zl_mlp_num_params(h))
 
@@ -127,20 +136,24 @@ class GpuMlp:
         return out
 
     def forward(self, x: DeviceBuffer, rows: int, ldx: int | None = None):
-        ldx = self.dims[0] if ldx is None else ldx
+        if ldx is None:
+            ldx = rows if self.fm else self.dims[0]
         self.ctx.check(self.ctx.lib.zl_mlp_forward(self.h, x.p, ldx, rows), "zl_mlp_forward")
 
     def output(self, rows: int) -> np.ndarray:
+        """The last forward's output as a host [rows x dims[-1]] array (either layout)."""
         ld = C.c_int()
         p = self.ctx.lib.zl_mlp_output(self.h, C.byref(ld))
-        buf = np.empty((rows, ld.value), np.float32)
+        shape = (self.dims[-1], ld.value) if self.fm else (rows, ld.value)
+        buf = np.empty(shape, np.float32)
         self.ctx.check(
             self.ctx.lib.zl_download(self.ctx.h, _fptr(buf), C.c_void_p(p), buf.nbytes), "download"
         )
-        return buf[:, : self.dims[-1]].copy()
+        return buf[:, :rows].T.copy() if self.fm else buf[:, : self.dims[-1]].copy()
 
-    def backward(self, g_out: DeviceBuffer, ld_g: int | None = None):
-        ld_g = self.dims[-1] if ld_g is None else ld_g
+    def backward(self, g_out: DeviceBuffer, ld_g: int | None = None, rows: int | None = None):
+        if ld_g is None:
+            ld_g = (rows if rows is not None else self.batch) if self.fm else self.dims[-1]
         self.ctx.check(self.ctx.lib.zl_mlp_backward(self.h, g_out.p, ld_g), "zl_mlp_backward")
 
     def read_grads(self) -> np.ndarray:
