@@ -10,7 +10,10 @@ semantics (src/bin/biped_train_gpu.rs:1164-1553), fixed learning rate and no
 KL early stop so every step does the same work.
 
 Prints ONE JSON line. `value` = PPO-update samples/s = 5 * 98,304 / t_step
-(sample-gradient evaluations per second). Unless --no-aux, `aux` adds the
+(sample-gradient evaluations per second). `self_check` reports the post-run
+check of the trained state (finite values, critic values against a float64
+forward, the first Adam moment of one more step against the minibatch
+gradient); the process exits 1 when it fails. Unless --no-aux, `aux` adds the
 workloads around the update: the 4096-env rollout step, the observation
 normaliser, the single dense layer (4096 x 123 -> 512, ELU) and the clipped
 Adam step over the 459,323 parameters, the reference trainer's own nets and
@@ -66,6 +69,78 @@ def cpu_baseline(ro, actor, critic, log_std, mean_old, action, logp_old, values,
             "sample": f"the same full update ({EPOCHS} epochs x {MINIBATCHES} minibatches of "
                       f"{n // MINIBATCHES} rows, fwd+bwd+clip+Adam, GPU-trainer semantics) on "
                       f"{threads} threads: {dt:.1f} s"}
+
+
+def _np_forward(dims, packed, x):
+    """float64 forward of a packed MLP (w[l] row-major [out x in], then b[l];
+    hidden ELU, linear output: zealot-rl/src/net.rs:88-108)."""
+    a, o = np.asarray(x, np.float64), 0
+    for l in range(len(dims) - 1):
+        out, inp = dims[l + 1], dims[l]
+        w = packed[o:o + out * inp].reshape(out, inp).astype(np.float64)
+        o += out * inp
+        a = a @ w.T + packed[o:o + out].astype(np.float64)
+        o += out
+        if l < len(dims) - 2:
+            a = np.where(a > 0, a, np.expm1(np.minimum(a, 0.0)))
+    return a
+
+
+def self_check(ctx, gac, obs, d_obs, ld, n, mb, batch_ptrs, stats):
+    """Post-run check of the timed update, outside the timed region (the
+    reference harness checks its result after the timed loop,
+    src/bin/iter_e2e_bench.rs:815-829):
+    * the trained parameters, the Adam moments and the update's statistics
+      are finite;
+    * critic values of 1,024 rows spread over the rollout against a float64
+      forward of the trained critic: max |err| / max |v| <= 1e-4;
+    * one more update of one minibatch (rows [0, mb), the normalised
+      advantages the timed updates wrote back) from the trained parameters
+      with fresh moments leaves Adam's first moment at (1 - beta1) * s * g,
+      where g is zl_ppo_minibatch_grads' gradient of the same rows and s the
+      global clip factor min(1, 1 / |g|): max |err| / max |m| <= 1e-4 for the
+      actor, the critic and log_std.
+    Leaves the handle's parameters one step further on."""
+    from zealot_amd import synth
+    from zealot_amd.rl import PpoConfig, _ffi
+
+    ad, cd = gac.actor_dims, gac.critic_dims
+    a, c, ls, lr = gac.get_params()
+    mom = gac.get_moments()
+    st = [stats.kl, stats.surrogate, stats.value_loss, stats.entropy, stats.lr, stats.last_kl]
+    finite = bool(all(np.all(np.isfinite(x)) for x in (a, c, ls, *mom)) and np.all(np.isfinite(st)))
+    rows = np.linspace(0, n - 1, 1024).astype(np.int64)
+    d_v = ctx.alloc(n)
+    gac.values(d_obs, n, d_v, ld=ld)
+    v = d_v.numpy()[rows].astype(np.float64)
+    v_ref = _np_forward(cd, c, obs[rows])[:, 0]
+    err_v = float(np.max(np.abs(v - v_ref)) / max(np.max(np.abs(v_ref)), 1e-30))
+    # One minibatch: its gradient, then one update step over the same rows.
+    (obs_p, ld_obs, cobs_p, ld_cobs, act_p, ld_act, mean_p, ld_mean, logp_p, val_p, adv_p, ret_p) = batch_ptrs
+    one = _ffi.zl_batch(mb, obs_p, ld_obs, cobs_p, ld_cobs, act_p, ld_act, mean_p, ld_mean, logp_p, val_p,
+                        adv_p, ret_p)
+    cfg = PpoConfig.gpu_trainer(epochs=1, minibatches=1, clip=0.2, entropy_coef=0.005, value_coef=1.0,
+                                max_grad_norm=1.0, adaptive_lr=False, early_stop=False, normalize_adv=False,
+                                clamp_log_std=False).to_c()
+    st3 = (C.c_float * 3)()
+    ctx.check(ctx.lib.zl_ppo_minibatch_grads(gac.h, C.byref(one), C.byref(cfg), 0, mb, None, st3), "grads")
+    ga, gc, gl = np.empty(gac.na, np.float32), np.empty(gac.nc, np.float32), np.empty(len(ls), np.float32)
+    ctx.check(ctx.lib.zl_ppo_get_grads(gac.h, ga.ctypes.data_as(C.c_void_p), gc.ctypes.data_as(C.c_void_p),
+                                       gl.ctypes.data_as(C.c_void_p)), "get_grads")
+    gac.reset_optimizer()
+    out = _ffi.zl_ppo_stats()
+    ctx.check(ctx.lib.zl_ppo_update(gac.h, C.byref(one), C.byref(cfg), C.byref(out)), "update")
+    ma, _, mc, _, mls, _ = gac.get_moments()
+    g = [x.astype(np.float64) for x in (ga, gc, gl)]
+    norm = np.sqrt(sum(float(np.sum(x * x)) for x in g))
+    s = min(1.0, 1.0 / norm) if norm > 0 else 1.0
+    err_m = {}
+    for name, m, gx in (("actor", ma, g[0]), ("critic", mc, g[1]), ("log_std", mls, g[2])):
+        want = 0.1 * s * gx
+        err_m[name] = float(np.max(np.abs(m - want)) / max(np.max(np.abs(want)), 1e-30))
+    ok = finite and err_v <= 1e-4 and max(err_m.values()) <= 1e-4
+    return {"pass": bool(ok), "finite": finite, "critic_values_rel_err": err_v,
+            "first_step_moment_rel_err": err_m, "grad_norm": norm, "clip_scale": s}
 
 
 def _timed(ctx, fn, reps):
@@ -479,19 +554,24 @@ def main():
 
         out["aux"]["actor_critic_update"] = actor_critic_measurement(ctx, gac, batch, values_and_gae,
                                                                      max(2, min(args.steps, 5)))
+    cpu_inputs = None
     if not args.no_cpu_baseline:
-        mean_old = d_mean.numpy()
-        action = d_act.numpy()
-        logp_old = d_logp.numpy()
-        values = d_val.numpy()
-        adv = d_adv.numpy()
-        ret = d_ret.numpy()
+        # The baseline's inputs as they stand after the timed updates.
         a_now, c_now, ls_now, _ = gac.get_params()
-        out["cpu_baseline"] = cpu_baseline(ro, a_now, c_now, ls_now, mean_old, action, logp_old,
-                                           values, (adv, ret))
+        cpu_inputs = (ro, a_now, c_now, ls_now, d_mean.numpy(), d_act.numpy(), d_logp.numpy(),
+                      d_val.numpy(), (d_adv.numpy(), d_ret.numpy()))
+    out["self_check"] = self_check(
+        ctx, gac, ro["obs"], d_obs, LD, n, mb,
+        (d_obs.ptr, LD, d_obs.ptr, LD, d_act.ptr, ad[-1], d_mean.ptr, ad[-1], d_logp.ptr, d_val.ptr,
+         d_adv.ptr, d_ret.ptr), stats)
+    if cpu_inputs is not None:
+        out["cpu_baseline"] = cpu_baseline(*cpu_inputs)
     gac.close()
     ctx.close()
     print(json.dumps(out), flush=True)
+    if not out["self_check"]["pass"]:
+        print("bench.py: post-run self-check failed: " + json.dumps(out["self_check"]), file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

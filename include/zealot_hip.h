@@ -177,12 +177,16 @@ zl_status zl_grad_clip_scale(zl_ctx* ctx, const zl_tensor* tensors, int count, f
 /* zl_grad_clip_scale without any allocation: no counterpart in the reference.
  * For callers that cannot allocate device memory (code under HIP graph
  * capture, serving or training loops that forbid hipMalloc). Same results,
- * bit for bit, as zl_grad_clip_scale. Its partial sums live in one static
- * device array per GPU of 16,384 floats (64 KiB, held until the process
- * ends): one partial per 2,048 elements of each tensor (at least one per
- * tensor), so about 33.5 M gradient elements per call at most; larger inputs
- * are refused with ZL_ERR_INVALID. Calls on one GPU share that array: calls
- * that overlap in time on one GPU (other streams or contexts) race. */
+ * bit for bit, as zl_grad_clip_scale. Its partial sums live in a static
+ * device array per GPU (256 KiB, held until the process ends) of 4 slots of
+ * 16,384 floats: one partial per 2,048 elements of each tensor (at least one
+ * per tensor), so about 33.5 M gradient elements per call at most; larger
+ * inputs are refused with ZL_ERR_INVALID. zl_init claims one slot for the
+ * context and zl_destroy returns it: the calls of one context are ordered on
+ * its stream and never share partials with another context's. With 4
+ * contexts alive on a GPU, a fifth gets ZL_ERR_INVALID from this entry point
+ * (its other entry points work) until one is destroyed. Each call leaves its
+ * slot holding its partials; nothing needs clearing between calls. */
 zl_status zl_grad_clip_scale_noalloc(zl_ctx* ctx, const zl_tensor* tensors, int count,
                                      float max_norm, float* scale_dev, float* norm_dev);
 
@@ -411,8 +415,18 @@ zl_status zl_ppo_get_grads(zl_ppo* ppo, float* actor, float* critic, float* log_
  * eps[r * A + k], logp[r] = ActorCritic::logp(action, mean) (ppo.rs:297-306)
  * and value[r] = critic(critic_obs_r). mean (row stride ld_mean) and value
  * may be NULL; critic_obs and critic_norm are only read when value is not
- * NULL. Asynchronous on the context's stream; rows go through the nets in
- * minibatch-sized chunks. */
+ * NULL. Asynchronous on the context's stream.
+ * Launch forms (same results either way): up to 8,192 rows, when the nets
+ * used fit, the whole step is ONE zk_policy launch (normalise, every layer
+ * with the activations in LDS, sampling, logp, value). A net fits when it
+ * has at most 8 layers, input and hidden widths up to 512 with hidden widths
+ * multiples of 16, at most 32 outputs, and layer-0 weight rows padded to a
+ * multiple of 16 (the handle pads them itself when that adds at most 1/8,
+ * e.g. 123 -> 128). Otherwise, and for larger n, the rows go through the
+ * layer GEMMs in minibatch-sized chunks with separate normalise and sampling
+ * launches. The environment variable ZL_POLICY_FUSED=0 (read at zl_init)
+ * turns the single-launch form off; zl_ppo_values and zl_ppo_actor_mean
+ * follow the same rule per net. */
 zl_status zl_ppo_act(zl_ppo* ppo, const float* obs_norm, const float* obs, int ld_obs,
                      const float* critic_norm, const float* critic_obs, int ld_critic_obs,
                      long long n, const float* eps, float* action, float* logp, float* mean,

@@ -19,19 +19,19 @@ from zealot_amd.rl import DeviceBatch, GpuActorCritic, PpoConfig, packed_count
 pytestmark = pytest.mark.gpu
 
 
-def _batch(ctx, batch, fm):
+def _batch(ctx, batch, fm, pad=0):
     return DeviceBatch(ctx, batch["obs"], batch["critic_obs"], batch["action"], batch["mean_old"],
                        batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"],
-                       feature_major=fm)
+                       feature_major=fm, pad=pad)
 
 
-def _run_update(ctx, actor, critic, log_std, batch, cfg, fm, gac=None):
+def _run_update(ctx, actor, critic, log_std, batch, cfg, fm, gac=None, pad=0):
     own = gac is None
     if own:
         gac = GpuActorCritic(ctx, SMALL_A, SMALL_C, batch["obs"].shape[0] // cfg.minibatches)
     gac.set_params(actor, critic, log_std, 1e-3)
     gac.reset_optimizer()
-    db = _batch(ctx, batch, fm)
+    db = _batch(ctx, batch, fm, pad)
     st = gac.update(db, cfg)
     out = gac.get_params(), gac.get_moments(), gac.counters(), st, db.adv.numpy()
     if own:
@@ -60,6 +60,28 @@ def test_update_feature_major_batch_is_bit_identical(ctx, semantics):
     assert bm[3] == fm[3]
     assert np.array_equal(bm[4], fm[4])
     # ... and the parameters moved (the comparison is not vacuous).
+    assert np.max(np.abs(bm[0][0] - actor)) > 1e-4
+
+
+@pytest.mark.parametrize("semantics", ["actor_critic", "gpu_trainer"])
+def test_update_feature_major_strided_capacity(ctx, semantics):
+    """Feature-major fields in tensors sized for a larger capacity: [dim x cap]
+    with stride cap = n + 37 (a trainer buffer allocated for more samples than
+    this update holds), the padding NaN. Bit-identical to the dense
+    batch-major run."""
+    actor, critic, log_std, batch = _small_problem(41, n=4096)
+    if semantics == "actor_critic":
+        cfg = PpoConfig(epochs=2, minibatches=4, shuffle=True, normalize_adv=True)
+    else:
+        cfg = PpoConfig.gpu_trainer(epochs=2, minibatches=4, desired_kl=100.0, lr_max=2e-3)
+    bm = _run_update(ctx, actor, critic, log_std, batch, cfg, False)
+    fm = _run_update(ctx, actor, critic, log_std, batch, cfg, True, pad=37)
+    for x, y in zip(bm[0][:3], fm[0][:3]):
+        assert np.array_equal(x, y)
+    for x, y in zip(bm[1], fm[1]):
+        assert np.array_equal(x, y)
+    assert bm[0][3] == fm[0][3] and bm[2] == fm[2] and bm[3] == fm[3]
+    assert np.array_equal(bm[4], fm[4])
     assert np.max(np.abs(bm[0][0] - actor)) > 1e-4
 
 
@@ -99,12 +121,13 @@ def test_minibatch_grads_feature_major_with_perm(ctx):
     gac.set_params(actor, critic, log_std, 1e-3)
     dperm = ctx.to_device(perm)
     res = []
-    for fm in (False, True):
-        db = _batch(ctx, batch, fm)
+    for fm, pad in ((False, 0), (True, 0), (True, 53)):  # 53: [dim x (n + 53)] capacity stride
+        db = _batch(ctx, batch, fm, pad)
         res.append(gac.minibatch_grads(db, PpoConfig(entropy_coef=0.01), 700, 1500, perm=dperm))
-    for x, y in zip(res[0][:3], res[1][:3]):
-        assert np.array_equal(x, y)
-    assert res[0][3] == res[1][3]
+    for r in res[1:]:
+        for x, y in zip(res[0][:3], r[:3]):
+            assert np.array_equal(x, y)
+        assert res[0][3] == r[3]
     idx = perm[700:2200]
     ra, rc, rl, rst = zo.minibatch_grads(SMALL_A, SMALL_C, actor, critic, log_std, batch, idx, 0.2, 0.01, 1.0)
     assert rel_amax(res[0][0], ra) <= 1e-4 and rel_amax(res[0][1], rc) <= 1e-4
@@ -148,10 +171,12 @@ def test_update_new_buffers_without_recapture(ctx):
 
 def test_update_graph_survives_buffer_growth(ctx):
     """A buffer the captured update uses is reallocated by another entry point
-    (the rollout step's staging grows for a larger chunk, minibatch_grads
-    re-lays the split-K partials): the next update must not replay a graph
-    that points at freed memory. It re-captures and matches the eager
-    (timed) update bit for bit."""
+    (a full-capacity minibatch_grads re-lays the split-K partial buffer the
+    update's graph reads): the next update must not replay a graph that
+    points at freed memory. It re-captures and matches the eager (timed)
+    update bit for bit. The rollout step run in between (one zk_policy launch
+    at 2048 rows) grows nothing; it checks that such a call leaves the update
+    unchanged."""
     actor, critic, log_std, batch = _small_problem(31, n=2048)
     gac = GpuActorCritic(ctx, SMALL_A, SMALL_C, 2048)
     cfg = PpoConfig(epochs=1, minibatches=4)

@@ -67,3 +67,41 @@ def test_noalloc_clip_scale_refuses_oversize(ctx):
     big.upload(np.full(n, 1e-4, np.float32))
     res = _both(ctx, ok, 1, 1.0)
     assert res[0] == res[1]
+
+
+def test_noalloc_slots_per_context(ctx):
+    """Every context claims one of the 4 static slots at zl_init: with 4
+    contexts alive (the session's and 3 more) a fifth context's call is
+    refused with ZL_ERR_INVALID, naming the slots; destroying one context
+    frees its slot for the next. Each context's result matches its own
+    allocating call."""
+    from zealot_amd import Context
+
+    g = np.random.default_rng(5)
+    extra = [Context(0) for _ in range(3)]
+    fifth = Context(0)
+    try:
+        for i, c in enumerate(extra):
+            buf = c.to_device((g.standard_normal(7000) * (i + 1)).astype(np.float32))
+            arr, count = _tensors(buf, [3000, 4000])
+            res = _both(c, arr, count, 1.0)
+            assert res[0] == res[1], (i, res)
+        buf = fifth.to_device(np.ones(100, np.float32))
+        arr, count = _tensors(buf, [100])
+        scale = fifth.alloc(1)
+        st = fifth.lib.zl_grad_clip_scale_noalloc(fifth.h, arr, count, 1.0, scale.p, None)
+        assert st == _ffi.ZL_ERR_INVALID
+        assert b"slots" in fifth.lib.zl_last_error(fifth.h)
+        extra.pop().close()
+        again = Context(0)
+        try:
+            buf2 = again.to_device(np.full(100, 0.5, np.float32))
+            arr2, count2 = _tensors(buf2, [100])
+            res = _both(again, arr2, count2, 1.0)
+            assert res[0] == res[1] and res[0][1] == np.float32(5.0)
+        finally:
+            again.close()
+    finally:
+        fifth.close()
+        for c in extra:
+            c.close()

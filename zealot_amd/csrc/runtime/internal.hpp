@@ -165,7 +165,8 @@ struct zl_ctx {
   bool fused_policy = true;
   // Device address of the allocation-free scratch array on this context's
   // device (zl_grad_clip_scale_noalloc), set at zl_init.
-  float* noalloc_scratch = nullptr;
+  float* noalloc_scratch = nullptr;  // this context's slot of the array
+  int noalloc_slot = -1;
   hipError_t noalloc_err = hipSuccess;
 };
 
@@ -271,6 +272,8 @@ zl_status launch_sample(zl_ctx* c, const zk::SampleArgs& a);
 // Looks up the allocation-free scratch array's address on the context's
 // device (defined in noalloc.hip; the device must be current).
 void noalloc_setup(zl_ctx* c);
+// Gives the context's slot of that array back (zl_destroy).
+void noalloc_release(zl_ctx* c);
 
 // zl_ppo internals for the checkpoint code (defined in mlp_ppo.cpp).
 zl_ctx* ppo_ctx(zl_ppo* p);

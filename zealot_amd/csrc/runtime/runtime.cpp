@@ -990,6 +990,7 @@ zl_status zl_timing_launch(const zl_ctx* c, long long i, const char** name, doub
 void zl_destroy(zl_ctx* c) {
   if (!c) return;
   if (c->stream) hipStreamSynchronize(c->stream);
+  noalloc_release(c);
   for (hipEvent_t e : c->ev_pool) hipEventDestroy(e);
   if (c->ws) hipFree(c->ws);
   if (c->stream) hipStreamDestroy(c->stream);

@@ -439,14 +439,24 @@ class DeviceBatch:
     (src/bin/biped_train_gpu.rs:1029-1030,1053-1056), with stride n."""
 
     def __init__(self, ctx: Context, obs, critic_obs, action, mean_old, logp_old, value_old, adv, ret,
-                 feature_major: bool = False):
+                 feature_major: bool = False, pad: int = 0):
+        """pad > 0 stores each matrix field with its stride `pad` elements past
+        the rows it holds (feature-major: [dim x (n + pad)], as a trainer
+        tensor sized for a larger capacity; batch-major: [n x (dim + pad)]);
+        the padding holds NaN, which the update never reads."""
         self.ctx = ctx
         self.n = int(np.asarray(obs).shape[0])
         self.feature_major = bool(feature_major)
+        self.pad = int(pad)
 
         def mat(x):
             x = np.asarray(x, np.float32)
-            return ctx.to_device(np.ascontiguousarray(x.T) if feature_major else x, np.float32)
+            y = x.T if feature_major else x
+            if self.pad:
+                z = np.full((y.shape[0], y.shape[1] + self.pad), np.nan, np.float32)
+                z[:, :y.shape[1]] = y
+                y = z
+            return ctx.to_device(np.ascontiguousarray(y), np.float32)
 
         self.obs = mat(obs)
         self.critic_obs = self.obs if critic_obs is obs else mat(critic_obs)
@@ -462,7 +472,7 @@ class DeviceBatch:
 
     def to_c(self) -> _ffi.zl_batch:
         fm = self.feature_major
-        ld = (lambda d: self.n) if fm else (lambda d: d)
+        ld = (lambda d: self.n + self.pad) if fm else (lambda d: d + self.pad)
         bits = (_ffi.ZL_FM_OBS | _ffi.ZL_FM_CRITIC_OBS | _ffi.ZL_FM_ACTION | _ffi.ZL_FM_MEAN_OLD) if fm else 0
         return _ffi.zl_batch(
             self.n, self.obs.ptr, ld(self.od), self.critic_obs.ptr, ld(self.cd), self.action.ptr,
