@@ -224,8 +224,9 @@ def operator_measurements(ctx):
     123] . W [123 x 512] + b, ELU; the reference's feature-major
     gemm_bias_act, src/biped/cutile_gemm.rs:578-625) and the clipped Adam
     step over actor + critic + log_std (459,323 parameters in the trainer's
-    17 tensors: device grad-norm clip at 1.0, then one tensor-list Adam
-    launch; src/bin/biped_train_gpu.rs:1368-1461). Kernel time by HIP
+    17 tensors: zl_adam_multi_clip, the sums of squares of the gradients,
+    then one tensor-list Adam launch whose blocks take the global clip scale
+    at 1.0; src/bin/biped_train_gpu.rs:1368-1461). Kernel time by HIP
     events; Adam warm (working set in the Infinity Cache) and cold (a
     512 MiB device copy between calls evicts it)."""
     from zealot_amd import ops, synth
@@ -252,14 +253,12 @@ def operator_measurements(ctx):
     dm, dv = ctx.to_device(np.zeros(npar, np.float32)), ctx.to_device(np.zeros(npar, np.float32))
     scale, norm = ctx.alloc(1), ctx.alloc(1)
     offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
-    gt = [(dg.offset(int(o)), int(s)) for o, s in zip(offs[:-1], sizes)]
     at = [(dp.offset(int(o)), dg.offset(int(o)), dm.offset(int(o)), dv.offset(int(o)), int(s))
           for o, s in zip(offs[:-1], sizes)]
     bc1, bc2 = float(np.float32(1.0) - np.float32(0.9 ** 11)), float(np.float32(1.0) - np.float32(0.999 ** 11))
 
     def adam():
-        ops.grad_clip_scale(ctx, gt, 1.0, scale, norm)
-        ops.adam_multi(ctx, at, 1e-3, bc1, bc2, clip_scale=scale)
+        ops.adam_multi_clip(ctx, at, 1e-3, bc1, bc2, 1.0, scale, norm)
 
     flush_bytes = 512 << 20
     fa, fb = ctx.alloc(flush_bytes, np.uint8), ctx.alloc(flush_bytes, np.uint8)
@@ -275,7 +274,7 @@ def operator_measurements(ctx):
             "tflops": flop1 / t_layer / 1e12, "fp32_mfma_frac": flop1 / t_layer / 157.3e12,
         },
         "adam_clip": {
-            "workload": f"global grad-norm clip 1.0 + Adam over {npar} params (17 tensors)",
+            "workload": f"global grad-norm clip 1.0 + Adam over {npar} params (17 tensors), 2 launches",
             "warm_kernel_us": t_warm * 1e6, "cold_kernel_us": t_cold * 1e6, "wall_us": t_adam_wall * 1e6,
             "warm_GBps": bytes3 / t_warm / 1e9, "cold_GBps": bytes3 / t_cold / 1e9,
             "cold_hbm_frac": bytes3 / t_cold / 8e12,

@@ -208,6 +208,19 @@ zl_status zl_adam_multi(zl_ctx* ctx, const zl_adam_tensor* tensors, int count, f
                         float beta1, float beta2, float eps, float bc1, float bc2,
                         const float* clip_scale_dev);
 
+/* The trainer's whole clipped optimiser step (src/bin/biped_train_gpu.rs:
+ * 1368-1461: Reduce::SqNorm per gradient tensor, the global norm and clip
+ * scale, Adam::step per tensor) in two launches instead of three: the sums
+ * of squares of the tensors' gradients, then one Adam launch whose blocks
+ * each take the clip scale from them (max_norm / norm when max_norm > 0 and
+ * norm > max_norm, else 1). Bit-identical to zl_grad_clip_scale over the
+ * gradients followed by zl_adam_multi with its scale. scale_dev[0] and
+ * norm_dev[0] receive the scale and the norm (either may be NULL). count <=
+ * 48. Asynchronous. */
+zl_status zl_adam_multi_clip(zl_ctx* ctx, const zl_adam_tensor* tensors, int count, float lr,
+                             float beta1, float beta2, float eps, float bc1, float bc2,
+                             float max_norm, float* scale_dev, float* norm_dev);
+
 /* GAE(lambda) for N independent trajectories of length T, one lane per env
  * (zealot-rl/src/ppo.rs:681-703, run per env by
  * src/bin/biped_train_gpu.rs:974-981). Element (t, e) of rewards / values /

@@ -259,6 +259,47 @@ def test_config3_device_clip_and_adam_multi(ctx):
     assert up <= 2 and um <= 2 and uv <= 2
 
 
+def test_config3_adam_multi_clip_two_launches(ctx):
+    """zl_adam_multi_clip (the clipped step in two launches: sums of squares,
+    then Adam blocks that each take the scale) against zl_grad_clip_scale +
+    zl_adam_multi over the same 11 steps of config 3: parameters, moments,
+    scale and norm bit-identical; plus a step with the clip inactive and one
+    with it disabled."""
+    na, nc = packed_count(synth.ACTOR_DIMS), packed_count(synth.CRITIC_DIMS)
+    c3 = synth.config3(na, nc)
+    sizes = _grad_tensors(synth.ACTOR_DIMS, synth.CRITIC_DIMS, 29)
+    n = sum(sizes)
+    p0 = np.concatenate([c3["actor"], c3["critic"], c3["log_std"]]).astype(np.float32)
+    offs = np.concatenate([[0], np.cumsum(sizes)])
+    runs = []
+    for fused in (False, True):
+        dp, dm, dv = ctx.to_device(p0), ctx.to_device(np.zeros(n, np.float32)), ctx.to_device(np.zeros(n, np.float32))
+        dg = ctx.alloc(n)
+        scale, norm = ctx.alloc(1), ctx.alloc(1)
+        gt = [(dg.offset(int(o)), int(s)) for o, s in zip(offs[:-1], sizes)]
+        at = [(dp.offset(int(o)), dg.offset(int(o)), dm.offset(int(o)), dv.offset(int(o)), int(s))
+              for o, s in zip(offs[:-1], sizes)]
+        trace = []
+        grads = list(c3["grads"]) + [c3["grads"][0] * np.float32(1e-3), c3["grads"][1]]
+        for t, gr in enumerate(grads, start=1):
+            bc1 = float(np.float32(1.0) - np.float32(zo.powi(0.9, t)))
+            bc2 = float(np.float32(1.0) - np.float32(zo.powi(0.999, t)))
+            mx = 0.0 if t == len(grads) else 1.0
+            dg.upload(gr)
+            if fused:
+                ops.adam_multi_clip(ctx, at, 1e-3, bc1, bc2, mx, scale, norm)
+            else:
+                ops.grad_clip_scale(ctx, gt, mx, scale, norm)
+                ops.adam_multi(ctx, at, 1e-3, bc1, bc2, clip_scale=scale)
+            trace.append((scale.numpy()[0], norm.numpy()[0]))
+        runs.append((dp.numpy(), dm.numpy(), dv.numpy(), trace))
+    for x, y in zip(runs[0][:3], runs[1][:3]):
+        assert np.array_equal(x, y)
+    assert runs[0][3] == runs[1][3]
+    sc = [s for s, _ in runs[1][3]]
+    assert all(s < 1.0 for s in sc[:11]) and sc[11] == 1.0 and sc[12] == 1.0
+
+
 def test_clip_scale_inactive_and_disabled(ctx):
     """Below the threshold, or with max_norm <= 0, the scale is exactly 1."""
     g = (np.random.default_rng(4).standard_normal(5000) * 1e-3).astype(np.float32)

@@ -275,6 +275,66 @@ def test_config1_aligned_and_odd_stride_agree(ctx):
     assert np.array_equal(a, p)
     assert rel_amax(p.T, ref) <= FWD_BWD_TOL
 
+@pytest.fixture(scope="module")
+def smallk_ctx():
+    """A context that takes the small-K variants also for float4-aligned A
+    rows (ZL_SMALLK=2, read at zl_init)."""
+    import os
+
+    from zealot_amd import Context
+
+    os.environ["ZL_SMALLK"] = "2"
+    try:
+        c = Context(0)
+    finally:
+        del os.environ["ZL_SMALLK"]
+    yield c
+    c.close()
+
+
+# (m, n, k, bias): A K-contiguous (lhs as stored), B N-contiguous, K <= 128:
+# ragged tiles, K tails, the padded K = 128 and the config-1 shape.
+SMALLK_CASES = [(1, 1, 1, False), (5, 7, 3, True), (130, 70, 17, True), (512, 4096, 123, True),
+                (512, 4096, 128, True), (300, 1000, 76, False), (64, 64, 128, False), (70, 4099, 100, True)]
+
+
+@pytest.mark.parametrize("case", SMALLK_CASES)
+def test_gemm_smallk_variants(ctx, smallk_ctx, case):
+    """The small-K form (one round of loads for the whole K <= 128 extent)
+    against float64 at 1e-4: on the default context it takes products whose
+    lhs rows are not float4-aligned (K not a multiple of 4), on the
+    ZL_SMALLK=2 context also the aligned ones. The same product with K padded
+    to a multiple of 4 by zero columns / rows (float4 rows: the k-tiled form
+    on the default context) adds exact zeros in the same 16-wide chunk order,
+    so all four results are bit-identical."""
+    m, n, k, bias = case
+    g = np.random.default_rng(m + 7 * n + 31 * k)
+    L = g.standard_normal((m, k)).astype(np.float32)
+    R = g.standard_normal((k, n)).astype(np.float32)
+    bb = g.uniform(-0.5, 0.5, m).astype(np.float32)
+    z = L.astype(np.float64) @ R.astype(np.float64) + (bb[:, None] if bias else 0.0)
+    ref = np.where(z > 0, z, np.expm1(np.minimum(z, 0))) if bias else z
+    kp = -(-k // 4) * 4
+    Lp = np.zeros((m, kp), np.float32)
+    Lp[:, :k] = L
+    Rp = np.zeros((kp, n), np.float32)
+    Rp[:k] = R
+    outs = []
+    for cx in (ctx, smallk_ctx):
+        for lhs, rhs, kk in ((L, R, k), (Lp, Rp, kp)):
+            out = cx.alloc((m, n))
+            dl, dr = cx.to_device(lhs), cx.to_device(rhs)
+            if bias:
+                ops.gemm_bias_act(cx, out, dl, dr, m, n, kk, cx.to_device(bb), 1, True)
+            else:
+                ops.gemm(cx, out, dl, False, dr, False, m, n, kk)
+            outs.append(out.numpy())
+    for o in outs:
+        assert rel_amax(o, ref) <= FWD_BWD_TOL, case
+    for o in outs[1:]:
+        assert np.array_equal(outs[0], o), case
+
+
 def _mlp_case(ctx, dims, rows, seed, bias_bound=0.1):
     g = np.random.default_rng(seed)
     params = synth.kaiming_uniform_net(g, dims, bias_bound=bias_bound)

@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 
 import np_ref
+import yardstick as ys
 from conftest import rel_amax
 from oracle import zl_oracle as zo
 from test_gpu_ppo import (WELL_POSED_CLIP, _assert_tight, _param_delta_report, f32_forward,
@@ -154,14 +155,23 @@ def test_config5_stated_settings_full_size(ctx):
     rows at clip 0.2, entropy 0.005, value x1.0, lr 1e-3 (fixed), global
     clip 1.0, log_std clamped to [-1.6, 0] after the update.
 
-    Twenty full-size steps at lr 1e-3 with clip 0.2 are chaotic in fp32 (any
-    valid change of summation order moves the actor update by tens of percent
-    relative L2), so the parameters cannot be compared per component. Checked:
-    two updates from one state are bit-identical; every parameter is finite;
-    the learning rate, gstep, epochs, Adam moments' finiteness and the clamp
-    range are exact; the value loss and entropy statistics match the oracle
-    within 1e-3; the actor, critic and log_std updates point the same way as
-    the oracle's (cosine >= 0.9)."""
+    Twenty full-size steps at lr 1e-3 with clip 0.2 are chaotic in fp32: any
+    valid change of evaluation order moves the update by a few tenths of a
+    percent (critic, log_std) to about 1.6 % (actor) relative L2, and more
+    than half of the components by over 1 % of lr, so the parameters cannot
+    be compared per component. The yardstick is the oracle's own spread
+    (tests/yardstick.py): the oracle is run three more times on the same
+    inputs, with another thread count (the fold grouping rayon leaves open,
+    zealot-rl/src/ppo.rs:406-462) and with the observations moved by a last
+    bit under two seeds, and the GPU's update must lie within 2x the largest
+    distance of those runs from the oracle's, per net (a minibatch out of
+    order lands 20-500x beyond it: test_update_yardstick_separates_minibatch_
+    order). The fraction of components off by more than 1 % of lr is
+    reported, not bounded: valid runs already reach 50-85 %. Also checked:
+    two updates from one state are bit-identical; every parameter and moment
+    is finite; the learning rate, gstep, epochs and the clamp range are
+    exact; the value loss and entropy statistics match the oracle within
+    1e-3."""
     ad, cd = synth.ACTOR_DIMS, synth.CRITIC_DIMS
     N, T = 4096, 24
     n, mb = N * T, N * T // 4
@@ -210,20 +220,32 @@ def test_config5_stated_settings_full_size(ctx):
         assert np.all(np.isfinite(x))
     assert st.epochs_run == 5 and gstep == 20 and lrg == np.float32(1e-3)
     assert np.all(lsg <= 0.0) and np.all(lsg >= -1.6)
-    # The oracle on the same inputs (GPU-trainer semantics, 16 host threads).
-    tr = zo.Trainer(ad, cd, actor, critic, log_std, 1e-3)
+    # The oracle on the same inputs (GPU-trainer semantics, 16 host threads),
+    # then the three valid variants that measure its own spread.
     batch["adv"] = zo.adv_normalize(adv_raw)
-    so = tr.update(batch, zo.TrainerCfg(0.2, 0.005, 1.0, 5, 4, 1.0, 0.01, 1e-5, 1e-2, 0, 0, 1),
-                   nthreads=NTHREADS)
-    ao, co, lso, lro, gso = tr.get()
-    ra = _param_delta_report(actor, ag, ao, 1e-3, 20)
-    rc = _param_delta_report(critic, cg, co, 1e-3, 20)
-    rl = _param_delta_report(log_std, lsg, lso, 1e-3, 20)
-    print(f"[gpu] config 5 stated settings: actor {ra} critic {rc} log_std {rl}; stats gpu {st} "
-          f"cpu {so}", flush=True)
+    tcfg = zo.TrainerCfg(0.2, 0.005, 1.0, 5, 4, 1.0, 0.01, 1e-5, 1e-2, 0, 0, 1)
+
+    def oracle(b, nth):
+        tr = zo.Trainer(ad, cd, actor, critic, log_std, 1e-3)
+        so_ = tr.update(b, tcfg, nthreads=nth)
+        return tr.get(), so_
+
+    (ao, co, lso, lro, gso), so = oracle(batch, NTHREADS)
+    variants = [oracle(batch, max(1, NTHREADS - 4))[0]]
+    for seed in (1, 2):
+        b = dict(batch)
+        b["obs"] = b["critic_obs"] = ys.perturb_last_bit(batch["obs"], seed)
+        variants.append(oracle(b, NTHREADS)[0])
+    p0, gpu, ref = (actor, critic, log_std), (ag, cg, lsg), (ao, co, lso)
+    yard = {}
+    for i, name in enumerate(("actor", "critic", "log_std")):
+        ok, d, sp = ys.within(p0[i], ref[i], [v[i] for v in variants], gpu[i])
+        yard[name] = dict(ok=ok, gpu_rel_l2=d, oracle_spread=sp,
+                          frac_gt_1pct_lr=_param_delta_report(p0[i], gpu[i], ref[i], 1e-3, 20)["frac_gt_1pct_lr"])
+    print(f"[gpu] config 5 stated settings: {yard}; stats gpu {st} cpu {so}", flush=True)
     assert gso == gstep and int(so[5]) == 5 and lro == lrg
     assert abs(st.value_loss - so[2]) <= 1e-3 * max(abs(so[2]), 1e-2)
     assert abs(st.entropy - so[3]) <= 1e-3 * max(abs(so[3]), 1e-2)
-    assert ra["cos"] >= 0.9 and rc["cos"] >= 0.9 and rl["cos"] >= 0.9
-    assert ra["max_abs"] <= ra["bound"] and rc["max_abs"] <= rc["bound"]
+    for name, r in yard.items():
+        assert r["ok"], (name, r)
     gac.close()

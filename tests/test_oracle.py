@@ -1031,3 +1031,65 @@ def test_trainer_lr_up_branch_and_ceiling():
     # would be 1.5x larger.
     fast = _trainer_epoch_f64(ad, cd, actor, critic, log_std, batch, n_mb, 1.5e-2, 1e30, 0.2, 0.01, 1.0)
     assert rel_amax(a1.astype(np.float64) - actor, fast[0][0] - actor) > 0.2
+
+
+# ---- the yardstick of the full-size chaotic update (tests/yardstick.py),
+# shown on the CPU to separate valid evaluations from a wrong update.
+
+def test_update_yardstick_separates_minibatch_order():
+    """The GPU trainer's update (src/bin/biped_train_gpu.rs:1164-1553) at the
+    headline nets and settings (clip 0.2, lr 1e-3, global clip 1.0, 5 x 4
+    minibatches) on a 128-env x 24-step rollout, in the oracle: the spread of
+    valid evaluations (another thread count, last-bit input changes) against
+    the same update with two minibatches swapped, as a GPU update one
+    minibatch out of order would be. Every valid variant passes the 2 x
+    spread bound of the others; each swapped run fails it for every net."""
+    import yardstick as ys
+    from zealot_amd import synth
+
+    ad, cd = synth.ACTOR_DIMS, synth.CRITIC_DIMS
+    N, T = 128, 24
+    n = N * T
+    g = synth.rng(5)
+    ro = synth.rollout(g, N, T)
+    actor, critic = synth.kaiming_uniform_net(g, ad), synth.kaiming_uniform_net(g, cd)
+    log_std = np.full(ad[-1], -0.5, np.float32)
+    means = zo.mlp_forward(ad, actor, ro["obs"])[-1]
+    vals = zo.mlp_forward(cd, critic, ro["obs"])[-1][:, 0]
+    last = zo.mlp_forward(cd, critic, ro["boot_obs"])[-1][:, 0]
+    act = (means + np.exp(log_std) * ro["eps"]).astype(np.float32)
+    adv, ret = np.empty((T, N), np.float32), np.empty((T, N), np.float32)
+    for e in range(N):
+        adv[:, e], ret[:, e] = zo.gae(ro["rewards"][:, e], vals.reshape(T, N)[:, e], ro["dones"][:, e],
+                                      float(last[e]), 0.99, 0.95)
+    batch = dict(obs=ro["obs"], critic_obs=ro["obs"], action=act, mean_old=means,
+                 logp_old=synth.gaussian_logp(act, means, log_std), value_old=vals,
+                 adv=zo.adv_normalize(adv.ravel()), ret=ret.ravel())
+
+    def run(b, nth):
+        tr = zo.Trainer(ad, cd, actor, critic, log_std, 1e-3)
+        tr.update(b, zo.TrainerCfg(0.2, 0.005, 1.0, 5, 4, 1.0, 0.01, 1e-5, 1e-2, 0, 0, 1), nthreads=nth)
+        return tr.get()[:3]
+
+    def with_obs(o):
+        b = dict(batch)
+        b["obs"] = b["critic_obs"] = o
+        return b
+
+    base = run(batch, 8)
+    valid = [run(batch, 3), run(with_obs(ys.perturb_last_bit(batch["obs"], 1)), 8),
+             run(with_obs(ys.perturb_last_bit(batch["obs"], 2)), 8)]
+    mb = n // 4
+    swapped = []
+    for order in ([1, 0, 2, 3], [0, 1, 3, 2]):
+        idx = np.concatenate([np.arange(k * mb, (k + 1) * mb) for k in order])
+        swapped.append(run({k: v[idx] for k, v in batch.items()}, 8))
+    p0 = [actor, critic, log_std]
+    for i, name in enumerate(("actor", "critic", "log_std")):
+        for j, v in enumerate(valid):
+            others = [w[i] for k, w in enumerate(valid) if k != j]
+            ok, d, s = ys.within(p0[i], base[i], others, v[i])
+            assert ok, (name, "valid", j, d, s)
+        for sw in swapped:
+            ok, d, s = ys.within(p0[i], base[i], [w[i] for w in valid], sw[i])
+            assert not ok and d > 10 * s, (name, "swapped", d, s)

@@ -157,6 +157,8 @@ SIGNATURES = {
         [vp, C.POINTER(zl_adam_tensor), C.c_int, C.c_float, C.c_float, C.c_float, C.c_float,
          C.c_float, C.c_float, vp],
     ),
+    "zl_adam_multi_clip": (C.c_int, [vp, C.POINTER(zl_adam_tensor), C.c_int, C.c_float, C.c_float, C.c_float,
+                                     C.c_float, C.c_float, C.c_float, C.c_float, vp, vp]),
     "zl_gae": (
         C.c_int,
         [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_longlong, C.c_longlong, C.c_longlong,

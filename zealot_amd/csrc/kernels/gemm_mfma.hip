@@ -608,6 +608,98 @@ __device__ __forceinline__ void gemm_body(float* __restrict__ smem, const GemmAr
   }
 }
 
+// Small-K form of the A K-contiguous x B N-contiguous product (the
+// reference's feature-major gemm_bias_act, src/biped/cutile_gemm.rs:578-625,
+// at K <= KP): every global load of the block -- the whole K extent of both
+// operand tiles -- is issued in one round, stored to LDS once, and the MFMAs
+// then run over the 16-wide chunks from LDS, so the block pays one memory
+// latency instead of one per k-tile. A may be read element by element (VA =
+// false: rows that are not 16-byte aligned, such as a 123-float stride); B
+// is read as float4 rows. Epilogues: store, bias per column (kEpiBiasN) or
+// per row (kEpiBiasM), optional ELU. No split-K, row sums or gathers.
+template <int BM, int BN, int KP, int WM, int WN, bool VA>
+constexpr int gemm_smallk_smem_floats() {
+  return Tile<BM, true, KP, 64 * WM * WN, VA>::SIZE + Tile<BN, false, KP, 64 * WM * WN, true>::SIZE;
+}
+template <int BM, int BN, int KP, int WM, int WN, bool VA>
+__device__ __forceinline__ void gemm_smallk_body(float* __restrict__ smem, const GemmArgs& p, int mt,
+                                                 int nt) {
+  constexpr int NT = 64 * WM * WN;
+  constexpr int TM = BM / (WM * 16);
+  constexpr int TN = BN / (WN * 16);
+  static_assert(TM * WM * 16 == BM && TN * WN * 16 == BN && KP % 16 == 0, "small-K tiling");
+  using TA = Tile<BM, true, KP, NT, VA>;
+  using TB = Tile<BN, false, KP, NT, true>;
+  float* sA = smem;
+  float* sB = smem + TA::SIZE;
+  if (p.guard && *p.guard == 0) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % WM, wn = wave / WM;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = mt * BM, n0 = nt * BN;
+  if (m0 >= p.M || n0 >= p.N) return;
+  TA ta;
+  TB tb;
+  ta.init(p.A, p.lda, m0, p.M, p.K, nullptr);
+  tb.init(p.B, p.ldb, n0, p.N, p.K, nullptr);
+  ta.load(0);
+  tb.load(0);
+  ta.store(sA, 0);  // zero past K and past the matrix edges
+  tb.store(sB, 0);
+  __syncthreads();
+  floatx4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int nq = (p.K + 15) / 16;
+  float4 fa[TM], fb[TN];
+  auto read = [&](int q) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[i] = TA::frag(sA, (wm * TM + i) * 16 + lr, q, lg);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[j] = TB::frag(sB, (wn * TN + j) * 16 + lr, q, lg);
+  };
+  read(0);
+  for (int q = 0; q < nq; ++q) {
+    float4 a[TM], b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) a[i] = fa[i];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) b[j] = fb[j];
+    if (q + 1 < nq) read(q + 1);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+      }
+  }
+  const bool full = m0 + BM <= p.M && n0 + BN <= p.N;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + (wm * TM + i) * 16 + lg * 4 + r;
+      if (!full && m >= p.M) continue;
+      const float bm = p.epi == kEpiBiasM ? p.bias[(long long)m * p.bias_stride] : 0.f;
+      float* crow = p.C + (long long)m * p.ldc;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + (wn * TN + j) * 16 + lr;
+        if (!full && n >= p.N) continue;
+        float v = acc[i][j][r];
+        if (p.epi == kEpiBiasN) v += p.bias[n];
+        if (p.epi == kEpiBiasM) v += bm;
+        if (p.epi != kEpiStore && p.act) v = elu(v);
+        crow[n] = v;
+      }
+    }
+}
+
 // out[(i / cols) * ldo + i % cols] = sum_z part[z*mn + i], rowout likewise.
 // A block is 256 / lanes elements (float4 quads of the matrix, or single
 // row sums) x `lanes` split lanes: lane l adds slices l, l+lanes, ... in
@@ -853,6 +945,19 @@ ZK_GEMM(zk_gemm_ak_bn_64x128x16_w22_s, true, false, 64, 128, 16, 2, 2, false)
 ZK_GEMM(zk_gemm_ak_bn_64x64x32_w22_s, true, false, 64, 64, 32, 2, 2, false)
 ZK_GEMM(zk_gemm_am_bn_64x128x16_w22_s, false, false, 64, 128, 16, 2, 2, false)
 ZK_GEMM(zk_gemm_am_bk_64x128x16_w22_s, false, true, 64, 128, 16, 2, 2, false)
+
+// Small-K variants (K <= 128): A element loads (_s) or float4 rows.
+#define ZK_GEMM_SMALLK(NAME, BM, BN, WM, WN, VA)                                                 \
+  extern "C" __global__ __launch_bounds__(64 * WM * WN) void NAME(zk::GemmBatch b) {            \
+    __shared__ __align__(16) float smem[zk::gemm_smallk_smem_floats<BM, BN, 128, WM, WN, VA>()]; \
+    int prob;                                                                                   \
+    const zk::BlockTile bt = zk::batch_tile(b, (int)blockIdx.x, prob);                          \
+    zk::gemm_smallk_body<BM, BN, 128, WM, WN, VA>(smem, b.g[prob], bt.mt, bt.nt);               \
+  }
+ZK_GEMM_SMALLK(zk_gemm_ak_bn_64x64xk128_w22_s, 64, 64, 2, 2, false)
+ZK_GEMM_SMALLK(zk_gemm_ak_bn_64x64xk128_w22, 64, 64, 2, 2, true)
+ZK_GEMM_SMALLK(zk_gemm_ak_bn_64x64xk128_w24_s, 64, 64, 2, 4, false)
+ZK_GEMM_SMALLK(zk_gemm_ak_bn_64x64xk128_w24, 64, 64, 2, 4, true)
 
 // One layer's backward as one launch (GemmPair): the split-K weight-gradient
 // GEMMs of both nets (exact-fit am_bn tiles, blocks [0, w grid)) and their

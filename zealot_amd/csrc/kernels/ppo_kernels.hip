@@ -858,14 +858,17 @@ __device__ void sumsq_multi_body(const SumsqMultiArgs& p) {
 // One wavefront: the norm from the partials in block order, and the clip
 // scale of the trainer's global clip (src/bin/biped_train_gpu.rs:1398-1404):
 // max_norm / norm when norm > max_norm, else 1.
+__device__ __forceinline__ float clip_scale_of(float sq, float max_norm, float* norm_out) {
+  const float norm = sqrtf(sq);
+  *norm_out = norm;
+  return (max_norm > 0.0f && norm > max_norm) ? max_norm / norm : 1.0f;
+}
 __device__ void clip_scale_body(const ClipScaleArgs& p) {
   if (threadIdx.x >= 64) return;
   const float sq = wave_sum_strided(p.part, p.nparts, 1);
   if (threadIdx.x != 0) return;
-  const float norm = sqrtf(sq);
-  float s = 1.0f;
-  if (p.max_norm > 0.0f && norm > p.max_norm) s = p.max_norm / norm;
-  *p.scale = s;
+  float norm;
+  *p.scale = clip_scale_of(sq, p.max_norm, &norm);
   if (p.norm) *p.norm = norm;
 }
 
@@ -878,12 +881,11 @@ __device__ void adam_multi_body(const AdamMultiArgs& p) {
   while (j + 1 < p.count && b >= p.blk0[j + 1]) ++j;
   const AdamTensor& T = p.t[j];
   const long long i0 = ((long long)(b - p.blk0[j]) * kThreads + threadIdx.x) * 4;
-  if (i0 >= T.n) return;
-  const float sc = p.scale ? *p.scale : 1.0f;
-  const float b1 = p.beta1, b2 = p.beta2, eps = p.eps, lr = p.lr, bc1 = p.bc1, bc2 = p.bc2;
-  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+  const bool live = i0 < T.n;
   const bool quad = i0 + 4 <= T.n &&
                     ((((uintptr_t)T.p | (uintptr_t)T.g | (uintptr_t)T.m | (uintptr_t)T.v) & 15u) == 0);
+  // The element loads first: they do not depend on the clip scale, so they
+  // are in flight while the block takes it.
   float x[4], g[4], m[4], v[4];
   if (quad) {
     const float4 x4 = *reinterpret_cast<const float4*>(T.p + i0);
@@ -904,6 +906,30 @@ __device__ void adam_multi_body(const AdamMultiArgs& p) {
       v[u] = in ? T.v[i0 + u] : 0.f;
     }
   }
+  float sc = 1.0f;
+  if (p.part) {
+    // Every block: wavefront 0 adds the partials as zk_clip_scale does and
+    // lane 0 takes the scale (every thread reaches the barrier).
+    __shared__ float s_sc;
+    if (threadIdx.x < 64) {
+      const float sq = wave_sum_strided(p.part, p.nparts, 1);
+      if (threadIdx.x == 0) {
+        float norm;
+        s_sc = clip_scale_of(sq, p.max_norm, &norm);
+        if (b == 0) {
+          if (p.scale_out) *p.scale_out = s_sc;
+          if (p.norm_out) *p.norm_out = norm;
+        }
+      }
+    }
+    __syncthreads();
+    sc = s_sc;
+  } else if (p.scale) {
+    sc = *p.scale;
+  }
+  if (!live) return;
+  const float b1 = p.beta1, b2 = p.beta2, eps = p.eps, lr = p.lr, bc1 = p.bc1, bc2 = p.bc2;
+  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const float gr = g[u] * sc;

@@ -510,6 +510,15 @@ struct AdamMultiArgs {
   int count;
   const float* scale;  // nullable
   float lr, bc1, bc2, beta1, beta2, eps;
+  // With `part` set, every block takes the clip scale itself from the
+  // zk_sumsq_multi partials (nparts, added in zk_clip_scale's order, the
+  // same rule) instead of reading `scale`; block 0 writes it and the norm
+  // to scale_out / norm_out (nullable).
+  const float* part;
+  int nparts;
+  float max_norm;
+  float* scale_out;
+  float* norm_out;
 };
 
 }  // namespace zk

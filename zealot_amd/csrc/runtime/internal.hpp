@@ -70,6 +70,7 @@ struct GemmKernel {
   int bm, bn, bk, threads;
   bool vec;
   int kind = G_TILED;
+  bool need_vec_b = false;  // reads B as float4 rows even when A is read by elements
 };
 
 // Narrow kernels: 16-row strips, four wavefronts per block; the data-gradient
@@ -153,6 +154,10 @@ struct zl_ctx {
   int force_gemm[4] = {-1, -1, -1, -1};
   int force_splits = 0;
   int splitk_target = 256;
+  // Divisor of the split-K slice count of weight gradients that share a
+  // launch with their layer's data gradients (ZL_BWD_SPLIT_DIV; 0: the
+  // rule in pair_backward).
+  int bwd_split_div = 0;
   // Narrow kernels for shapes with a dimension <= 32 (ZL_NARROW=0 turns them
   // off) and the block count their row slices aim at (ZL_NARROW_TARGET).
   bool narrow = true;
@@ -163,6 +168,11 @@ struct zl_ctx {
   // Forwards of up to kPolicyFusedRows rows (a rollout step) as one zk_policy
   // launch where the nets fit it (ZL_POLICY_FUSED=0 keeps the layer GEMMs).
   bool fused_policy = true;
+  // A K-contiguous x B N-contiguous products with K <= 128 and a plain or
+  // bias epilogue on the small-K variants (ZL_SMALLK: 0 off, 1 when A rows
+  // are not float4-aligned (default), 2 always).
+  int smallk = 1;
+  int smallk_waves = 4;  // wavefronts per small-K block (ZL_SMALLK_WAVES: 4 or 8)
   // Device address of the allocation-free scratch array on this context's
   // device (zl_grad_clip_scale_noalloc), set at zl_init.
   float* noalloc_scratch = nullptr;  // this context's slot of the array
@@ -239,8 +249,10 @@ struct GemmDesc {
 // Variant choice and split-K decision shared by run_gemm and the scratch
 // sizing of composites.
 // vec: both operands can be read as aligned float4 rows (see run_gemm).
+// vec_b: B alone can be read as float4 rows and the problem has no split-K,
+// row sums or gathers (the small-K variants may then take it).
 int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec = true,
-              int epi = zk::kEpiStore);
+              int epi = zk::kEpiStore, bool vec_b = false);
 int gemm_splits(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi,
                 bool vec = true);
 size_t gemm_ws_floats(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, int epi);

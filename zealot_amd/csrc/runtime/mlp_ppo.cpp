@@ -334,6 +334,26 @@ static zl_status pair_backward(zl_ctx* c, const NetView v[2], const float* param
       q.seg_out = &segs[i * L[0] + l];
       if (l > 0) d[nd++] = dgrad_desc(nl, nb, params, rows, dl, ldd, guard, l);
     }
+    // Weight gradients that share a launch with data gradients filling at
+    // least three rounds of the CUs (two 128 x 128 tiles per CU each) take
+    // half the split-K slices: the data-gradient blocks keep the CUs busy
+    // while the longer slices run, and the reduction reads half the
+    // partials (the 24,576-row layer-1 backward 225.9 -> 221.6 us and its
+    // share of zk_reduce_all ~1.6 us less per minibatch; the layer-2
+    // backward, 768 data-gradient tiles, measured 70.8 -> 77.1 us with half
+    // and keeps them). ZL_BWD_SPLIT_DIV > 0 sets the divisor for every such
+    // layer instead.
+    if (paired && nd > 0) {
+      long long dg_tiles = 0;
+      for (int j = 0; j < nd; ++j) dg_tiles += cdiv(d[j].M, 128) * cdiv(d[j].N, 128);
+      int div = c->bwd_split_div;
+      if (div == 0) div = dg_tiles >= 6LL * c->cu_count ? 2 : 1;
+      if (div > 1)
+        for (int j = 0; j < nw; ++j)
+          if (w[j].M > 0 && L[j] - 1 - depth > 0)  // a layer with a data gradient
+            w[j].splits = std::max(1, gemm_splits(c, w[j].M, w[j].N, w[j].K, w[j].a_kc, w[j].b_kc,
+                                                  w[j].epi) / div);
+    }
     zl_status s = ZL_OK;
     if (paired) {
       s = run_gemm_bwd(c, w, nw, d, nd);

@@ -58,6 +58,10 @@ const GemmKernel kGemmTable[] = {
     {"zk_gemm_am_bk_64x128x16_w22_s", false, true, 64, 128, 16, 256, false},
     {"zk_gemm_ak_bn_64x64x32_w22", true, false, 64, 64, 32, 256, true},
     {"zk_gemm_ak_bn_64x64x32_w22_s", true, false, 64, 64, 32, 256, false},
+    {"zk_gemm_ak_bn_64x64xk128_w22_s", true, false, 64, 64, 128, 256, false, G_TILED, true},
+    {"zk_gemm_ak_bn_64x64xk128_w22", true, false, 64, 64, 128, 256, true},
+    {"zk_gemm_ak_bn_64x64xk128_w24_s", true, false, 64, 64, 128, 512, false, G_TILED, true},
+    {"zk_gemm_ak_bn_64x64xk128_w24", true, false, 64, 64, 128, 512, true},
     {"zk_narrow_n1_v", true, true, kNarrowRows, 16, 16, 256, true, G_NARROW_N},
     {"zk_narrow_n2_v", true, true, kNarrowRows, 32, 16, 256, true, G_NARROW_N},
     {"zk_narrow_n1_s", true, true, kNarrowRows, 16, 16, 256, false, G_NARROW_N},
@@ -158,9 +162,18 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // 512- and 256-wide layers, 64 x 128 for the 128-wide one (both with 32-row
 // k-tiles, so that the k-loop's barrier sits between two chunks) and
 // 32 x 128 for the narrow heads (measured on gfx950 at 24,576 rows).
-int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec, int epi) {
+int pick_gemm(const zl_ctx* c, int M, int N, int K, bool a_kc, bool b_kc, bool vec, int epi,
+              bool vec_b) {
   const int lay = layout_of(a_kc, b_kc);
   const bool forced = c && c->force_gemm[lay] >= 0;
+  // K <= 128 with B float4-aligned: one round of loads for the whole K
+  // extent (the single 4096 x 123 -> 512 feature-major layer, whose weight
+  // rows of 123 floats are not float4-aligned).
+  if (!forced && c && c->smallk > 0 && lay == L_AK_BN && K > 0 && K <= 128 && vec_b &&
+      (epi == zk::kEpiStore || epi == zk::kEpiBiasN || epi == zk::kEpiBiasM) &&
+      (!vec || c->smallk > 1))
+    return gemm_id(c->smallk_waves == 8 ? (vec ? "zk_gemm_ak_bn_64x64xk128_w24" : "zk_gemm_ak_bn_64x64xk128_w24_s")
+                                        : (vec ? "zk_gemm_ak_bn_64x64xk128_w22" : "zk_gemm_ak_bn_64x64xk128_w22_s"));
   if (!forced && (!c || c->narrow)) {
     if (lay == L_AK_BK && N <= 32) {
       const bool v = vec && K % 16 == 0;
@@ -319,13 +332,18 @@ static zl_status plan_gemm(zl_ctx* c, const GemmDesc& d, GemmPlan& P) {
   // float4 row loads need 16-byte aligned rows that cover the padded extent.
   const int a_ext = d.a_kc ? d.K : d.M;
   const int b_ext = d.b_kc ? d.K : d.N;
-  P.vec = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4) && aligned16(d.B) &&
-          d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
-  P.kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc, P.vec, d.epi);
+  const bool va = aligned16(d.A) && d.lda % 4 == 0 && d.lda >= round_up(a_ext, 4);
+  const bool vb = aligned16(d.B) && d.ldb % 4 == 0 && d.ldb >= round_up(b_ext, 4);
+  P.vec = va && vb;
+  const bool plain = !d.rowsum_out && !d.permA && !d.permB && d.splits <= 1;
+  P.kid = pick_gemm(c, d.M, d.N, d.K, d.a_kc, d.b_kc, P.vec, d.epi, vb && plain);
   if (P.kid < 0) return fail(c, ZL_ERR_INVALID, "no GEMM variant for this layout");
   const GemmKernel& g = kGemmTable[P.kid - K_GEMM_BASE];
-  if (g.a_kc != d.a_kc || g.b_kc != d.b_kc || (g.vec && !P.vec))
+  if (g.a_kc != d.a_kc || g.b_kc != d.b_kc || (g.vec && !P.vec) || (g.need_vec_b && !(vb && plain)))
     return fail(c, ZL_ERR_INVALID, "GEMM variant %s does not match the operand layout", g.name);
+  if (strstr(g.name, "xk128") && (d.K > 128 || !plain))
+    return fail(c, ZL_ERR_INVALID, "GEMM variant %s takes K <= 128 without split-K, row sums or gathers",
+                g.name);
   if (g.kind == G_NARROW_N || g.kind == G_NARROW_K) {
     P.splits = 1;
     P.per = 0;
@@ -888,10 +906,13 @@ zl_status zl_init(int device, zl_ctx** out) {
   }
   if (const char* v = getenv("ZL_SPLITK")) c->force_splits = std::max(0, atoi(v));
   if (const char* v = getenv("ZL_SPLITK_TARGET")) c->splitk_target = std::max(1, atoi(v));
+  if (const char* v = getenv("ZL_BWD_SPLIT_DIV")) c->bwd_split_div = std::max(0, atoi(v));
   if (const char* v = getenv("ZL_NARROW")) c->narrow = atoi(v) != 0;
   if (const char* v = getenv("ZL_NARROW_TARGET")) c->narrow_target = std::max(1, atoi(v));
   if (const char* v = getenv("ZL_MERGED_BWD")) c->merged_bwd = atoi(v) != 0;
   if (const char* v = getenv("ZL_POLICY_FUSED")) c->fused_policy = atoi(v) != 0;
+  if (const char* v = getenv("ZL_SMALLK")) c->smallk = std::max(0, atoi(v));
+  if (const char* v = getenv("ZL_SMALLK_WAVES")) c->smallk_waves = atoi(v) == 8 ? 8 : 4;
   // Default-priority stream (no priority variants are used anywhere).
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -1287,12 +1308,18 @@ zl_status zl_grad_clip_scale(zl_ctx* c, const zl_tensor* tensors, int count, flo
   return launch(c, K_CLIP_SCALE, 1, 1, 1, cs, 0, 64);
 }
 
-zl_status zl_adam_multi(zl_ctx* c, const zl_adam_tensor* tensors, int count, float lr, float beta1,
-                        float beta2, float eps, float bc1, float bc2, const float* clip_scale_dev) {
-  if (!c) return ZL_ERR_INVALID;
-  if (!tensors || count < 1 || count > zk::kMaxAdamTensors)
-    return fail(c, ZL_ERR_INVALID, "zl_adam_multi: bad argument (count %d)", count);
+// zl_adam_multi (part == nullptr) or its clipped form (the scale taken in
+// every block from `nparts` sum-of-squares partials at `part`).
+static zl_status adam_multi_launch(zl_ctx* c, const zl_adam_tensor* tensors, int count, float lr,
+                                   float beta1, float beta2, float eps, float bc1, float bc2,
+                                   const float* clip_scale_dev, const float* part, int nparts,
+                                   float max_norm, float* scale_out, float* norm_out) {
   zk::AdamMultiArgs a{};
+  a.part = part;
+  a.nparts = nparts;
+  a.max_norm = max_norm;
+  a.scale_out = scale_out;
+  a.norm_out = norm_out;
   int blk = 0;
   for (int j = 0; j < count; ++j) {
     const zl_adam_tensor& t = tensors[j];
@@ -1316,6 +1343,45 @@ zl_status zl_adam_multi(zl_ctx* c, const zl_adam_tensor* tensors, int count, flo
   a.beta2 = beta2;
   a.eps = eps;
   return launch(c, K_ADAM_MULTI, (unsigned)blk, 1, 1, a);
+}
+
+zl_status zl_adam_multi(zl_ctx* c, const zl_adam_tensor* tensors, int count, float lr, float beta1,
+                        float beta2, float eps, float bc1, float bc2, const float* clip_scale_dev) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!tensors || count < 1 || count > zk::kMaxAdamTensors)
+    return fail(c, ZL_ERR_INVALID, "zl_adam_multi: bad argument (count %d)", count);
+  return adam_multi_launch(c, tensors, count, lr, beta1, beta2, eps, bc1, bc2, clip_scale_dev,
+                           nullptr, 0, 0.0f, nullptr, nullptr);
+}
+
+zl_status zl_adam_multi_clip(zl_ctx* c, const zl_adam_tensor* tensors, int count, float lr,
+                             float beta1, float beta2, float eps, float bc1, float bc2,
+                             float max_norm, float* scale_dev, float* norm_dev) {
+  if (!c) return ZL_ERR_INVALID;
+  if (!tensors || count < 1 || count > zk::kMaxAdamTensors || count > zk::kMaxNormTensors)
+    return fail(c, ZL_ERR_INVALID, "zl_adam_multi_clip: bad argument (count %d)", count);
+  // The partials of zl_grad_clip_scale over the gradients, same chunking.
+  zk::SumsqMultiArgs q{};
+  const int chunk = 2048;
+  int blk = 0;
+  for (int j = 0; j < count; ++j) {
+    const zl_adam_tensor& t = tensors[j];
+    if (t.n && (!t.p || !t.g || !t.m || !t.v))
+      return fail(c, ZL_ERR_INVALID, "zl_adam_multi_clip: tensor %d has a NULL pointer", j);
+    q.x[j] = t.g;
+    q.n[j] = (long long)t.n;
+    q.blk0[j] = blk;
+    blk += (int)std::max<long long>(1, cdiv((long long)t.n, chunk));
+  }
+  q.blk0[count] = blk;
+  q.count = count;
+  q.chunk = chunk;
+  zl_status s = ensure_ws(c, (size_t)blk);
+  if (s) return s;
+  q.part = c->ws;
+  if ((s = launch(c, K_SUMSQ_MULTI, (unsigned)blk, 1, 1, q))) return s;
+  return adam_multi_launch(c, tensors, count, lr, beta1, beta2, eps, bc1, bc2, nullptr, c->ws, blk,
+                           max_norm, scale_dev, norm_dev);
 }
 
 zl_status zl_gae(zl_ctx* c, const float* rewards, const float* values, const uint8_t* dones,

@@ -88,6 +88,17 @@ def adam_multi(ctx: Context, tensors, lr, bc1, bc2, clip_scale=None, beta1=0.9, 
               "zl_adam_multi")
 
 
+def adam_multi_clip(ctx: Context, tensors, lr, bc1, bc2, max_norm, scale_out=None, norm_out=None,
+                    beta1=0.9, beta2=0.999, eps=1e-8):
+    """Global grad-norm clip + Adam over [(p, g, m, v, n), ...] in two launches."""
+    arr = (_ffi.zl_adam_tensor * len(tensors))(
+        *[_ffi.zl_adam_tensor(_ptr(p), _ptr(g), _ptr(m), _ptr(v), int(n)) for p, g, m, v, n in tensors])
+    ctx.check(ctx.lib.zl_adam_multi_clip(ctx.h, arr, len(tensors), lr, beta1, beta2, eps, bc1, bc2, max_norm,
+                                         _ptr(scale_out) if scale_out is not None else None,
+                                         _ptr(norm_out) if norm_out is not None else None),
+              "zl_adam_multi_clip")
+
+
 def gae(ctx: Context, rewards, values, dones, last_values, T, N, adv, ret, gamma=0.99, lam=0.95,
         in_strides=None, out_strides=None):
     """GAE over N envs x T steps; default layout [T x N] (time-major) in and out."""
