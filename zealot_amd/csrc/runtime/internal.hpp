@@ -172,7 +172,7 @@ struct zl_ctx {
   // bias epilogue on the small-K variants (ZL_SMALLK: 0 off, 1 when A rows
   // are not float4-aligned (default), 2 always).
   int smallk = 1;
-  int smallk_waves = 4;  // wavefronts per small-K block (ZL_SMALLK_WAVES: 4 or 8)
+  int smallk_waves = 8;  // wavefronts per small-K block (ZL_SMALLK_WAVES: 4 or 8; 8 measured 12.8 vs 13.3 us)
   // Device address of the allocation-free scratch array on this context's
   // device (zl_grad_clip_scale_noalloc), set at zl_init.
   float* noalloc_scratch = nullptr;  // this context's slot of the array
