@@ -44,8 +44,8 @@ HBM_PEAK = 8.0e12  # bytes/s
 # averaged over an update's launch mix; reported as roofline.traffic for the
 # dominant kernel when it is one of these.
 MEASURED_TRAFFIC = {
-    "zk_gemm_bwd_128x128_dg128_x": 457.1e6,
-    "zk_gemm_ak_bk_128x128x32_w24_x": 150.2e6,
+    "zk_gemm_bwd_128x128_dg128_x": 441.1e6,
+    "zk_gemm_ak_bk_128x128x32_w24_x": 150.3e6,
 }
 
 
