@@ -386,7 +386,7 @@ struct SampleArgs {
 // of 16 within the layer-0 weight rows, and the output width at most 32
 // (the host checks).
 constexpr int kPolicyRows = 16;
-constexpr int kPolicyThreads = 512;
+constexpr int kPolicyThreads = 1024;  // 16 wavefronts: at most two 16-column tiles each
 constexpr int kPolicyMaxWidth = 512;
 constexpr int kPolicyMaxLayers = 8;
 struct PolicyNet {
