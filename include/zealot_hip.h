@@ -439,7 +439,10 @@ zl_status zl_ppo_get_grads(zl_ppo* ppo, float* actor, float* critic, float* log_
  * layer GEMMs in minibatch-sized chunks with separate normalise and sampling
  * launches. The environment variable ZL_POLICY_FUSED=0 (read at zl_init)
  * turns the single-launch form off; zl_ppo_values and zl_ppo_actor_mean
- * follow the same rule per net. */
+ * follow the same rule per net. The single launch reads the weights from a
+ * second, fragment-major copy held by the handle (about the size of the
+ * weights), which zl_ppo_create, zl_ppo_set_params, zl_ppo_load* and every
+ * zl_ppo_update rewrite on the stream after changing the parameters. */
 zl_status zl_ppo_act(zl_ppo* ppo, const float* obs_norm, const float* obs, int ld_obs,
                      const float* critic_norm, const float* critic_obs, int ld_critic_obs,
                      long long n, const float* eps, float* action, float* logp, float* mean,

@@ -173,3 +173,66 @@ def test_fused_policy_step_matches_layer_launches(ctx, n, ad, cd):
     for name, x, y in zip(names, out[0], out[1]):
         assert np.array_equal(x, y), name
     print(f"[gpu] fused policy step n={n} actor {ad}: bit-identical to the layer launches", flush=True)
+
+
+def test_policy_weights_follow_parameter_changes(ctx):
+    """zk_policy reads a fragment-major copy of the weights that the handle
+    rewrites after every parameter change (zk_policy_pack). After
+    set_params, after each of two updates (the second replays the captured
+    graph), after an update that early-stops in its first epoch and after a
+    checkpoint loaded into the same handle, the rollout step, zl_ppo_values
+    and zl_ppo_actor_mean equal the layer launches (ZL_POLICY_FUSED=0, a
+    context of its own) on the same parameters, bit for bit."""
+    from test_gpu_ppo import SMALL_A, SMALL_C, _small_problem
+    from zealot_amd.rl import DeviceBatch, PpoConfig
+
+    actor, critic, log_std, batch = _small_problem(71, n=4096)
+    os.environ["ZL_POLICY_FUSED"] = "0"
+    try:
+        cref = Context(0)
+    finally:
+        os.environ.pop("ZL_POLICY_FUSED", None)
+    gac = GpuActorCritic(ctx, SMALL_A, SMALL_C, 1024)
+    ref = GpuActorCritic(cref, SMALL_A, SMALL_C, 1024)
+    n, A = 1000, SMALL_A[-1]
+    g = np.random.default_rng(72)
+    obs = g.standard_normal((n, SMALL_A[0])).astype(np.float32)
+    cobs = g.standard_normal((n, SMALL_C[0])).astype(np.float32)
+    eps = g.standard_normal((n, A)).astype(np.float32)
+
+    def step(h, cx):
+        d_obs, d_cobs, d_eps = cx.to_device(obs), cx.to_device(cobs), cx.to_device(eps)
+        d_act, d_lp, d_mean, d_val = cx.alloc((n, A)), cx.alloc(n), cx.alloc((n, A)), cx.alloc(n)
+        h.act(d_obs, n, d_eps, d_act, d_lp, mean=d_mean, value=d_val, critic_obs=d_cobs)
+        pv, pm = cx.alloc(n), cx.alloc((n, A))
+        h.values(d_cobs, n, pv)
+        h.actor_mean(d_obs, n, pm)
+        return [x.numpy() for x in (d_act, d_lp, d_mean, d_val, pv, pm)]
+
+    def check(tag):
+        a, c, l, lr = gac.get_params()
+        ref.set_params(a, c, l, lr)
+        got, want = step(gac, ctx), step(ref, cref)
+        for name, x, y in zip(["action", "logp", "mean", "value", "values", "actor mean"], got, want):
+            assert np.array_equal(x, y), (tag, name)
+        print(f"[gpu] policy copy current after {tag}", flush=True)
+
+    gac.set_params(actor, critic, log_std, 1e-3)
+    check("set_params")
+    db = DeviceBatch(ctx, batch["obs"], batch["critic_obs"], batch["action"], batch["mean_old"],
+                     batch["logp_old"], batch["value_old"], batch["adv"], batch["ret"])
+    cfg = PpoConfig(epochs=2, minibatches=4)
+    for i in range(2):
+        gac.update(db, cfg)
+        check(f"update {i + 1}")
+    assert gac.graph_info()[0] == 1
+    st = gac.update(db, PpoConfig.gpu_trainer(epochs=3, minibatches=4, desired_kl=1e-12))
+    assert st.epochs_run == 1
+    check("an early-stopped update")
+    other = GpuActorCritic(ctx, SMALL_A, SMALL_C, 1024)
+    other.set_params(actor * np.float32(0.5), critic, log_std - np.float32(0.25), 2e-3)
+    gac.load_into(other.save_bytes())
+    check("a checkpoint load")
+    for h in (other, gac, ref):
+        h.close()
+    cref.close()

@@ -3,7 +3,9 @@
 // trainer's sampling (src/bin/biped_train_gpu.rs:910-930). At a rollout's
 // few thousand rows the per-layer GEMM launches are latency-bound; here a
 // block takes kPolicyRows rows through every layer with the activations in
-// LDS, reading each layer's weights from L2.
+// LDS, reading each layer's weights from L2 in the fragment-major copy that
+// zk_policy_pack writes (a wavefront's load of one tile's 16-wide chunk is
+// 1 KB of consecutive floats instead of 64 bytes of each of 16 weight rows).
 //
 // Every value is computed as on the multi-launch path: the normalisation is
 // Normalizer::normalize's expression (ppo.rs:198-205), each layer sums its
@@ -60,7 +62,7 @@ __device__ void policy_body(const PolicyArgs& p) {
     const int K = l == 0 ? k0w : q.dims[l];
     const int N = q.dims[l + 1];
     const bool last = l == q.L - 1;
-    const float* W = p.params + q.w_off[l];
+    const float* Wp = q.wp + q.wp_off[l];
     const float* bias = p.params + q.b_off[l];
     const float* src = act[cur];
     float* dst = act[cur ^ 1];
@@ -76,12 +78,14 @@ __device__ void policy_body(const PolicyArgs& p) {
       return s >= nt ? s - nt : s;
     };
     floatx4 acc[kPolicyMaxTiles];
-    int woff[kPolicyMaxTiles];  // 32-bit offsets from the uniform W
+    // 32-bit offsets from the uniform Wp: tile T's chunk c is the 256 floats
+    // at (T * kc + c) * 256, this lane's float4 at 4 * lane within them.
+    const int kc = K / 16;
+    int toff[kPolicyMaxTiles];
 #pragma unroll
     for (int u = 0; u < kPolicyMaxTiles; ++u) {
       acc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const int n = min(16 * tile_of(u) + lr, N - 1);
-      woff[u] = n * q.ldw[l];
+      toff[u] = tile_of(u) * kc * 256 + 4 * lane;
     }
     if (wave < nt) {  // uniform over the wavefront
       for (int kp = 0; kp < K; kp += 16 * kPolicyPass) {
@@ -93,8 +97,9 @@ __device__ void policy_body(const PolicyArgs& p) {
           av[j] = in ? *reinterpret_cast<const float4*>(src + lr * kPolicyPitch + k) : float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int u = 0; u < kPolicyMaxTiles; ++u)
-            bv[j][u] = in && wave + kPolicyWaves * u < nt ? *reinterpret_cast<const float4*>(W + (woff[u] + k))
-                                                          : float4{0.f, 0.f, 0.f, 0.f};
+            bv[j][u] = in && wave + kPolicyWaves * u < nt
+                           ? *reinterpret_cast<const float4*>(Wp + (toff[u] + 16 * (kp + 16 * j)))
+                           : float4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int j = 0; j < kPolicyPass; ++j) {
@@ -155,13 +160,50 @@ __device__ void policy_body(const PolicyArgs& p) {
   }
 }
 
+// One float4 of the packed weights per thread (the layout is described with
+// PolicyPackArgs). The segment is found by comparing against every
+// segment's start with constant indices, so the arguments stay in scalar
+// registers.
+__device__ void policy_pack_body(const PolicyPackArgs& a) {
+  const long long i = (long long)blockIdx.x * kThreads + threadIdx.x;
+  if (i >= a.nq) return;
+  long long src = 0, dst = 0, q0 = 0;
+  int ldw = 0, N = 0, K = 0, kc = 1;
+#pragma unroll
+  for (int s = 0; s < kPolicyPackSegs; ++s)
+    if (s < a.nseg && i >= a.seg[s].q0) {
+      src = a.seg[s].src;
+      dst = a.seg[s].dst;
+      q0 = a.seg[s].q0;
+      ldw = a.seg[s].ldw;
+      N = a.seg[s].N;
+      K = a.seg[s].K;
+      kc = a.seg[s].kc;
+    }
+  const long long j = i - q0;
+  const int lane = (int)(j & 63);
+  const long long b = j >> 6;
+  const int n = 16 * (int)(b / kc) + (lane & 15);
+  const int k = 16 * (int)(b % kc) + 4 * (lane >> 4);
+  float4 v = {0.f, 0.f, 0.f, 0.f};
+  if (n < N && k < K) {
+    // k < K <= ldw with k and ldw multiples of 4: the float4 stays in the row.
+    v = *reinterpret_cast<const float4*>(a.params + src + (long long)n * ldw + k);
+    if (k + 1 >= K) v.y = 0.f;
+    if (k + 2 >= K) v.z = 0.f;
+    if (k + 3 >= K) v.w = 0.f;
+  }
+  *reinterpret_cast<float4*>(a.dst + dst + 4 * j) = v;
+}
+
 }  // namespace zk
 
-// Held to eight waves per SIMD (two 16-wave blocks per CU, at most 64 VGPRs):
-// sixteen wavefronts per block keep more weight-row loads in flight than
-// eight (actor step 39.5 -> 37.4 us, bit-identical: every tile is still summed
-// by one wavefront in chunk order).
+// Held to eight waves per SIMD (two 16-wave blocks per CU, at most 64 VGPRs).
 extern "C" __global__ __launch_bounds__(zk::kPolicyThreads) __attribute__((amdgpu_waves_per_eu(8)))
 void zk_policy(zk::PolicyArgs p) {
   zk::policy_body(p);
+}
+
+extern "C" __global__ __launch_bounds__(zk::kThreads) void zk_policy_pack(zk::PolicyPackArgs a) {
+  zk::policy_pack_body(a);
 }

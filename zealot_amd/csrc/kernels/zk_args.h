@@ -393,10 +393,31 @@ struct PolicyNet {
   const float* x;     // [rows x ldx] inputs (raw, or already normalised)
   const float* norm;  // Normalizer state [2 * dims[0] + 1], nullable
   float* out;         // [rows x ldo] the last layer's output, nullable
-  long long w_off[kPolicyMaxLayers], b_off[kPolicyMaxLayers];
-  int ldw[kPolicyMaxLayers];
+  const float* wp;    // the net's weights in the zk_policy_pack layout; layer l at wp + wp_off[l]
+  long long wp_off[kPolicyMaxLayers], b_off[kPolicyMaxLayers];
   int dims[kPolicyMaxLayers + 1];
   int L, ldx, ldo;
+};
+// zk_policy_pack: the weights zk_policy reads, rewritten from the flat
+// parameter rows ([N x ldw] per layer) so that one wavefront's load of a
+// 16-column tile's 16-wide reduction chunk is 1 KB of consecutive floats:
+// per tile T and chunk c, 256 floats in which lane L's float4 is
+// W[16 T + L % 16][16 c + 4 (L / 16) .. + 3], zero past N rows and K columns
+// (K the layer's input width; kc = ceil(K / 16) chunks). One segment per
+// (net, layer); segment s covers float4 indices [q0, next q0) of the output.
+constexpr int kPolicyPackSegs = 2 * kPolicyMaxLayers;
+struct PolicyPackSeg {
+  long long src;  // the layer's weight rows in params
+  long long dst;  // its packed block in dst
+  long long q0;   // first float4 index of the segment
+  int ldw, N, K, kc;
+};
+struct PolicyPackArgs {
+  const float* params;
+  float* dst;
+  PolicyPackSeg seg[kPolicyPackSegs];
+  int nseg;
+  long long nq;  // float4 outputs over all segments
 };
 struct PolicyArgs {
   PolicyNet net[2];

@@ -53,6 +53,7 @@ enum KernelId : int {
   K_HEAD_FWD_X,
   K_POLICY,
   K_TRANSPOSE,
+  K_POLICY_PACK,
   K_GEMM_BASE
 };
 

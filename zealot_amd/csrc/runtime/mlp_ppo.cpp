@@ -676,6 +676,15 @@ struct zl_ppo {
   // Bumped whenever a device buffer of this handle is reallocated: a captured
   // graph is only replayed while every buffer it references is still alive.
   unsigned long long gen = 0;
+  // zk_policy's fragment-major copy of the weights of each net that fits it
+  // (zk_policy_pack), rewritten after every change of the parameters
+  // (zl_ppo_create, zl_ppo_set_params and so zl_ppo_load, the end of every
+  // update, eager or captured), so that it matches them at every point of
+  // the stream where a call that reads it runs.
+  float* polw = nullptr;
+  long long polw_off[2][zk::kPolicyMaxLayers] = {};
+  bool polw_net[2] = {false, false};
+  zk::PolicyPackArgs pack{};
   // Captured update graph and the signature it was captured for.
   hipGraphExec_t gexec = nullptr;
   std::string gkey;
@@ -684,6 +693,63 @@ struct zl_ppo {
 };
 
 namespace {
+
+// zk_policy: below this many rows a forward runs as one launch (each block
+// reads every weight once from L2, so the weight traffic grows with the row
+// blocks; the layer GEMMs take larger batches).
+constexpr long long kPolicyFusedRows = 8192;
+
+// Whether a net fits zk_policy: at most kPolicyMaxLayers layers, hidden widths
+// multiples of 16 up to kPolicyMaxWidth, input width up to kPolicyMaxWidth
+// with its 16-padded width inside the layer-0 weight rows, at most 32 outputs,
+// 16-byte aligned weight rows.
+static bool policy_fits(const zl_ppo* p, const NetLayout& nl) {
+  if (nl.L < 1 || nl.L > zk::kPolicyMaxLayers || nl.dims[0] > zk::kPolicyMaxWidth ||
+      nl.dims[nl.L] > 32 || nl.ldw[0] < round_up(nl.dims[0], 16))
+    return false;
+  for (int l = 1; l < nl.L; ++l)
+    if (nl.dims[l] % 16 != 0 || nl.dims[l] > zk::kPolicyMaxWidth) return false;
+  for (int l = 0; l < nl.L; ++l)
+    if (nl.w_off[l] % 4 != 0 || nl.ldw[l] % 4 != 0) return false;
+  return ((uintptr_t)p->params & 15) == 0;
+}
+
+// zk_policy_pack's segments for the nets that fit zk_policy and the size of
+// their packed copy in floats: per layer, ceil(N / 16) tiles x ceil(K / 16)
+// chunks x 256 floats (K the layer's input width).
+static long long policy_layout(zl_ppo* p) {
+  zk::PolicyPackArgs& a = p->pack;
+  a = zk::PolicyPackArgs{};
+  long long floats = 0;
+  for (int net = 0; net < 2; ++net) {
+    const NetLayout& nl = net ? p->critic : p->actor;
+    p->polw_net[net] = policy_fits(p, nl);
+    if (!p->polw_net[net]) continue;
+    for (int l = 0; l < nl.L; ++l) {
+      zk::PolicyPackSeg& g = a.seg[a.nseg++];
+      g.src = nl.w_off[l];
+      g.dst = floats;
+      g.q0 = floats / 4;
+      g.ldw = nl.ldw[l];
+      g.N = nl.dims[l + 1];
+      g.K = nl.dims[l];
+      g.kc = (int)cdiv(nl.dims[l], 16);
+      p->polw_off[net][l] = floats;
+      floats += cdiv(g.N, 16) * g.kc * 256;
+    }
+  }
+  a.nq = floats / 4;
+  return floats;
+}
+
+// Rewrite zk_policy's copy of the weights from the parameters (stream-ordered
+// after whatever wrote them).
+static zl_status policy_pack(zl_ppo* p) {
+  if (p->pack.nseg == 0) return ZL_OK;
+  p->pack.params = p->params;
+  p->pack.dst = p->polw;
+  return launch(p->c, K_POLICY_PACK, (unsigned)cdiv(p->pack.nq, kThreads), 1, 1, p->pack);
+}
 
 // Grow a device buffer of the handle (outside graph capture: may synchronize).
 // A reallocation bumps the handle's buffer generation, which is part of the
@@ -1214,7 +1280,9 @@ zl_status enqueue_update(zl_ppo* p, const zl_ppo_config* cfg, const Plan& pl) {
     cl.hi = 0.0f;
     if ((s = launch(c, K_CLAMP, 1, 1, 1, cl))) return s;
   }
-  return ZL_OK;
+  // The rollout step's copy of the updated weights (unguarded: it runs after
+  // an early stop too).
+  return policy_pack(p);
 }
 
 }  // namespace
@@ -1285,6 +1353,11 @@ zl_status zl_ppo_create(zl_ctx* c, const int* adims, int na, const int* cdims, i
   if (!s) p->bptrs = (zk::BatchPtrs*)((char*)p->dstate + offsetof(UpdateIn, ptrs));
   dalloc((void**)&p->ls_old, (size_t)p->A * 4);
   dalloc((void**)&p->stat_out, 8 * 4);
+  if (!s) {
+    const long long pw = policy_layout(p);
+    if (pw > 0) dalloc((void**)&p->polw, (size_t)pw * 4);
+    if (!s) s = policy_pack(p);
+  }
   if (!s && hipStreamSynchronize(c->stream) != hipSuccess)
     s = fail(c, ZL_ERR_HIP, "zl_ppo_create: stream sync failed");
   if (s) {
@@ -1307,7 +1380,7 @@ void zl_ppo_destroy(zl_ppo* p) {
                   (void*)p->gls_part, (void*)p->astat_part, (void*)p->vstat_part,
                   (void*)p->kl_part, (void*)p->sq_part, (void*)p->adv_part, (void*)p->dstate,
                   (void*)p->ls_old, (void*)p->obs_pad, (void*)p->cobs_pad, (void*)p->perm,
-                  (void*)p->stat_out, (void*)p->pws})
+                  (void*)p->stat_out, (void*)p->pws, (void*)p->polw})
     if (b) hipFree(b);
   for (float* b : p->stg)
     if (b) hipFree(b);
@@ -1327,6 +1400,8 @@ zl_status zl_ppo_set_params(zl_ppo* p, const float* actor, const float* critic,
   if (critic) p->critic.scatter(critic, host.data());
   if (log_std) std::memcpy(host.data() + p->ls_off, log_std, (size_t)p->A * 4);
   ZL_HIP(c, hipMemcpyAsync(p->params, host.data(), host.size() * 4, hipMemcpyHostToDevice, c->stream));
+  zl_status s = policy_pack(p);
+  if (s) return s;
   ZL_HIP(c, hipStreamSynchronize(c->stream));
   p->hstate.lr = lr;
   return ZL_OK;
@@ -1621,29 +1696,11 @@ zl_status zl_ppo_minibatch_grads(zl_ppo* p, const zl_batch* b, const zl_ppo_conf
   return ZL_OK;
 }
 
-// zk_policy: below this many rows a forward runs as one launch (each block
-// reads every weight once from L2, so the weight traffic grows with the row
-// blocks; the layer GEMMs take larger batches).
-constexpr long long kPolicyFusedRows = 8192;
-
-// Whether a net fits zk_policy: at most kPolicyMaxLayers layers, hidden widths
-// multiples of 16 up to kPolicyMaxWidth, input width up to kPolicyMaxWidth
-// with its 16-padded width inside the layer-0 weight rows, at most 32 outputs,
-// 16-byte aligned weight rows.
-static bool policy_fits(const zl_ppo* p, const NetLayout& nl) {
-  if (nl.L < 1 || nl.L > zk::kPolicyMaxLayers || nl.dims[0] > zk::kPolicyMaxWidth ||
-      nl.dims[nl.L] > 32 || nl.ldw[0] < round_up(nl.dims[0], 16))
-    return false;
-  for (int l = 1; l < nl.L; ++l)
-    if (nl.dims[l] % 16 != 0 || nl.dims[l] > zk::kPolicyMaxWidth) return false;
-  for (int l = 0; l < nl.L; ++l)
-    if (nl.w_off[l] % 4 != 0 || nl.ldw[l] % 4 != 0) return false;
-  return ((uintptr_t)p->params & 15) == 0;
-}
-
-static void policy_net(zk::PolicyNet& q, const NetLayout& nl, const float* x, int ldx,
+static void policy_net(zk::PolicyNet& q, const zl_ppo* p, int net, const float* x, int ldx,
                        const float* norm, float* out, int ldo) {
+  const NetLayout& nl = net ? p->critic : p->actor;
   q = zk::PolicyNet{};
+  q.wp = p->polw;
   q.x = x;
   q.ldx = ldx;
   q.norm = norm;
@@ -1652,9 +1709,8 @@ static void policy_net(zk::PolicyNet& q, const NetLayout& nl, const float* x, in
   q.L = nl.L;
   for (int l = 0; l <= nl.L; ++l) q.dims[l] = nl.dims[l];
   for (int l = 0; l < nl.L; ++l) {
-    q.w_off[l] = nl.w_off[l];
+    q.wp_off[l] = p->polw_off[net][l];
     q.b_off[l] = nl.b_off[l];
-    q.ldw[l] = nl.ldw[l];
   }
 }
 
@@ -1665,9 +1721,9 @@ static zl_status chunked_forward(zl_ppo* p, bool critic, const float* x, int ld,
   const NetBuffers& nb = critic ? p->cb : p->ab;
   if (!x || !out || n < 0 || ld < nl.dims[0] || ld_out < cols)
     return fail(c, ZL_ERR_INVALID, "forward: bad argument");
-  if (n > 0 && n <= kPolicyFusedRows && c->fused_policy && policy_fits(p, nl)) {
+  if (n > 0 && n <= kPolicyFusedRows && c->fused_policy && p->polw_net[critic ? 1 : 0]) {
     zk::PolicyArgs a{};
-    policy_net(a.net[0], nl, x, ld, nullptr, out, ld_out);
+    policy_net(a.net[0], p, critic ? 1 : 0, x, ld, nullptr, out, ld_out);
     a.params = p->params;
     a.rows = n;
     return launch(c, K_POLICY, (unsigned)cdiv(n, zk::kPolicyRows), 1, 1, a, 0, zk::kPolicyThreads);
@@ -1724,12 +1780,12 @@ zl_status zl_ppo_act(zl_ppo* p, const float* obs_norm, const float* obs, int ld_
       (value && (!cobs || ld_cobs < cd)) || (!value && critic_norm))
     return fail(c, ZL_ERR_INVALID, "zl_ppo_act: bad argument");
   if (n == 0) return ZL_OK;
-  if (n <= kPolicyFusedRows && c->fused_policy && A <= 32 && policy_fits(p, p->actor) &&
-      (!value || policy_fits(p, p->critic))) {
+  if (n <= kPolicyFusedRows && c->fused_policy && A <= 32 && p->polw_net[0] &&
+      (!value || p->polw_net[1])) {
     // One launch: normalise, both nets' layers, sampling (zk_policy).
     zk::PolicyArgs a{};
-    policy_net(a.net[0], p->actor, obs, ld_obs, obs_norm, mean, ld_mean);
-    if (value) policy_net(a.net[1], p->critic, cobs, ld_cobs, critic_norm, value, 1);
+    policy_net(a.net[0], p, 0, obs, ld_obs, obs_norm, mean, ld_mean);
+    if (value) policy_net(a.net[1], p, 1, cobs, ld_cobs, critic_norm, value, 1);
     a.params = p->params;
     a.log_std = p->params + p->ls_off;
     a.eps = eps;

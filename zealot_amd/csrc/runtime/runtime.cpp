@@ -24,7 +24,7 @@ const char* const kFixedNames[K_GEMM_BASE] = {
     "zk_norm_stats",    "zk_norm_merge",  "zk_norm_commit", "zk_sample_g32",  "zk_sample_g64",
     "zk_stage",         "zk_sumsq_multi", "zk_clip_scale",  "zk_adam_multi",
     "zk_gemm_bwd_128x128_dg_x", "zk_gemm_bwd_64x128_dg_x", "zk_gemm_bwd_128x128_dg128_x", "zk_gemm_bwd_64x128_dg128_x", "zk_head_fwd", "zk_head_fwd_x",
-    "zk_policy",        "zk_transpose",
+    "zk_policy",        "zk_transpose",   "zk_policy_pack",
 };
 
 // {name, A K-contiguous, B K-contiguous, BM, BN, BK, threads, float4 loads, family}
