@@ -120,14 +120,17 @@ TRAINER_A, TRAINER_C = [265, 256, 256, 128, 12], [64, 512, 256, 128, 1]
                                      (17, synth.ACTOR_DIMS, [64, 512, 256, 128, 1]),
                                      (1, synth.ACTOR_DIMS, [64, 512, 256, 128, 1]),
                                      (4096, TRAINER_A, TRAINER_C),
-                                     (777, [64, 128, 64, 9], [48, 96, 48, 1])])
+                                     (777, [64, 128, 64, 9], [48, 96, 48, 1]),
+                                     (300, [64, 128, 64, 9], [48, 100, 1])])
 def test_fused_policy_step_matches_layer_launches(ctx, n, ad, cd):
     """zk_policy (normalise, every layer of both nets and the sampling in one
     launch, 16 rows per block) against the layer-GEMM launches
     (ZL_POLICY_FUSED=0, read when a context is created: that run gets a
     context of its own), on the headline nets, the reference trainer's nets
-    (a 265-wide input, 16-padded inside its 288-wide weight rows) and narrow
-    ones. Both add every reduction in the same order, so actions,
+    (a 265-wide input, 16-padded inside its 288-wide weight rows), narrow
+    ones, and a critic whose 100-wide hidden layer does not fit the single
+    launch (only the actor has a packed weight copy; steps with the value
+    take the layer launches for both nets). Both add every reduction in the same order, so actions,
     log-probabilities, means and values are bit-identical; so are the plain
     forwards of zl_ppo_values and zl_ppo_actor_mean at these sizes."""
     g = np.random.default_rng(40 + n + ad[0])
