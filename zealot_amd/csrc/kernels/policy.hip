@@ -69,9 +69,8 @@ __device__ void policy_body(const PolicyArgs& p) {
     const int nt = (N + 15) / 16;
     // This wave's 16-column tiles: slots wave, wave + kPolicyWaves, ... < nt,
     // slot s on tile (s + rot) % nt, rotated per block so that concurrent
-    // blocks read different weight rows (measured within 1 % of no rotation;
-    // the step is bound by the latency of its weight loads, one round per
-    // kPolicyPass chunks).
+    // blocks read different weight tiles (measured within 1 % of no
+    // rotation). The weight loads go out one round per kPolicyPass chunks.
     const int rot = (int)(blockIdx.x % (unsigned)nt);
     auto tile_of = [&](int u) {
       const int s = wave + kPolicyWaves * u + rot;
